@@ -1,0 +1,208 @@
+/*
+ * taraference_hip.h -- C ABI of the MI355X (gfx950) batch-1 decode hot path.
+ *
+ * Drop-in replacement for the launch layer behind taraference's Rust
+ * operator API (agkomyint/taraference v0.5.3, crates/core/src/cuda/).  Each
+ * entry point replaces one NVRTC kernel symbol that the Rust side binds in
+ * types.rs:302-475 and launches from matmul.rs / layer.rs.  It keeps that
+ * kernel's argument list and meaning, appends the stream, and chooses the
+ * launch geometry internally.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers owned by the caller.  The library does
+ *     not allocate device memory.  The one exception is the one-time
+ *     hipModule-free kernel registration done by the HIP runtime itself.
+ *   - Weights use the reference layout.  n_rows = K is the input length and
+ *     n_cols = N is the number of outputs.  Output column j occupies
+ *     col_bytes bytes at w + j*col_bytes and holds floor(n_rows/256)
+ *     super-blocks: Q4_K blocks are 144 B and must be 16-byte aligned;
+ *     compact Q6_K blocks are 212 B (cuda/load.rs:145-159) and raw Q6_K
+ *     blocks are 210 B.  As in the reference, a K tail that is not a whole
+ *     super-block is ignored (kernels/gemv.cu:397,484).
+ *   - The Q8 activation is int8 q8[K] plus f32 d8[K/32]
+ *     (kernels/gemv.cu:43-65).
+ *   - use_res selects the residual: 0 = none, 1 = out[j] = acc + residual[j],
+ *     2 = out[j] += acc in place.  The bias is added after the residual
+ *     (kernels/gemv.cu:367-373).
+ *   - The return value is a hipError_t: 0 on success, hipErrorInvalidValue
+ *     (1) for a shape or pointer that the kernel cannot serve, or the launch
+ *     error.  Launches are asynchronous on `stream` (a hipStream_t; NULL is
+ *     the default stream).
+ */
+#ifndef TARAFERENCE_HIP_H
+#define TARAFERENCE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *tf_stream_t; /* hipStream_t */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tf_version(void);
+
+/* Number of entries in tf_exported_symbols(). */
+int tf_exported_symbol_count(void);
+/* Name of the i-th C-ABI entry point (used by tests that check exports). */
+const char *tf_exported_symbol(int i);
+
+/* ------------------------------------------------------------ Q8 quantize */
+
+/* kernels/gemv.cu:43 quantize_q8_global; host cuda/matmul.rs:47
+ * quantize_q8.  x f32[n_rows] -> q8 int8[n_rows], d8 f32[n_rows/32].
+ * n_rows % 32 == 0. */
+int tf_quantize_q8(const float *x, int8_t *q8, float *d8, int n_rows,
+                   tf_stream_t stream);
+
+/* ------------------------------------------------------- Q4_K x Q8 GEMVs */
+
+/* kernels/gemv.cu:469 gemv_q4_k_global (matmul.rs:142-302 single pass):
+ * out[j] = dot(Q4_K column j, Q8 x) [+res] [+bias]. */
+int tf_gemv_q4k_q8(const uint8_t *w, const int8_t *xq, const float *xd,
+                   float *out, int n_rows, int n_cols, int col_bytes,
+                   int use_bias, const float *bias, int use_res,
+                   const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:1877 gemv_q4_k_global_splitk (matmul.rs:225-283):
+ * partial[s*n_cols + j] = dot over super-blocks
+ * [floor(nb*s/n_split), floor(nb*(s+1)/n_split)). 1 <= n_split <= 8. */
+int tf_gemv_q4k_q8_splitk(const uint8_t *w, const int8_t *xq,
+                          const float *xd, float *partial, int n_rows,
+                          int n_cols, int col_bytes, int n_split,
+                          tf_stream_t stream);
+
+/* kernels/gemv.cu:2243 gemv_splitk_reduce: out[j] = sum_s partial[s][j]
+ * [+res] [+bias]. */
+int tf_gemv_splitk_reduce(const float *partial, float *out, int n_cols,
+                          int n_split, int use_bias, const float *bias,
+                          int use_res, const float *residual,
+                          tf_stream_t stream);
+
+/* kernels/gemv.cu:2346 gemv_q4_k_pair (matmul.rs:727-784 try_gemv_q4_pair):
+ * out_a = W_a x (+ba), out_b = W_b x (+bb), one launch, shared Q8 x. */
+int tf_gemv_q4k_pair(const uint8_t *wa, const uint8_t *wb, const int8_t *xq,
+                     const float *xd, float *out_a, float *out_b, int n_rows,
+                     int n_a, int n_b, int col_bytes, int use_bias,
+                     const float *ba, const float *bb, tf_stream_t stream);
+
+/* kernels/gemv.cu:2401 gemv_q4_k_dual (matmul.rs:582-624 try_gemv_q4_dual):
+ * equal-width pair without bias. */
+int tf_gemv_q4k_dual(const uint8_t *wa, const uint8_t *wb, const int8_t *xq,
+                     const float *xd, float *out_a, float *out_b, int n_rows,
+                     int n_cols, int col_bytes, tf_stream_t stream);
+
+/* kernels/gemv.cu:2440 gemv_q4_k_ffn (and _4way :2510, _8way :2578):
+ * out[j] = silu(gate_j . x) * (up_j . x) with x pre-quantized. */
+int tf_gemv_q4k_ffn(const uint8_t *gate, const uint8_t *up, const int8_t *xq,
+                    const float *xd, float *out, int n_rows, int n_cols,
+                    int col_bytes, tf_stream_t stream);
+
+/* kernels/gemv.cu:2546 gemv_q4_k_ffn_mcol (matmul.rs:680-697): as
+ * tf_gemv_q4k_ffn but x is f32 and is quantized to Q8 inside every
+ * workgroup (in LDS), bit-identically to tf_quantize_q8. */
+int tf_gemv_q4k_ffn_f32(const uint8_t *gate, const uint8_t *up,
+                        const float *x, float *out, int n_rows, int n_cols,
+                        int col_bytes, tf_stream_t stream);
+
+/* kernels/gemv.cu:2662 gemv_q4_k_qkv (matmul.rs:962-1002 try_gemv_qkv):
+ * Q, K and V projections in one launch; all three Q4_K with the same K. */
+int tf_gemv_q4k_qkv(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
+                    const int8_t *xq, const float *xd, float *q, float *k,
+                    float *v, int n_rows, int n_q, int n_k, int n_v,
+                    int col_bytes, int use_bias, const float *bq,
+                    const float *bk, const float *bv, tf_stream_t stream);
+
+/* ------------------------------------------------------- Q6_K GEMVs */
+
+/* kernels/gemv.cu:515 gemv_q6_k_compact_global (matmul.rs:165-169,285-300):
+ * compact 212-byte Q6_K blocks x Q8 (the lm_head path). */
+int tf_gemv_q6k_compact_q8(const uint8_t *w, const int8_t *xq,
+                           const float *xd, float *out, int n_rows,
+                           int n_cols, int col_bytes, int use_bias,
+                           const float *bias, int use_res,
+                           const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:2081 gemv_q6_k_compact_global_8way and :2025 _4way
+ * (matmul.rs:196-223): the tall Q6_K ffn_down.  The in-block split-K merge
+ * and the residual/bias epilogue are fused; no partial buffer. */
+int tf_gemv_q6k_down_splitk(const uint8_t *w, const int8_t *xq,
+                            const float *xd, float *out, int n_rows,
+                            int n_cols, int col_bytes, int use_bias,
+                            const float *bias, int use_res,
+                            const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:1998 gemv_q6_k_compact_global_splitk: partial[s][j]
+ * over super-block split s, combined by tf_gemv_splitk_reduce. */
+int tf_gemv_q6k_compact_q8_splitk(const uint8_t *w, const int8_t *xq,
+                                  const float *xd, float *partial,
+                                  int n_rows, int n_cols, int col_bytes,
+                                  int n_split, tf_stream_t stream);
+
+/* kernels/gemv.cu:405 gemv_q6_k (matmul.rs:346-412 gemv_baseline): raw
+ * 210-byte Q6_K blocks times an f32 activation, fp32 arithmetic (attn_v). */
+int tf_gemv_q6k_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                    int n_cols, int col_bytes, int use_bias,
+                    const float *bias, int use_res, const float *residual,
+                    tf_stream_t stream);
+
+/* cuda/load.rs:145-159 align_q6_decode, on the device: copy raw 210-byte
+ * blocks to 212-byte compact blocks (two zero pad bytes).
+ * dst holds n_cols * floor(n_rows/256) * 212 bytes. */
+int tf_q6k_compact_repack(const uint8_t *raw, uint8_t *dst, int n_rows,
+                          int n_cols, int col_bytes, tf_stream_t stream);
+
+/* ---------------------------------------------------- split-KV flash decode */
+
+/* kernels/attn/flash.cu:16 attn_flash_partial (layer.rs:2040-2103), n_q = 1.
+ * q f32[n_head*head_dim]; k_cache/v_cache f16 bits [seq][n_kv*head_dim];
+ * attends positions 0..pos0.  The sequence is split into n_split chunks of
+ * ceil((pos0+1)/n_split) tokens and partial[(h*n_split+s)*(2+head_dim)]
+ * receives (m, l, O[head_dim]) with O not yet divided by l.  An empty chunk
+ * writes (-1e30, 0, 0...).  n_head % n_kv == 0, head_dim % 4 == 0,
+ * head_dim <= 256, 1 <= n_split <= 1024. */
+int tf_flash_decode_partial(const float *q, const uint16_t *k_cache,
+                            const uint16_t *v_cache, float *partial,
+                            int n_head, int n_kv, int head_dim, int pos0,
+                            int n_q, int n_split, float scale,
+                            tf_stream_t stream);
+
+/* kernels/attn/flash.cu:119 attn_flash_partial_d: pos0 read from device
+ * memory so that a captured HIP graph stays valid as the position moves. */
+int tf_flash_decode_partial_d(const float *q, const uint16_t *k_cache,
+                              const uint16_t *v_cache, float *partial,
+                              int n_head, int n_kv, int head_dim,
+                              const int *pos0_dev, int n_q, int n_split,
+                              float scale, tf_stream_t stream);
+
+/* kernels/attn/flash.cu:222 attn_flash_reduce: log-sum-exp merge,
+ * out[h*head_dim+d] = sum_s e^(m_s-M) O_s[d] / max(sum_s e^(m_s-M) l_s, 1e-20). */
+int tf_flash_decode_reduce(const float *partial, float *out, int n_head,
+                           int head_dim, int n_split, int n_q,
+                           tf_stream_t stream);
+
+/* Partition count this library recommends for a context of max_seq tokens
+ * (a multiple of 8; 8 for short contexts).  The reference fixes 8
+ * (cuda/decode.rs:38-41); on MI355X long contexts need more partitions to
+ * occupy 256 CUs.  The caller sizes partial[] as
+ * n_head * n_split * (2 + head_dim) floats. */
+int tf_flash_decode_n_split(int n_kv, int max_seq);
+
+/* ------------------------------------------------------- integer diagnostics */
+/* No reference counterpart: these expose the exact integer stage of the GEMV
+ * kernels (the same device code) so that the int32 sums can be checked
+ * bit-exactly.  For column j, super-block bi and sub-block g:
+ *   Q4_K: dots[(j*nb+bi)*8+g] = sum q4*q8, sums[...] = sum q8 (32 values)
+ *   Q6_K: dots[(j*nb+bi)*16+g] = sum (q6-32)*q8 (16 values)          */
+int tf_q4k_block_dots(const uint8_t *w, const int8_t *xq, int32_t *dots,
+                      int32_t *sums, int n_rows, int n_cols, int col_bytes,
+                      tf_stream_t stream);
+int tf_q6k_block_dots(const uint8_t *w, int block_bytes, const int8_t *xq,
+                      int32_t *dots, int n_rows, int n_cols, int col_bytes,
+                      tf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TARAFERENCE_HIP_H */

@@ -1,0 +1,100 @@
+"""ctypes binding of libtaraference_hip.so (the C ABI in include/taraference_hip.h).
+
+torch is imported first so that the library resolves libamdhip64.so.7 to the
+HIP runtime torch already loaded; device buffers and streams come from torch
+and are handed to the library as raw pointers.  There is no fallback: if the
+library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load: shared HIP runtime)
+
+LIB_PATH = Path(__file__).resolve().parent / "libtaraference_hip.so"
+
+_P = C.c_void_p
+_I = C.c_int
+_F = C.c_float
+
+# name -> argument types (every function returns int, a hipError_t)
+SIGNATURES: dict[str, list] = {
+    "tf_quantize_q8": [_P, _P, _P, _I, _P],
+    "tf_gemv_q4k_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q4k_q8_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_splitk_reduce": [_P, _P, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q4k_pair": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P],
+    "tf_gemv_q4k_dual": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_gemv_q4k_ffn": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_gemv_q4k_ffn_f32": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_gemv_q4k_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                        _P, _P, _P, _P],
+    "tf_gemv_q6k_compact_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q6k_down_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q6k_compact_q8_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_q6k_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_q6k_compact_repack": [_P, _P, _I, _I, _I, _P],
+    "tf_flash_decode_partial": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "tf_flash_decode_partial_d": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _F, _P],
+    "tf_flash_decode_reduce": [_P, _P, _I, _I, _I, _I, _P],
+    "tf_flash_decode_n_split": [_I, _I],
+    "tf_q4k_block_dots": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_q6k_block_dots": [_P, _I, _P, _P, _I, _I, _I, _P],
+    "tf_version": [],
+    "tf_exported_symbol_count": [],
+}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load(path: Path | str = LIB_PATH) -> C.CDLL:
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = Path(path)
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is missing: build it with `python -m taraference_amd.build` "
+            "(or __graft_entry__.build()); there is no non-HIP fallback")
+    lib = C.CDLL(str(p))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = C.c_int
+    lib.tf_exported_symbol.argtypes = [C.c_int]
+    lib.tf_exported_symbol.restype = C.c_char_p
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    lib = load()
+    return [lib.tf_exported_symbol(i).decode() for i in range(lib.tf_exported_symbol_count())]
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a tensor; None for None."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_ptr(stream=None) -> int | None:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def call(name: str, *args) -> None:
+    """Call C-ABI entry point `name`; raise HipError on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise HipError(f"{name} returned hipError {rc}")

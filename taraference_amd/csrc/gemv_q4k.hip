@@ -1,0 +1,396 @@
+// Q4_K x Q8 GEMV family for gfx950 (batch 1).
+//
+// Replaces kernels/gemv.cu gemv_q4_k_global (:469), gemv_q4_k_global_splitk
+// (:1877), gemv_splitk_reduce (:2243), gemv_q4_k_pair (:2346),
+// gemv_q4_k_dual (:2401), gemv_q4_k_ffn{,_4way,_8way} (:2440-2619),
+// gemv_q4_k_ffn_mcol (:2546) and gemv_q4_k_qkv (:2662).
+//
+// Every kernel is a persistent grid of 256-thread workgroups sized from the
+// occupancy of the kernel: each workgroup stages the Q8 activation in LDS
+// once, then each wave loops over row tasks.  See q4k.hpp for the lane map.
+#include <type_traits>
+
+#include "q4k.hpp"
+#include "tf_host.hpp"
+
+// ------------------------------------------------------------------ kernels
+
+struct TfQ4kMats {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    float* o0;
+    float* o1;
+    float* o2;
+    const float* b0;
+    const float* b1;
+    const float* b2;
+    int n0, n1, n2;
+};
+
+// Rows of up to three matrices that share K (global / pair / qkv).
+template <int SPR, int ITERS>
+__global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
+    TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+    int nb, int col_bytes, int use_bias, int use_res,
+    const float* __restrict__ residual) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    tf_stage_q8(xq, xd, nb, lds);
+    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int n_total = m.n0 + m.n1 + m.n2;
+    for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
+        const int r = r0 + unit;
+        const bool valid = r < n_total;
+        int j = r, mi = 0;
+        if (j >= m.n0) {
+            j -= m.n0;
+            mi = 1;
+            if (j >= m.n1) {
+                j -= m.n1;
+                mi = 2;
+            }
+        }
+        const uint8_t* w = mi == 0 ? m.w0 : (mi == 1 ? m.w1 : m.w2);
+        float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, 0, nb,
+                                               sir, t, x);
+        if (valid && (lane & (4 * SPR - 1)) == 0) {
+            float* out = mi == 0 ? m.o0 : (mi == 1 ? m.o1 : m.o2);
+            if (use_res == 1) acc += residual[j];
+            else if (use_res == 2) acc += out[j];
+            if (use_bias) acc += (mi == 0 ? m.b0 : (mi == 1 ? m.b1 : m.b2))[j];
+            out[j] = acc;
+        }
+    }
+}
+
+// Equal-width pair on the same output index: MODE 0 writes
+// silu(gate)*up (ffn), MODE 1 writes both dots (dual).  xf != nullptr means
+// the activation is f32 and is quantized into LDS by each workgroup.
+template <int SPR, int ITERS, int MODE>
+__global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
+    const uint8_t* __restrict__ wa, const uint8_t* __restrict__ wb,
+    const int8_t* __restrict__ xq, const float* __restrict__ xd,
+    const float* __restrict__ xf, float* __restrict__ out_a,
+    float* __restrict__ out_b, int nb, int n_cols, int col_bytes) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    if (xf) tf_quantize_to_lds(xf, nb, lds);
+    else tf_stage_q8(xq, xd, nb, lds);
+    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    const int lane = threadIdx.x & 63;
+    const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    if constexpr (SPR <= 8) {
+        // even unit = gate row j, odd unit = up row j
+        constexpr int JPW = 16 / SPR / 2;
+        for (int j0 = wave * JPW; j0 < n_cols; j0 += nwaves * JPW) {
+            const int j = j0 + (unit >> 1);
+            const bool valid = j < n_cols;
+            const uint8_t* w = (unit & 1) ? wb : wa;
+            const float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, 0,
+                                                         nb, sir, t, x);
+            const float other = __shfl(acc, (lane + 4 * SPR) & 63, 64);
+            if (valid && (unit & 1) == 0 && (lane & (4 * SPR - 1)) == 0) {
+                if (MODE == 0) {
+                    out_a[j] = (acc / (1.f + __expf(-acc))) * other;
+                } else {
+                    out_a[j] = acc;
+                    out_b[j] = other;
+                }
+            }
+        }
+    } else {
+        for (int j = wave; j < n_cols; j += nwaves) {
+            const float g = tf_q4k_row_dot<SPR, ITERS>(wa + (size_t)j * col_bytes, true, 0,
+                                                       nb, sir, t, x);
+            const float u = tf_q4k_row_dot<SPR, ITERS>(wb + (size_t)j * col_bytes, true, 0,
+                                                       nb, sir, t, x);
+            if (lane == 0) {
+                if (MODE == 0) {
+                    out_a[j] = (g / (1.f + __expf(-g))) * u;
+                } else {
+                    out_a[j] = g;
+                    out_b[j] = u;
+                }
+            }
+        }
+    }
+}
+
+// Split-K partials: task (s, j) covers super-blocks
+// [floor(nb*s/n_split), floor(nb*(s+1)/n_split)).
+template <int SPR, int ITERS>
+__global__ __launch_bounds__(256) void tf_q4k_splitk_kernel(
+    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+    const float* __restrict__ xd, float* __restrict__ partial, int nb,
+    int n_cols, int col_bytes, int n_split) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    tf_stage_q8(xq, xd, nb, lds);
+    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int n_total = n_split * n_cols;
+    for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
+        const int r = r0 + unit;
+        const bool valid = r < n_total;
+        const int s = valid ? r / n_cols : 0;
+        const int j = valid ? r - s * n_cols : 0;
+        const int sb0 = (nb * s) / n_split, sb1 = (nb * (s + 1)) / n_split;
+        const float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, sb0,
+                                                     sb1, sir, t, x);
+        if (valid && (lane & (4 * SPR - 1)) == 0) partial[(size_t)s * n_cols + j] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void tf_splitk_reduce_kernel(
+    const float* __restrict__ partial, float* __restrict__ out, int n_cols,
+    int n_split, int use_bias, const float* __restrict__ bias, int use_res,
+    const float* __restrict__ residual) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n_cols) return;
+    float acc = 0.f;
+    for (int s = 0; s < n_split; s++) acc += partial[(size_t)s * n_cols + j];
+    if (use_res == 1) acc += residual[j];
+    else if (use_res == 2) acc += out[j];
+    if (use_bias) acc += bias[j];
+    out[j] = acc;
+}
+
+// Integer diagnostics: the exact stage of tf_q4k_part_dot.
+__global__ __launch_bounds__(256) void tf_q4k_block_dots_kernel(
+    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+    int32_t* __restrict__ dots, int32_t* __restrict__ sums, int nb, int n_cols,
+    int col_bytes) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    int32_t* lsums = reinterpret_cast<int32_t*>(lds + tf_q8_lds_bytes(nb));
+    // Same copy-and-sum as tf_stage_q8; only the integer sums are kept.
+    {
+        int8_t* q8s = reinterpret_cast<int8_t*>(lds);
+        for (int g = threadIdx.x; g < nb * 8; g += blockDim.x) {
+            tf_u32x4 a = tf_ld16(xq + g * 32), b = tf_ld16(xq + g * 32 + 16);
+            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[0] = a;
+            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[1] = b;
+            const int one = 0x01010101;
+            int s = tf_dot4(one, (int)a.x, 0);
+            s = tf_dot4(one, (int)a.y, s);
+            s = tf_dot4(one, (int)a.z, s);
+            s = tf_dot4(one, (int)a.w, s);
+            s = tf_dot4(one, (int)b.x, s);
+            s = tf_dot4(one, (int)b.y, s);
+            s = tf_dot4(one, (int)b.z, s);
+            s = tf_dot4(one, (int)b.w, s);
+            lsums[g] = s;
+        }
+        __syncthreads();
+    }
+    const int8_t* q8s = reinterpret_cast<const int8_t*>(lds);
+    const long long task = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)n_cols * nb * 4;
+    if (task >= total) return;
+    const int t = (int)(task & 3);
+    const long long blk = task >> 2;
+    const int j = (int)(blk / nb), sb = (int)(blk % nb);
+    TfQ4kPart p;
+    tf_q4k_load(w + (size_t)j * col_bytes + (size_t)sb * 144, t, p);
+    int dlo, dhi;
+    tf_q4k_idots(p, q8s + sb * 256 + 64 * t, dlo, dhi);
+    const size_t o = ((size_t)j * nb + sb) * 8 + 2 * t;
+    dots[o] = dlo;
+    dots[o + 1] = dhi;
+    sums[o] = lsums[sb * 8 + 2 * t];
+    sums[o + 1] = lsums[sb * 8 + 2 * t + 1];
+}
+
+// ---------------------------------------------------------------- dispatch
+
+template <int V>
+using tf_ic = std::integral_constant<int, V>;
+
+// Pick slots-per-row and unroll depth for rows of `len` super-blocks.
+template <typename F>
+static void tf_q4k_dispatch(int len, F&& f) {
+    if (len <= 4) return f(tf_ic<4>{}, tf_ic<1>{});
+    if (len <= 8) return f(tf_ic<8>{}, tf_ic<1>{});
+    switch ((len + 15) / 16) {
+    case 1: return f(tf_ic<16>{}, tf_ic<1>{});
+    case 2: return f(tf_ic<16>{}, tf_ic<2>{});
+    case 3: return f(tf_ic<16>{}, tf_ic<3>{});
+    case 4: return f(tf_ic<16>{}, tf_ic<4>{});
+    case 5: return f(tf_ic<16>{}, tf_ic<5>{});
+    default: return f(tf_ic<16>{}, tf_ic<0>{});
+    }
+}
+
+static bool tf_q4k_weights_ok(const uint8_t* w, int nb, int col_bytes) {
+    return w && ((uintptr_t)w & 15) == 0 && (col_bytes & 15) == 0 && col_bytes >= nb * 144;
+}
+
+static int tf_q4k_rows(const TfQ4kMats& m, const int8_t* xq, const float* xd, int n_rows,
+                       int col_bytes, int use_bias, int use_res, const float* residual,
+                       tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    const int n_total = m.n0 + m.n1 + m.n2;
+    const int lds = tf_q8_lds_bytes(nb);
+    int rc = 0;
+    tf_q4k_dispatch(nb, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        auto fn = tf_q4k_rows_kernel<SPR, IT>;
+        const int tasks = (n_total + 16 / SPR - 1) / (16 / SPR);
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, xq, xd, nb,
+                           col_bytes, use_bias, use_res, residual);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+static int tf_q4k_pair_rows(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
+                            const float* xd, const float* xf, float* out_a, float* out_b,
+                            int n_rows, int n_cols, int col_bytes, int mode,
+                            tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    const int lds = tf_q8_lds_bytes(nb);
+    int rc = 0;
+    tf_q4k_dispatch(nb, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        auto fn0 = tf_q4k_pair_rows_kernel<SPR, IT, 0>;
+        auto fn1 = tf_q4k_pair_rows_kernel<SPR, IT, 1>;
+        auto fn = mode == 0 ? fn0 : fn1;
+        const int jpw = SPR <= 8 ? 16 / SPR / 2 : 1;
+        const int tasks = (n_cols + jpw - 1) / jpw;
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), wa, wb, xq, xd,
+                           xf, out_a, out_b, nb, n_cols, col_bytes);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" int tf_gemv_q4k_q8(const uint8_t* w, const int8_t* xq, const float* xd,
+                              float* out, int n_rows, int n_cols, int col_bytes,
+                              int use_bias, const float* bias, int use_res,
+                              const float* residual, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q4k_weights_ok(w, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
+    TF_CHECK_ARG(use_res != 1 || residual);
+    TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
+                n_cols, 0, 0};
+    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, use_res, residual, stream);
+}
+
+extern "C" int tf_gemv_q4k_pair(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
+                                const float* xd, float* out_a, float* out_b, int n_rows,
+                                int n_a, int n_b, int col_bytes, int use_bias,
+                                const float* ba, const float* bb, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_a >= 0 && n_b >= 0 && n_a + n_b > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(wa, nb, col_bytes) && tf_q4k_weights_ok(wb, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && out_a && out_b && (!use_bias || (ba && bb)));
+    TfQ4kMats m{wa, wb, nullptr, out_a, out_b, nullptr, ba, bb, nullptr, n_a, n_b, 0};
+    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+}
+
+extern "C" int tf_gemv_q4k_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const int8_t* xq, const float* xd, float* q, float* k,
+                               float* v, int n_rows, int n_q, int n_k, int n_v,
+                               int col_bytes, int use_bias, const float* bq,
+                               const float* bk, const float* bv, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_q >= 0 && n_k >= 0 && n_v >= 0 && n_q + n_k + n_v > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(wq, nb, col_bytes) && tf_q4k_weights_ok(wk, nb, col_bytes) &&
+                 tf_q4k_weights_ok(wv, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && q && k && v && (!use_bias || (bq && bk && bv)));
+    TfQ4kMats m{wq, wk, wv, q, k, v, bq, bk, bv, n_q, n_k, n_v};
+    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+}
+
+extern "C" int tf_gemv_q4k_dual(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
+                                const float* xd, float* out_a, float* out_b, int n_rows,
+                                int n_cols, int col_bytes, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(wa, nb, col_bytes) && tf_q4k_weights_ok(wb, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && out_a && out_b);
+    return tf_q4k_pair_rows(wa, wb, xq, xd, nullptr, out_a, out_b, n_rows, n_cols, col_bytes,
+                            1, stream);
+}
+
+extern "C" int tf_gemv_q4k_ffn(const uint8_t* gate, const uint8_t* up, const int8_t* xq,
+                               const float* xd, float* out, int n_rows, int n_cols,
+                               int col_bytes, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && out);
+    return tf_q4k_pair_rows(gate, up, xq, xd, nullptr, out, nullptr, n_rows, n_cols, col_bytes,
+                            0, stream);
+}
+
+extern "C" int tf_gemv_q4k_ffn_f32(const uint8_t* gate, const uint8_t* up, const float* x,
+                                   float* out, int n_rows, int n_cols, int col_bytes,
+                                   tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
+    TF_CHECK_ARG(x && out);
+    return tf_q4k_pair_rows(gate, up, nullptr, nullptr, x, out, nullptr, n_rows, n_cols,
+                            col_bytes, 0, stream);
+}
+
+extern "C" int tf_gemv_q4k_q8_splitk(const uint8_t* w, const int8_t* xq, const float* xd,
+                                     float* partial, int n_rows, int n_cols, int col_bytes,
+                                     int n_split, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && n_split >= 1 && n_split <= 8);
+    TF_CHECK_ARG(tf_q4k_weights_ok(w, nb, col_bytes) && xq && xd && partial);
+    const int lds = tf_q8_lds_bytes(nb);
+    const int len = (nb + n_split - 1) / n_split;
+    int rc = 0;
+    tf_q4k_dispatch(len, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        auto fn = tf_q4k_splitk_kernel<SPR, IT>;
+        const long long total = (long long)n_split * n_cols;
+        const int tasks = (int)((total + 16 / SPR - 1) / (16 / SPR));
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd,
+                           partial, nb, n_cols, col_bytes, n_split);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+extern "C" int tf_gemv_splitk_reduce(const float* partial, float* out, int n_cols,
+                                     int n_split, int use_bias, const float* bias,
+                                     int use_res, const float* residual, tf_stream_t stream) {
+    TF_CHECK_ARG(partial && out && n_cols > 0 && n_split >= 1);
+    TF_CHECK_ARG((!use_bias || bias) && use_res >= 0 && use_res <= 2 && (use_res != 1 || residual));
+    hipLaunchKernelGGL(tf_splitk_reduce_kernel, dim3((n_cols + 255) / 256), dim3(256), 0,
+                       tf_stream(stream), partial, out, n_cols, n_split, use_bias, bias,
+                       use_res, residual);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_q4k_block_dots(const uint8_t* w, const int8_t* xq, int32_t* dots,
+                                 int32_t* sums, int n_rows, int n_cols, int col_bytes,
+                                 tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q4k_weights_ok(w, nb, col_bytes));
+    TF_CHECK_ARG(xq && ((uintptr_t)xq & 15) == 0 && dots && sums);
+    const long long total = (long long)n_cols * nb * 4;
+    const int lds = tf_q8_lds_bytes(nb) + nb * 8 * 4;
+    hipLaunchKernelGGL(tf_q4k_block_dots_kernel, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), lds, tf_stream(stream), w, xq, dots, sums, nb, n_cols,
+                       col_bytes);
+    return TF_LAUNCH_RESULT();
+}

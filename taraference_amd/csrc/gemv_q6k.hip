@@ -1,0 +1,327 @@
+// Q6_K GEMV family for gfx950 (batch 1).
+//
+// Replaces kernels/gemv.cu gemv_q6_k_compact_global (:515),
+// gemv_q6_k_compact_global_{4way,8way} (:2025, :2081),
+// gemv_q6_k_compact_global_splitk (:1998), gemv_q6_k (:405) and the load-time
+// repack cuda/load.rs:145-159.
+//
+// The reference splits a tall Q6_K row over 4 or 8 warps of one block and
+// merges in shared memory.  Here a row is spread over 16 four-lane slots of
+// one wave with all of its weight loads issued up front, and the grid is
+// persistent, so the tall ffn_down and the wide lm_head use the same kernel.
+#include <type_traits>
+
+#include "q6k.hpp"
+#include "tf_host.hpp"
+
+template <int SPR, int ITERS>
+__global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
+    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+    const float* __restrict__ xd, float* __restrict__ out, int nb, int n_cols,
+    int col_bytes, int use_bias, const float* __restrict__ bias, int use_res,
+    const float* __restrict__ residual) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    tf_stage_q6(xq, xd, nb, lds);
+    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    for (int r0 = wave * UNITS; r0 < n_cols; r0 += nwaves * UNITS) {
+        const int j = r0 + unit;
+        const bool valid = j < n_cols;
+        float acc = tf_q6k_row_dot<SPR, ITERS>(w + (size_t)(valid ? j : 0) * col_bytes, valid, 0,
+                                               nb, sir, p, x);
+        if (valid && (lane & (4 * SPR - 1)) == 0) {
+            if (use_res == 1) acc += residual[j];
+            else if (use_res == 2) acc += out[j];
+            if (use_bias) acc += bias[j];
+            out[j] = acc;
+        }
+    }
+}
+
+template <int SPR, int ITERS>
+__global__ __launch_bounds__(256) void tf_q6k_splitk_kernel(
+    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+    const float* __restrict__ xd, float* __restrict__ partial, int nb, int n_cols,
+    int col_bytes, int n_split) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    tf_stage_q6(xq, xd, nb, lds);
+    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int n_total = n_split * n_cols;
+    for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
+        const int r = r0 + unit;
+        const bool valid = r < n_total;
+        const int s = valid ? r / n_cols : 0;
+        const int j = valid ? r - s * n_cols : 0;
+        const int sb0 = (nb * s) / n_split, sb1 = (nb * (s + 1)) / n_split;
+        const float acc = tf_q6k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, sb0, sb1,
+                                                     sir, p, x);
+        if (valid && (lane & (4 * SPR - 1)) == 0) partial[(size_t)s * n_cols + j] = acc;
+    }
+}
+
+// f32 activation over raw 210-byte blocks (kernels/gemv.cu:405-438).  x and
+// its 16-value sums live in LDS; per scale group the lane forms
+// sum(q*x) - 32*sum(x), then scales by d*sc.
+template <int SPR>
+__global__ __launch_bounds__(256) void tf_q6k_f32_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ xg, float* __restrict__ out,
+    int nb, int n_cols, int col_bytes, int use_bias, const float* __restrict__ bias,
+    int use_res, const float* __restrict__ residual) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    float* xs = reinterpret_cast<float*>(lds);
+    float* xsum = xs + nb * 256;
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(xg + i * 16 + k);
+            *reinterpret_cast<float4*>(xs + i * 16 + k) = v;
+            s += (v.x + v.y) + (v.z + v.w);
+        }
+        xsum[i] = s;
+    }
+    __syncthreads();
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int n = p >> 1, h = p & 1;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    for (int r0 = wave * UNITS; r0 < n_cols; r0 += nwaves * UNITS) {
+        const int j = r0 + unit;
+        const bool valid = j < n_cols;
+        const uint8_t* col = w + (size_t)(valid ? j : 0) * col_bytes;
+        float acc = 0.f;
+        for (int sb = sir; valid && sb < nb; sb += SPR) {
+            TfQ6kPart q;
+            tf_q6k_load_r(col + (size_t)sb * 210, p, q);
+            const float d = tf_h2f(q.d);
+            float part = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float* xv = xs + sb * 256 + 128 * n + 32 * k + 16 * h;
+                float s = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t word = tf_q6k_word(q, k, i);
+                    const float4 xx = *reinterpret_cast<const float4*>(xv + 4 * i);
+                    s += (float)(word & 0xff) * xx.x;
+                    s += (float)((word >> 8) & 0xff) * xx.y;
+                    s += (float)((word >> 16) & 0xff) * xx.z;
+                    s += (float)(word >> 24) * xx.w;
+                }
+                s -= 32.f * xsum[sb * 16 + 8 * n + 2 * k + h];
+                part += (float)tf_q6k_scale(q, p, k) * s;
+            }
+            acc += d * part;
+        }
+        acc = tf_group_sum<4 * SPR>(acc);
+        if (valid && (lane & (4 * SPR - 1)) == 0) {
+            if (use_res == 1) acc += residual[j];
+            else if (use_res == 2) acc += out[j];
+            if (use_bias) acc += bias[j];
+            out[j] = acc;
+        }
+    }
+}
+
+template <int BLOCK_BYTES>
+__global__ __launch_bounds__(256) void tf_q6k_block_dots_kernel(
+    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq, int32_t* __restrict__ dots,
+    int nb, int n_cols, int col_bytes) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    // stage only the bytes and 16-value sums (d8 is not part of the integer stage)
+    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
+    int32_t* s16 = reinterpret_cast<int32_t*>(lds + nb * 256);
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
+        const tf_u32x4 a = tf_ld16(xq + i * 16);
+        reinterpret_cast<tf_u32x4*>(q8s)[i] = a;
+        const int one = 0x01010101;
+        int s = tf_dot4(one, (int)a.x, 0);
+        s = tf_dot4(one, (int)a.y, s);
+        s = tf_dot4(one, (int)a.z, s);
+        s = tf_dot4(one, (int)a.w, s);
+        s16[i] = s;
+    }
+    __syncthreads();
+    const long long task = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (task >= (long long)n_cols * nb * 4) return;
+    const int p = (int)(task & 3);
+    const long long blk = task >> 2;
+    const int j = (int)(blk / nb), sb = (int)(blk % nb);
+    TfQ6kPart q;
+    const uint8_t* base = w + (size_t)j * col_bytes + (size_t)sb * BLOCK_BYTES;
+    if (BLOCK_BYTES == 212) tf_q6k_load_c(base, p, q);
+    else tf_q6k_load_r(base, p, q);
+    int idot[4];
+    tf_q6k_idots(q, p, q8s + sb * 256, s16 + sb * 16, idot);
+    const int n = p >> 1, h = p & 1;
+    for (int k = 0; k < 4; k++) dots[((size_t)j * nb + sb) * 16 + 8 * n + 2 * k + h] = idot[k];
+}
+
+__global__ __launch_bounds__(256) void tf_q6k_repack_kernel(const uint8_t* __restrict__ raw,
+                                                             uint8_t* __restrict__ dst, int nb,
+                                                             int n_cols, int col_bytes) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // dst dword
+    const long long total = (long long)n_cols * nb * 53;
+    if (i >= total) return;
+    const long long blk = i / 53;
+    const int k = (int)(i - blk * 53);
+    const int j = (int)(blk / nb), sb = (int)(blk % nb);
+    const uint8_t* src = raw + (size_t)j * col_bytes + (size_t)sb * 210 + 4 * k;
+    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(src);
+    uint32_t v = s2[0];
+    if (k < 52) v |= (uint32_t)s2[1] << 16;  // bytes 208,209 then two zero pad bytes
+    reinterpret_cast<uint32_t*>(dst)[i] = v;
+}
+
+// ---------------------------------------------------------------- dispatch
+
+template <int V>
+using tf_ic6 = std::integral_constant<int, V>;
+
+template <typename F>
+static void tf_q6k_dispatch(int len, F&& f) {
+    if (len <= 4) return f(tf_ic6<4>{}, tf_ic6<1>{});
+    if (len <= 8) return f(tf_ic6<8>{}, tf_ic6<1>{});
+    switch ((len + 15) / 16) {
+    case 1: return f(tf_ic6<16>{}, tf_ic6<1>{});
+    case 2: return f(tf_ic6<16>{}, tf_ic6<2>{});
+    case 3: return f(tf_ic6<16>{}, tf_ic6<3>{});
+    case 4: return f(tf_ic6<16>{}, tf_ic6<4>{});
+    case 5: return f(tf_ic6<16>{}, tf_ic6<5>{});
+    default: return f(tf_ic6<16>{}, tf_ic6<0>{});
+    }
+}
+
+static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
+    return w && ((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212;
+}
+
+static int tf_q6k_rows(const uint8_t* w, const int8_t* xq, const float* xd, float* out,
+                       int n_rows, int n_cols, int col_bytes, int use_bias, const float* bias,
+                       int use_res, const float* residual, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q6c_weights_ok(w, nb, col_bytes));
+    TF_CHECK_ARG(xq && xd && out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
+    TF_CHECK_ARG(use_res != 1 || residual);
+    const int lds = tf_q6_lds_bytes(nb);
+    int rc = 0;
+    tf_q6k_dispatch(nb, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        auto fn = tf_q6k_rows_kernel<SPR, IT>;
+        const int tasks = (n_cols + 16 / SPR - 1) / (16 / SPR);
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd, out,
+                           nb, n_cols, col_bytes, use_bias, bias, use_res, residual);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" int tf_gemv_q6k_compact_q8(const uint8_t* w, const int8_t* xq, const float* xd,
+                                      float* out, int n_rows, int n_cols, int col_bytes,
+                                      int use_bias, const float* bias, int use_res,
+                                      const float* residual, tf_stream_t stream) {
+    return tf_q6k_rows(w, xq, xd, out, n_rows, n_cols, col_bytes, use_bias, bias, use_res,
+                       residual, stream);
+}
+
+extern "C" int tf_gemv_q6k_down_splitk(const uint8_t* w, const int8_t* xq, const float* xd,
+                                       float* out, int n_rows, int n_cols, int col_bytes,
+                                       int use_bias, const float* bias, int use_res,
+                                       const float* residual, tf_stream_t stream) {
+    // Full-K per row inside one wave: the reference's in-block 4/8-way merge
+    // collapses into the wave reduction.
+    return tf_q6k_rows(w, xq, xd, out, n_rows, n_cols, col_bytes, use_bias, bias, use_res,
+                       residual, stream);
+}
+
+extern "C" int tf_gemv_q6k_compact_q8_splitk(const uint8_t* w, const int8_t* xq,
+                                             const float* xd, float* partial, int n_rows,
+                                             int n_cols, int col_bytes, int n_split,
+                                             tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && n_split >= 1 && n_split <= 8);
+    TF_CHECK_ARG(tf_q6c_weights_ok(w, nb, col_bytes) && xq && xd && partial);
+    const int lds = tf_q6_lds_bytes(nb);
+    int rc = 0;
+    tf_q6k_dispatch((nb + n_split - 1) / n_split, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        auto fn = tf_q6k_splitk_kernel<SPR, IT>;
+        const long long total = (long long)n_split * n_cols;
+        const int tasks = (int)((total + 16 / SPR - 1) / (16 / SPR));
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd,
+                           partial, nb, n_cols, col_bytes, n_split);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+extern "C" int tf_gemv_q6k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
+                               int n_cols, int col_bytes, int use_bias, const float* bias,
+                               int use_res, const float* residual, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && w && ((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
+    TF_CHECK_ARG(col_bytes >= nb * 210 && x && ((uintptr_t)x & 15) == 0 && out);
+    TF_CHECK_ARG((!use_bias || bias) && use_res >= 0 && use_res <= 2 && (use_res != 1 || residual));
+    const int lds = nb * 256 * 4 + nb * 16 * 4;
+    int rc = 0;
+    auto go = [&](auto spr) {
+        constexpr int SPR = decltype(spr)::value;
+        auto fn = tf_q6k_f32_kernel<SPR>;
+        const int tasks = (n_cols + 16 / SPR - 1) / (16 / SPR);
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, x, out, nb,
+                           n_cols, col_bytes, use_bias, bias, use_res, residual);
+        rc = TF_LAUNCH_RESULT();
+    };
+    if (nb <= 4) go(tf_ic6<4>{});
+    else if (nb <= 8) go(tf_ic6<8>{});
+    else go(tf_ic6<16>{});
+    return rc;
+}
+
+extern "C" int tf_q6k_compact_repack(const uint8_t* raw, uint8_t* dst, int n_rows, int n_cols,
+                                     int col_bytes, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && raw && dst && ((uintptr_t)raw & 1) == 0);
+    TF_CHECK_ARG((col_bytes & 1) == 0 && col_bytes >= nb * 210 && ((uintptr_t)dst & 3) == 0);
+    const long long total = (long long)n_cols * nb * 53;
+    hipLaunchKernelGGL(tf_q6k_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, tf_stream(stream), raw, dst, nb, n_cols, col_bytes);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_q6k_block_dots(const uint8_t* w, int block_bytes, const int8_t* xq,
+                                 int32_t* dots, int n_rows, int n_cols, int col_bytes,
+                                 tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && w && xq && ((uintptr_t)xq & 15) == 0 && dots);
+    TF_CHECK_ARG(block_bytes == 210 || block_bytes == 212);
+    TF_CHECK_ARG(col_bytes >= nb * block_bytes);
+    if (block_bytes == 212) TF_CHECK_ARG(tf_q6c_weights_ok(w, nb, col_bytes));
+    else TF_CHECK_ARG(((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
+    const long long total = (long long)n_cols * nb * 4;
+    const int lds = nb * 256 + nb * 64;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (block_bytes == 212)
+        hipLaunchKernelGGL(tf_q6k_block_dots_kernel<212>, grid, dim3(256), lds,
+                           tf_stream(stream), w, xq, dots, nb, n_cols, col_bytes);
+    else
+        hipLaunchKernelGGL(tf_q6k_block_dots_kernel<210>, grid, dim3(256), lds,
+                           tf_stream(stream), w, xq, dots, nb, n_cols, col_bytes);
+    return TF_LAUNCH_RESULT();
+}

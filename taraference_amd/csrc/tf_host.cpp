@@ -1,0 +1,104 @@
+// Host-side helpers: device properties, occupancy-sized persistent grids and
+// the list of exported C-ABI symbols.
+#include "tf_host.hpp"
+
+#include <mutex>
+#include <unordered_map>
+
+#include "taraference_hip.h"
+
+namespace {
+std::mutex g_mu;
+int g_cus[64];
+
+struct OccKey {
+    const void* fn;
+    int threads, lds, dev;
+    bool operator==(const OccKey& o) const {
+        return fn == o.fn && threads == o.threads && lds == o.lds && dev == o.dev;
+    }
+};
+struct OccHash {
+    size_t operator()(const OccKey& k) const {
+        return std::hash<const void*>()(k.fn) ^ ((size_t)k.threads << 40) ^
+               ((size_t)k.lds << 12) ^ (size_t)k.dev;
+    }
+};
+std::unordered_map<OccKey, int, OccHash> g_occ;
+}  // namespace
+
+int tf_device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_cus[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess || cus <= 0)
+            cus = 256;
+        g_cus[dev] = cus;
+    }
+    return g_cus[dev];
+}
+
+int tf_persistent_blocks(const void* kernel, int threads, int lds_bytes, int tasks) {
+    if (tasks <= 0) return 1;
+    const int cus = tf_device_cus();
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int per_cu = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        OccKey key{kernel, threads, lds_bytes, dev};
+        auto it = g_occ.find(key);
+        if (it != g_occ.end()) {
+            per_cu = it->second;
+        } else {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads,
+                                                             lds_bytes) != hipSuccess ||
+                per_cu <= 0)
+                per_cu = 1;
+            g_occ[key] = per_cu;
+        }
+    }
+    const int waves_per_block = threads / 64;
+    const long long max_waves = (long long)cus * per_cu * waves_per_block;
+    const long long per_wave = (tasks + max_waves - 1) / max_waves;
+    const long long waves = (tasks + per_wave - 1) / per_wave;
+    return (int)((waves + waves_per_block - 1) / waves_per_block);
+}
+
+static const char* const k_symbols[] = {
+    "tf_version",
+    "tf_exported_symbol_count",
+    "tf_exported_symbol",
+    "tf_quantize_q8",
+    "tf_gemv_q4k_q8",
+    "tf_gemv_q4k_q8_splitk",
+    "tf_gemv_splitk_reduce",
+    "tf_gemv_q4k_pair",
+    "tf_gemv_q4k_dual",
+    "tf_gemv_q4k_ffn",
+    "tf_gemv_q4k_ffn_f32",
+    "tf_gemv_q4k_qkv",
+    "tf_gemv_q6k_compact_q8",
+    "tf_gemv_q6k_down_splitk",
+    "tf_gemv_q6k_compact_q8_splitk",
+    "tf_gemv_q6k_f32",
+    "tf_q6k_compact_repack",
+    "tf_flash_decode_partial",
+    "tf_flash_decode_partial_d",
+    "tf_flash_decode_reduce",
+    "tf_flash_decode_n_split",
+    "tf_q4k_block_dots",
+    "tf_q6k_block_dots",
+};
+
+extern "C" int tf_version(void) { return 100; }
+extern "C" int tf_exported_symbol_count(void) {
+    return (int)(sizeof(k_symbols) / sizeof(k_symbols[0]));
+}
+extern "C" const char* tf_exported_symbol(int i) {
+    if (i < 0 || i >= tf_exported_symbol_count()) return nullptr;
+    return k_symbols[i];
+}

@@ -1,0 +1,11 @@
+// Host-side helpers shared by the C-ABI entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+
+// Compute units of the current device (cached per device).
+int tf_device_cus();
+
+// Workgroups for a persistent grid: `tasks` wave-tasks spread evenly over at
+// most (resident workgroups per CU) * CUs workgroups of `threads` threads,
+// so that every wave runs the same number of tasks.
+int tf_persistent_blocks(const void* kernel, int threads, int lds_bytes, int tasks);

@@ -1,0 +1,99 @@
+"""Seeded synthetic K-quant weights and activations.
+
+Block formats follow the GGUF / reference layout (kernels/common.cu:40-186):
+  Q4_K, 144 B: d f16, dmin f16, 12 packed 6-bit scale/min bytes, 128 qs bytes.
+  Q6_K, 210 B: ql[128], qh[64], int8 scales[16], d f16.
+Distributions: d and dmin ~ U[1e-3, 1e-2] as f16;
+6-bit scales and mins ~ U{0..63}; nibbles ~ U{0..15}; Q6_K ql/qh bytes
+uniform, scales ~ U[-32, 31]; activations ~ N(0, 1) f32.
+
+A weight matrix is returned as uint8 [n_cols, col_bytes]: output column j is
+the contiguous run of ceil(n_rows/256) super-blocks, as the reference stores
+it (cuda/load.rs:205-206,235).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4K_BYTES = 144
+Q6K_BYTES = 210
+Q6K_COMPACT_BYTES = 212
+
+SEED_BASE = 0x7A7A0000
+
+
+def rng_for(config: int, salt: int = 0) -> np.random.Generator:
+    return np.random.default_rng(SEED_BASE + config * 1000 + salt)
+
+
+def pack_q4k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Pack 6-bit scales/mins [n, 8] into the 12-byte Q4_K layout.
+
+    Inverse of get_scale_min_k4 (kernels/common.cu:40-50): for j < 4 the low
+    six bits of bytes j and j+4 hold sc_j and m_j; for j >= 4 byte j+4 holds
+    the low nibbles of sc_j | m_j << 4 and the top two bits of sc_j / m_j go
+    to bits 6-7 of bytes j-4 / j.
+    """
+    sc = sc.astype(np.uint8)
+    m = m.astype(np.uint8)
+    out = np.zeros((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = m[:, 0:4] | ((m[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 0xF) | ((m[:, 4:8] & 0xF) << 4)
+    return out
+
+
+def q4k_blocks(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n random Q4_K super-blocks as uint8 [n, 144]."""
+    blk = np.empty((n, Q4K_BYTES), np.uint8)
+    d = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    dmin = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(n, 2)
+    sc = rng.integers(0, 64, (n, 8), dtype=np.uint8)
+    m = rng.integers(0, 64, (n, 8), dtype=np.uint8)
+    blk[:, 4:16] = pack_q4k_scales(sc, m)
+    blk[:, 16:] = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+    return blk
+
+
+def q6k_blocks(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n random Q6_K super-blocks as uint8 [n, 210]."""
+    blk = np.empty((n, Q6K_BYTES), np.uint8)
+    blk[:, 0:192] = rng.integers(0, 256, (n, 192), dtype=np.uint8)
+    blk[:, 192:208] = rng.integers(-32, 32, (n, 16), dtype=np.int8).view(np.uint8)
+    d = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(n, 2)
+    return blk
+
+
+def q4k_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
+    """Q4_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*144."""
+    nb = (n_rows + 255) // 256
+    w = q4k_blocks(rng, n_cols * nb).reshape(n_cols, nb * Q4K_BYTES)
+    return np.ascontiguousarray(w), nb * Q4K_BYTES
+
+
+def q6k_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
+    """Raw Q6_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*210."""
+    nb = (n_rows + 255) // 256
+    w = q6k_blocks(rng, n_cols * nb).reshape(n_cols, nb * Q6K_BYTES)
+    return np.ascontiguousarray(w), nb * Q6K_BYTES
+
+
+def q6k_compact(raw: np.ndarray, n_rows: int) -> tuple[np.ndarray, int]:
+    """Host restatement of cuda/load.rs:145-159 (210 -> 212-byte blocks)."""
+    n_cols = raw.shape[0]
+    nb = n_rows // 256
+    out = np.zeros((n_cols, nb, Q6K_COMPACT_BYTES), np.uint8)
+    out[:, :, :Q6K_BYTES] = raw[:, : nb * Q6K_BYTES].reshape(n_cols, nb, Q6K_BYTES)
+    return out.reshape(n_cols, nb * Q6K_COMPACT_BYTES), nb * Q6K_COMPACT_BYTES
+
+
+def activation(rng, n: int) -> np.ndarray:
+    return rng.standard_normal(n).astype(np.float32)
+
+
+def kv_cache(rng, seq: int, n_kv: int, head_dim: int) -> np.ndarray:
+    """f16 cache [seq, n_kv*head_dim] ~ N(0,1), returned as uint16 bits."""
+    return rng.standard_normal((seq, n_kv * head_dim)).astype(np.float16).view(np.uint16)

@@ -1,0 +1,77 @@
+"""GPU parity of split-KV flash decode (BASELINE config 2 and the 7B GQA
+shape) against the oracle and textbook fp64 attention, tolerance 2e-3
+absolute.  Also checks the reference's partial-buffer contract (m, l, O) for
+empty partitions and the device-position (graph) variant."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from taraference_amd import capi, synth
+from _gpu import P, S, call, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-3
+
+
+def case(L, n_head, n_kv, hd, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    K = synth.kv_cache(rng, L, n_kv, hd)
+    V = synth.kv_cache(rng, L, n_kv, hd)
+    return q, K, V
+
+
+def run_gpu(q, K, V, n_head, n_kv, hd, pos0, n_split, scale, device_pos=False):
+    part = empty(n_head * n_split * (2 + hd))
+    out = empty(n_head * hd)
+    qd, kd, vd = dev(q), dev(K), dev(V)
+    if device_pos:
+        pd = dev(np.array([pos0], np.int32))
+        call("tf_flash_decode_partial_d", P(qd), P(kd), P(vd), P(part), n_head, n_kv, hd, P(pd),
+             1, n_split, scale, S())
+    else:
+        call("tf_flash_decode_partial", P(qd), P(kd), P(vd), P(part), n_head, n_kv, hd, pos0, 1,
+             n_split, scale, S())
+    call("tf_flash_decode_reduce", P(part), P(out), n_head, hd, n_split, 1, S())
+    return host(part), host(out)
+
+
+@pytest.mark.parametrize("L", [1, 5, 512, 777, 4096, 32768])
+@pytest.mark.parametrize("split", ["8", "auto"])
+def test_flash_config2(gpu, L, split):
+    n_head, n_kv, hd = 16, 2, 128
+    q, K, V = case(L, n_head, n_kv, hd, L)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    n_split = 8 if split == "8" else capi.load().tf_flash_decode_n_split(n_kv, L)
+    part, out = run_gpu(q, K, V, n_head, n_kv, hd, L - 1, n_split, scale)
+    ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)
+    assert np.abs(out - ref).max() < ATOL
+    if n_split == 8 and L <= 4096:
+        oref = oracle.flash_reduce(oracle.flash_partial(q, K, V, n_head, n_kv, hd, L - 1, 8, scale),
+                                   n_head, hd, 8)
+        assert np.abs(out - oref).max() < ATOL
+    p = part.reshape(n_head, n_split, 2 + hd)
+    chunk = -(-L // n_split)
+    empty_s = [s for s in range(n_split) if s * chunk >= L]
+    for s in empty_s:
+        assert np.all(p[:, s, 0] == np.float32(-1e30)) and np.all(p[:, s, 1:] == 0)
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,L", [(28, 4, 128, 3000), (8, 8, 64, 100),
+                                              (16, 4, 256, 700)])
+def test_flash_shapes(gpu, n_head, n_kv, hd, L):
+    q, K, V = case(L, n_head, n_kv, hd, 3)
+    scale = 0.09
+    _, out = run_gpu(q, K, V, n_head, n_kv, hd, L - 1, 8, scale, device_pos=True)
+    ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)
+    assert np.abs(out - ref).max() < ATOL
+
+
+def test_flash_prefix_of_longer_cache(gpu):
+    """Attends only positions 0..pos0 of a cache that holds more rows."""
+    n_head, n_kv, hd = 16, 2, 128
+    q, K, V = case(1024, n_head, n_kv, hd, 11)
+    _, out = run_gpu(q, K, V, n_head, n_kv, hd, 600, 8, 0.088)
+    ref = oracle.attn_f64(q, K[:601].copy(), V[:601].copy(), n_head, n_kv, hd, 601, 0.088)
+    assert np.abs(out - ref).max() < ATOL
