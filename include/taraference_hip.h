@@ -9,9 +9,9 @@
  * launch geometry internally.
  *
  * Conventions shared by every entry point
- *   - All pointers are device pointers owned by the caller.  The library does
- *     not allocate device memory.  The one exception is the one-time
- *     hipModule-free kernel registration done by the HIP runtime itself.
+ *   - All pointers are device pointers owned by the caller.  The kernel entry
+ *     points never allocate device memory; only tf_model_create (the decode
+ *     runtime, at load time) allocates its workspace and KV cache.
  *   - Weights use the reference layout.  n_rows = K is the input length and
  *     n_cols = N is the number of outputs.  Output column j occupies
  *     col_bytes bytes at w + j*col_bytes and holds floor(n_rows/256)
@@ -98,6 +98,13 @@ int tf_gemv_q4k_dual(const uint8_t *wa, const uint8_t *wb, const int8_t *xq,
 int tf_gemv_q4k_ffn(const uint8_t *gate, const uint8_t *up, const int8_t *xq,
                     const float *xd, float *out, int n_rows, int n_cols,
                     int col_bytes, tf_stream_t stream);
+
+/* kernels/gemv.cu:377 gemv_q4_k (matmul.rs:346-412 gemv_baseline): f32
+ * activation, quantized to Q8 inside every workgroup (bit-identically to
+ * tf_quantize_q8), then the Q4_K x Q8 dot. */
+int tf_gemv_q4k_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                    int n_cols, int col_bytes, int use_bias, const float *bias,
+                    int use_res, const float *residual, tf_stream_t stream);
 
 /* kernels/gemv.cu:2546 gemv_q4_k_ffn_mcol (matmul.rs:680-697): as
  * tf_gemv_q4k_ffn but x is f32 and is quantized to Q8 inside every
@@ -188,6 +195,94 @@ int tf_flash_decode_reduce(const float *partial, float *out, int n_head,
  * occupy 256 CUs.  The caller sizes partial[] as
  * n_head * n_split * (2 + head_dim) floats. */
 int tf_flash_decode_n_split(int n_kv, int max_seq);
+
+/* ------------------------------------------------------- decode-step glue */
+
+/* kernels/embed.cu:51-131 embed_q{4,6}_k_one[_d]: dequantize row `token`
+ * (or *token_dev when token_dev != NULL) of a Q4_K (block_bytes 144) or raw
+ * Q6_K (210) table into out[n_rows]. */
+int tf_embed_row(const uint8_t *table, int block_bytes, float *out, int token,
+                 const int *token_dev, int n_rows, int col_bytes,
+                 tf_stream_t stream);
+/* kernels/ops.cu:4-34 rms_norm_f32 (one row): out = x * rsqrt(mean x^2 + eps) * w */
+int tf_rms_norm(const float *x, const float *w, float *out, int n, float eps,
+                tf_stream_t stream);
+/* kernels/ops.cu:348-398 rope_neox_f32[_d]: rotate (i, i+hd/2) of every head
+ * by pos * theta^(-2i/hd); pos read from pos_dev when non-NULL. */
+int tf_rope_neox(float *x, int n_heads, int head_dim, int pos,
+                 const int *pos_dev, float theta, tf_stream_t stream);
+/* kernels/ops.cu:471-504 copy_kv_f16[_d]: cache[pos*stride + i] =
+ * f16(src[i]) with the reference's round-half-up conversion. */
+int tf_copy_kv_f16(const float *src, uint16_t *cache, int pos,
+                   const int *pos_dev, int stride, tf_stream_t stream);
+/* kernels/ops.cu:573-599 argmax_f32: *out_idx = index of the largest x
+ * (lowest index among exact ties). */
+int tf_argmax(const float *x, int n, int *out_idx, tf_stream_t stream);
+
+/* ----------------------------------------------------- decode-step runtime */
+/* C++ restatement of the reference model runtime for dense Qwen2-style
+ * models (cuda/forward.rs:42-407, cuda/layer.rs:99-709,1210-1456,2125-2259,
+ * cuda/model.rs:522-570): one greedy decode step per call, optionally
+ * replayed from a captured HIP graph with the position and token in device
+ * memory.  Weights are caller-owned device buffers. */
+
+#define TF_TYPE_Q4_K 12 /* GGML type ids */
+#define TF_TYPE_Q6_K 14
+
+/* cuda/types.rs:212-225 GpuMat: data = GGUF bytes; compact = 212-byte Q6_K
+ * repack (NULL for Q4_K). */
+typedef struct tf_mat {
+    const uint8_t *data;
+    const uint8_t *compact;
+    int type;
+    int n_rows;
+    int n_cols;
+    int col_bytes;
+    int compact_col_bytes;
+} tf_mat;
+
+typedef struct tf_layer {
+    const float *attn_norm;
+    tf_mat wq, wk, wv;
+    const float *bq, *bk, *bv; /* NULL when the model has no QKV bias */
+    tf_mat wo;
+    const float *ffn_norm;
+    tf_mat gate, up, down;
+} tf_layer;
+
+typedef struct tf_model_config {
+    int n_layer, n_embd, n_ff, n_head, n_kv, head_dim, n_vocab, max_seq;
+    float rope_theta, rms_eps;
+} tf_model_config;
+
+typedef struct tf_model tf_model;
+
+/* cuda/load.rs:166 + model.rs:522: bind weights, allocate workspace and the
+ * f16 KV cache [n_layer][max_seq][n_kv*head_dim] (K and V). token_embd is
+ * the embedding table; output is the lm_head (may be the same tensor). */
+int tf_model_create(const tf_model_config *cfg, const tf_layer *layers,
+                    const tf_mat *token_embd, const tf_mat *output,
+                    const float *output_norm, tf_model **out);
+void tf_model_destroy(tf_model *m);
+/* cuda/forward.rs:42 forward_greedy for one token at position pos: runs the
+ * eager kernel sequence, leaves logits on the device, *next_token set on the
+ * host (blocks on the stream). */
+int tf_model_forward(tf_model *m, int token, int pos, int *next_token,
+                     tf_stream_t stream);
+/* Runs n_forced + n_gen decode steps from position pos0 with the position,
+ * token and outputs kept in device memory (forward.rs:73-264; replayed from
+ * a captured HIP graph when use_graph).  Step i < n_forced consumes
+ * forced[i] (a prompt fed through the decode path); later steps consume the
+ * previous argmax.  tokens[i] (i < n_gen) receives the argmax of step
+ * n_forced - 1 + i, i.e. the greedy continuation.  The stream is
+ * synchronized once, at the end. */
+int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
+                      int n_gen, int *tokens, int use_graph, tf_stream_t stream);
+/* Device pointer of the last logits (n_vocab floats) and of the f16 K/V
+ * cache of layer li. */
+const float *tf_model_logits(const tf_model *m);
+uint16_t *tf_model_k_cache(const tf_model *m, int li);
+uint16_t *tf_model_v_cache(const tf_model *m, int li);
 
 /* ------------------------------------------------------- integer diagnostics */
 /* No reference counterpart: these expose the exact integer stage of the GEMV

@@ -238,6 +238,40 @@ def attn_f64(q, k_cache, v_cache, n_head, n_kv, head_dim, seq_len, scale):
     return out
 
 
+# ------------------------------------------------------------------ decode glue
+
+def embed_row(table, block_bytes, token, n_rows, col_bytes):
+    out = _f32(n_rows)
+    lib().or_embed_row(_p(table), block_bytes, token, n_rows, col_bytes, _p(out))
+    return out
+
+
+def rms_norm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = _f32(x.size)
+    lib().or_rms_norm(_p(x), _p(w), _p(out), x.size, C.c_float(eps))
+    return out
+
+
+def rope_neox(x, n_heads, head_dim, pos, theta):
+    x = np.array(x, np.float32)
+    lib().or_rope_neox(_p(x), n_heads, head_dim, pos, C.c_float(theta))
+    return x
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(x.size, np.uint16)
+    lib().or_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def argmax(x):
+    x = np.ascontiguousarray(x, np.float32)
+    return lib().or_argmax(_p(x), x.size)
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def gemv_q4k_q8_mt(w, xq, xd, n_rows, n_cols, col_bytes, nthreads):

@@ -746,6 +746,77 @@ void or_attn_f64(const float *q, const uint16_t *k_cache,
     free(sc);
 }
 
+/* ------------------------------------------------------- decode-step glue */
+
+/* kernels/common.cu:64-84 dequant_q4_k_block_smem, one value:
+ * (d*sc)*q - dmin*m; both products are exact in fp32. */
+static float q4k_dequant_value(const uint8_t *blk, int v) {
+    const float d = or_f16_to_f32(rd16(blk)), dmin = or_f16_to_f32(rd16(blk + 2));
+    int sc, m;
+    scale_min_k4(v >> 5, blk + 4, &sc, &m);
+    const int t = v >> 6, l = v & 31;
+    const uint8_t qb = blk[16 + 32 * t + l];
+    const int q = ((v >> 5) & 1) ? (qb >> 4) : (qb & 0xF);
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    return d1 * (float)q - m1;
+}
+
+void or_embed_row(const uint8_t *table, int block_bytes, int token, int n_rows,
+                  int col_bytes, float *out) {
+    const uint8_t *col = table + (size_t)token * col_bytes;
+    const int nb = n_rows / 256;
+    for (int bi = 0; bi < nb; bi++) {
+        const uint8_t *blk = col + (size_t)bi * block_bytes;
+        for (int v = 0; v < 256; v++) {
+            if (block_bytes == 144) {
+                out[bi * 256 + v] = q4k_dequant_value(blk, v);
+            } else { /* kernels/common.cu:164-186: (d*sc)*q */
+                const float d = or_f16_to_f32(rd16(blk + 208));
+                out[bi * 256 + v] = d * (float)(int8_t)blk[192 + v / 16] * (float)q6_value(blk, v);
+            }
+        }
+    }
+}
+
+void or_rms_norm(const float *x, const float *w, float *out, int n, float eps) {
+    float buf[256];
+    for (int t = 0; t < 256; t++) {
+        float local = 0.f;
+        for (int i = t; i < n; i += 256) local += x[i] * x[i];
+        buf[t] = local;
+    }
+    for (int s = 128; s > 0; s >>= 1)
+        for (int t = 0; t < s; t++) buf[t] += buf[t + s];
+    const float scale = 1.0f / sqrtf(buf[0] / (float)n + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+}
+
+void or_rope_neox(float *x, int n_heads, int head_dim, int pos, float theta) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < n_heads; h++) {
+        float *base = x + (size_t)h * head_dim;
+        for (int i = 0; i < half; i++) {
+            const float freq = powf(theta, -2.f * (float)i / (float)head_dim);
+            const float ang = (float)pos * freq;
+            const float c = cosf(ang), s = sinf(ang);
+            const float x0 = base[i], x1 = base[i + half];
+            base[i] = x0 * c - x1 * s;
+            base[i + half] = x0 * s + x1 * c;
+        }
+    }
+}
+
+void or_f32_to_f16_array(const float *src, uint16_t *dst, int n) {
+    for (int i = 0; i < n; i++) dst[i] = or_f32_to_f16_halfup(src[i]);
+}
+
+int or_argmax(const float *x, int n) {
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (x[i] > x[best]) best = i;
+    return best;
+}
+
 /* ------------------------------------------------------ CPU baseline (MT) */
 
 typedef struct {

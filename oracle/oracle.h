@@ -125,6 +125,21 @@ void or_attn_f64(const float *q, const uint16_t *k_cache,
                  const uint16_t *v_cache, double *out, int n_head, int n_kv,
                  int head_dim, int seq_len, float scale);
 
+/* Decode-step glue.
+ * kernels/embed.cu:51-131: dequantize row `token` (block_bytes 144 = Q4_K,
+ * 210 = raw Q6_K) into out[n_rows]. */
+void or_embed_row(const uint8_t *table, int block_bytes, int token, int n_rows,
+                  int col_bytes, float *out);
+/* kernels/ops.cu:4-34 with 256 threads: strided per-thread sums of squares,
+ * halving tree, scale = 1/sqrt(ss/n + eps), out = (x*scale)*w. */
+void or_rms_norm(const float *x, const float *w, float *out, int n, float eps);
+/* kernels/ops.cu:348-371 rope_neox_f32 (one token, all heads). */
+void or_rope_neox(float *x, int n_heads, int head_dim, int pos, float theta);
+/* kernels/ops.cu:471-486 copy_kv_f16: f16 bits with round-half-up. */
+void or_f32_to_f16_array(const float *src, uint16_t *dst, int n);
+/* Largest value, lowest index among exact ties. */
+int or_argmax(const float *x, int n);
+
 /* CPU baseline: or_gemv_q4k_q8 / or_gemv_q6k_compact_q8_kway with the
  * output columns partitioned over nthreads POSIX threads.           */
 void or_gemv_q4k_q8_mt(const uint8_t *w, const int8_t *xq, const float *xd,

@@ -98,3 +98,19 @@ def call(name: str, *args) -> None:
     rc = getattr(lib, name)(*args)
     if rc != 0:
         raise HipError(f"{name} returned hipError {rc}")
+
+
+_hip = None
+
+
+def memcpy_d2h(dst, src_ptr: int) -> None:
+    """Blocking copy of dst.nbytes bytes from device address src_ptr into the
+    numpy array dst (through the HIP runtime torch loaded)."""
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hip.hipMemcpy.restype = C.c_int
+    rc = _hip.hipMemcpy(dst.ctypes.data_as(C.c_void_p), C.c_void_p(src_ptr), dst.nbytes, 2)
+    if rc != 0:
+        raise HipError(f"hipMemcpy returned {rc}")

@@ -1,0 +1,244 @@
+// Decode-step glue kernels for gfx950: token embedding row, RMSNorm, NeoX
+// RoPE, f32 -> f16 KV append and argmax.  Each has a host-position and a
+// device-position ("_d") variant where the reference has one, so that a
+// captured HIP graph stays valid while the position advances.
+//
+// Replaces kernels/embed.cu embed_q{4,6}_k_one[_d] (:51-131), kernels/ops.cu
+// rms_norm_f32 (:4-34), rope_neox_f32[_d] (:348-398), copy_kv_f16[_d]
+// (:471-504) and argmax_f32 (:573-599).
+#include <math.h>
+
+#include "tf_common.hpp"
+#include "tf_host.hpp"
+
+// ------------------------------------------------------------ embedding
+
+// One 256-value super-block per wave-quarter: value v of block bi.
+// Q4_K: d*sc*q - dmin*m (kernels/common.cu:64-84); Q6_K: d*sc*(q-32)
+// (kernels/common.cu:164-186).  Both products are exact in fp32, so the row
+// is bit-identical to any evaluation order.
+__device__ __forceinline__ float tf_q4k_value(const uint8_t* blk, int v) {
+    const float d = tf_h2f(blk[0] | (blk[1] << 8));
+    const float dmin = tf_h2f(blk[2] | (blk[3] << 8));
+    const uint8_t* sc = blk + 4;
+    const int g = v >> 5, t = v >> 6, l = v & 31;
+    int s, m;
+    if (g < 4) {
+        s = sc[g] & 63;
+        m = sc[g + 4] & 63;
+    } else {
+        s = (sc[g + 4] & 0xF) | ((sc[g - 4] >> 6) << 4);
+        m = (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+    }
+    const uint8_t qb = blk[16 + 32 * t + l];
+    const int q = (g & 1) ? (qb >> 4) : (qb & 0xF);
+    const float d1 = d * (float)s, m1 = dmin * (float)m;
+    return d1 * (float)q - m1;
+}
+
+__device__ __forceinline__ float tf_q6k_value(const uint8_t* blk, int v) {
+    const int n = v >> 7, r = v & 127, k = r >> 5, l = r & 31;
+    const uint8_t* ql = blk + 64 * n;
+    const uint8_t qh = blk[128 + 32 * n + l];
+    int lo;
+    switch (k) {
+    case 0: lo = ql[l] & 0xF; break;
+    case 1: lo = ql[32 + l] & 0xF; break;
+    case 2: lo = ql[l] >> 4; break;
+    default: lo = ql[32 + l] >> 4; break;
+    }
+    const int q = (lo | (((qh >> (2 * k)) & 3) << 4)) - 32;
+    const float d = tf_h2f(blk[208] | (blk[209] << 8));
+    const int8_t sc = (int8_t)blk[192 + (v >> 4)];
+    return d * (float)sc * (float)q;
+}
+
+template <int BLOCK_BYTES>
+__global__ __launch_bounds__(256) void tf_embed_kernel(const uint8_t* __restrict__ table,
+                                                       float* __restrict__ out, int token,
+                                                       const int* __restrict__ token_dev,
+                                                       int n_rows, int col_bytes) {
+    if (token_dev) token = token_dev[0];
+    const uint8_t* col = table + (size_t)token * col_bytes;
+    const int nb = n_rows / 256;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nb * 256; i += gridDim.x * blockDim.x) {
+        const uint8_t* blk = col + (size_t)(i >> 8) * BLOCK_BYTES;
+        out[i] = BLOCK_BYTES == 144 ? tf_q4k_value(blk, i & 255) : tf_q6k_value(blk, i & 255);
+    }
+}
+
+// ------------------------------------------------------------ RMSNorm
+
+// out = x * (1/sqrt(mean(x^2) + eps)) * w  (kernels/ops.cu:4-34), one row,
+// with the reference's summation order: 256 strided per-thread sums, then a
+// halving tree in LDS, so the normalized row is bit-identical to a CPU
+// restatement of the same order.
+__global__ __launch_bounds__(256) void tf_rms_norm_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          float* __restrict__ out, int n,
+                                                          float eps) {
+    __shared__ float buf[256];
+    float local = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = x[i];
+        local += v * v;
+    }
+    buf[threadIdx.x] = local;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) buf[threadIdx.x] += buf[threadIdx.x + s];
+        __syncthreads();
+    }
+    const float scale = 1.0f / sqrtf(buf[0] / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) out[i] = x[i] * scale * w[i];
+}
+
+// ------------------------------------------------------------ RoPE (NeoX)
+
+// Rotates pairs (i, i + hd/2) of every head by pos * theta^(-2i/hd)
+// (kernels/ops.cu:348-398).
+__global__ __launch_bounds__(64) void tf_rope_neox_kernel(float* __restrict__ x, int head_dim,
+                                                          int pos, const int* __restrict__ pos_dev,
+                                                          float theta) {
+    if (pos_dev) pos = pos_dev[0];
+    const int h = blockIdx.x;
+    const int half = head_dim / 2;
+    float* base = x + (size_t)h * head_dim;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float freq = powf(theta, -2.f * (float)i / (float)head_dim);
+        const float ang = (float)pos * freq;
+        float s, c;
+        sincosf(ang, &s, &c);
+        const float x0 = base[i], x1 = base[i + half];
+        base[i] = x0 * c - x1 * s;
+        base[i + half] = x0 * s + x1 * c;
+    }
+}
+
+// ------------------------------------------------------------ KV append
+
+// f32 -> f16 bits, truncating the mantissa and adding one ulp when the first
+// dropped bit is set (kernels/common.cu:9-38); subnormals, zero, inf and nan
+// as the reference.
+__device__ __forceinline__ uint16_t tf_f2h_halfup(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t absx = x & 0x7fffffffu;
+    if (absx == 0u) return (uint16_t)sign;
+    if (absx >= 0x7f800000u) return (uint16_t)(sign | (absx == 0x7f800000u ? 0x7c00u : 0x7e00u));
+    if (absx < 0x33000000u) return (uint16_t)sign;
+    if (absx >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
+    const int e = (int)((absx >> 23) & 0xff) - 127 + 15;
+    uint32_t mant = absx & 0x7fffffu;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        mant |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t hm = mant >> shift;
+        if ((mant >> (shift - 1)) & 1u) hm += 1u;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (mant >> 13);
+    if (mant & 0x1000u) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+__global__ __launch_bounds__(256) void tf_copy_kv_kernel(const float* __restrict__ src,
+                                                         uint16_t* __restrict__ cache, int pos,
+                                                         const int* __restrict__ pos_dev,
+                                                         int stride) {
+    if (pos_dev) pos = pos_dev[0];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < stride) cache[(size_t)pos * stride + i] = tf_f2h_halfup(src[i]);
+}
+
+// ------------------------------------------------------------ argmax
+
+// Index of the largest value; ties go to the lowest index.  The reference's
+// strided scan + tree (kernels/ops.cu:573-599) does not always pick the
+// lowest index among exact ties; that is the only difference.
+__global__ __launch_bounds__(1024) void tf_argmax_kernel(const float* __restrict__ x, int n,
+                                                         int* __restrict__ out_idx) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > best) {
+            best = v;
+            idx = i;
+        }
+    }
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int k = bi[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (bv[w] > b || (bv[w] == b && bi[w] < k)) {
+                b = bv[w];
+                k = bi[w];
+            }
+        out_idx[0] = k == 0x7fffffff ? 0 : k;
+    }
+}
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" int tf_embed_row(const uint8_t* table, int block_bytes, float* out, int token,
+                            const int* token_dev, int n_rows, int col_bytes,
+                            tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(table && out && nb > 0 && (token_dev || token >= 0));
+    TF_CHECK_ARG((block_bytes == 144 || block_bytes == 210) && col_bytes >= nb * block_bytes);
+    const int blocks = (nb * 256 + 255) / 256;
+    if (block_bytes == 144)
+        hipLaunchKernelGGL(tf_embed_kernel<144>, dim3(blocks), dim3(256), 0, tf_stream(stream),
+                           table, out, token, token_dev, n_rows, col_bytes);
+    else
+        hipLaunchKernelGGL(tf_embed_kernel<210>, dim3(blocks), dim3(256), 0, tf_stream(stream),
+                           table, out, token, token_dev, n_rows, col_bytes);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_rms_norm(const float* x, const float* w, float* out, int n, float eps,
+                           tf_stream_t stream) {
+    TF_CHECK_ARG(x && w && out && n > 0);
+    hipLaunchKernelGGL(tf_rms_norm_kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, out, n,
+                       eps);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_rope_neox(float* x, int n_heads, int head_dim, int pos, const int* pos_dev,
+                            float theta, tf_stream_t stream) {
+    TF_CHECK_ARG(x && n_heads > 0 && head_dim > 0 && (head_dim & 1) == 0 && (pos_dev || pos >= 0));
+    hipLaunchKernelGGL(tf_rope_neox_kernel, dim3(n_heads), dim3(64), 0, tf_stream(stream), x,
+                       head_dim, pos, pos_dev, theta);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_copy_kv_f16(const float* src, uint16_t* cache, int pos, const int* pos_dev,
+                              int stride, tf_stream_t stream) {
+    TF_CHECK_ARG(src && cache && stride > 0 && (pos_dev || pos >= 0));
+    hipLaunchKernelGGL(tf_copy_kv_kernel, dim3((stride + 255) / 256), dim3(256), 0,
+                       tf_stream(stream), src, cache, pos, pos_dev, stride);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_argmax(const float* x, int n, int* out_idx, tf_stream_t stream) {
+    TF_CHECK_ARG(x && n > 0 && out_idx);
+    hipLaunchKernelGGL(tf_argmax_kernel, dim3(1), dim3(1024), 0, tf_stream(stream), x, n, out_idx);
+    return TF_LAUNCH_RESULT();
+}

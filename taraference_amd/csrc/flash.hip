@@ -5,34 +5,53 @@
 // reference layout partial[(h*n_split + s)*(2+hd)] = (m, l, O[hd]).
 //
 // A workgroup serves one (kv head, split) pair and every GQA query head that
-// reads that kv head, so each K/V byte of the split is read once.  Its four
-// waves walk the split in 64-token steps (wave w takes steps w, w+4, ...):
-//   scores: lane = token; the lane streams its K row (16-byte loads) and
-//           accumulates q_g . k for all G heads (q is wave-uniform);
-//   softmax: per-head wave max / sum, online rescale (running m, l);
-//   PV:     lane = head_dim/64 contiguous dims; every token's V row is one
-//           coalesced 2*hd-byte load; exp weights are broadcast from LDS.
-// The four per-wave states are merged with log-sum-exp in LDS at the end.
+// reads that kv head (G = n_head/n_kv), so each K/V byte of the split is read
+// once.  Wave w owns heads w*HPW .. w*HPW+HPW-1.  The split is walked in
+// 64-token tiles:
+//   load:    the workgroup copies the K and V tiles to LDS with 16-byte
+//            loads; the next tile is already in flight (registers) while the
+//            current one is being used;
+//   scores:  lane = token; K row from LDS (rows padded by 16 bytes so 16
+//            lanes hit 16 distinct bank quads), q broadcast from LDS;
+//   softmax: per head, wave max / sum with the running (m, l) rescale;
+//   PV:      lane = head_dim/64 contiguous dims, exp weights broadcast from
+//            LDS, V row from LDS.
+// Each wave owns whole heads, so (m, l, O) is written without a merge.
 #include <math.h>
 
 #include "tf_common.hpp"
 #include "tf_host.hpp"
 
-#define TF_FLASH_STEP 64
-#define TF_FLASH_WAVES 4
+#define TF_FLASH_TILE 64
 #define TF_NEG_BIG (-1e30f)
 
-template <int HD, int GMAX>
+template <int HD>
+struct TfFlashLds {
+    static constexpr int KROW = HD + 8;  // halves per padded K row
+    static constexpr int CHUNKS = TF_FLASH_TILE * HD / 8;  // 16-byte chunks per tile
+    static constexpr int PER_THREAD = CHUNKS / 256;
+};
+
+template <int HD, int HPW>
 __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, float* __restrict__ partial, int n_head, int n_kv,
     int pos0, const int* __restrict__ pos0_dev, int n_split, float scale) {
-    constexpr int DPL = HD / 64;  // dims per lane in the PV phase
+    using L = TfFlashLds<HD>;
+    constexpr int GMAX = 4 * HPW;
+    constexpr int DPL = HD / 64;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    float* q_lds = reinterpret_cast<float*>(lds_raw);                      // [GMAX][HD]
+    float* p_lds = q_lds + GMAX * HD;                                       // [GMAX][TILE]
+    uint16_t* k_lds = reinterpret_cast<uint16_t*>(p_lds + GMAX * TF_FLASH_TILE);  // [TILE][KROW]
+    uint16_t* v_lds = k_lds + TF_FLASH_TILE * L::KROW;                      // [TILE][HD]
+
     const int kv_h = blockIdx.x;
     const int s = blockIdx.y;
     const int G = n_head / n_kv;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int stride = n_kv * HD;
     if (pos0_dev) pos0 = pos0_dev[0];
     const int seq_len = pos0 + 1;
@@ -40,34 +59,62 @@ __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
     const int t_begin = s * chunk;
     const int t_end = min(t_begin + chunk, seq_len);
 
-    __shared__ float e_lds[TF_FLASH_WAVES][GMAX][TF_FLASH_STEP];
-    __shared__ float m_lds[TF_FLASH_WAVES][GMAX];
-    __shared__ float l_lds[TF_FLASH_WAVES][GMAX];
-    __shared__ float o_lds[TF_FLASH_WAVES][GMAX][HD];
+    const uint16_t* kbase = k_cache + (size_t)kv_h * HD;
+    const uint16_t* vbase = v_cache + (size_t)kv_h * HD;
 
-    const float* qk = q + (size_t)kv_h * G * HD;  // heads kv_h*G .. kv_h*G+G-1
+    // tile t0 -> registers (row r of chunk c: r = c / (HD/8), col = 8*(c % (HD/8)))
+    tf_u32x4 kr[L::PER_THREAD], vr[L::PER_THREAD];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < L::PER_THREAD; i++) {
+            const int c = tid + 256 * i;
+            const int r = c / (HD / 8), col = 8 * (c % (HD / 8));
+            const int t = t0 + r;
+            if (t < t_end) {
+                kr[i] = tf_ld16(kbase + (size_t)t * stride + col);
+                vr[i] = tf_ld16(vbase + (size_t)t * stride + col);
+            } else {
+                kr[i] = tf_u32x4{0, 0, 0, 0};
+                vr[i] = tf_u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    if (t_begin < t_end) load_tile(t_begin);
 
-    float m[GMAX], l[GMAX], o[GMAX][DPL];
+    const float* qk = q + (size_t)kv_h * G * HD;
+    for (int i = tid; i < GMAX * HD; i += 256) q_lds[i] = (i / HD) < G ? qk[i] : 0.f;
+
+    float m[HPW], l[HPW], o[HPW][DPL];
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-        m[g] = TF_NEG_BIG;
-        l[g] = 0.f;
+    for (int hh = 0; hh < HPW; hh++) {
+        m[hh] = TF_NEG_BIG;
+        l[hh] = 0.f;
 #pragma unroll
-        for (int i = 0; i < DPL; i++) o[g][i] = 0.f;
+        for (int i = 0; i < DPL; i++) o[hh][i] = 0.f;
     }
 
-    for (int t0 = t_begin + wave * TF_FLASH_STEP; t0 < t_end;
-         t0 += TF_FLASH_WAVES * TF_FLASH_STEP) {
-        // ---- scores (lane = token)
+    for (int t0 = t_begin; t0 < t_end; t0 += TF_FLASH_TILE) {
+        __syncthreads();  // previous tile fully consumed
+#pragma unroll
+        for (int i = 0; i < L::PER_THREAD; i++) {
+            const int c = tid + 256 * i;
+            const int r = c / (HD / 8), col = 8 * (c % (HD / 8));
+            *reinterpret_cast<tf_u32x4*>(k_lds + r * L::KROW + col) = kr[i];
+            *reinterpret_cast<tf_u32x4*>(v_lds + r * HD + col) = vr[i];
+        }
+        if (t0 + TF_FLASH_TILE < t_end) load_tile(t0 + TF_FLASH_TILE);
+        __syncthreads();
+
+        // ---- scores: lane = token
         const int t = t0 + lane;
         const bool tv = t < t_end;
-        float sc[GMAX];
+        float sc[HPW];
 #pragma unroll
-        for (int g = 0; g < GMAX; g++) sc[g] = 0.f;
-        const uint16_t* krow = k_cache + (size_t)(tv ? t : t0) * stride + (size_t)kv_h * HD;
-#pragma unroll 2
+        for (int hh = 0; hh < HPW; hh++) sc[hh] = 0.f;
+        const uint16_t* krow = k_lds + lane * L::KROW;
+#pragma unroll 4
         for (int d = 0; d < HD; d += 8) {
-            const tf_u32x4 kw = tf_ld16(krow + d);
+            const tf_u32x4 kw = *reinterpret_cast<const tf_u32x4*>(krow + d);
             float kf[8];
             kf[0] = tf_h2f(kw.x);
             kf[1] = tf_h2f(kw.x >> 16);
@@ -78,132 +125,164 @@ __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
             kf[6] = tf_h2f(kw.w);
             kf[7] = tf_h2f(kw.w >> 16);
 #pragma unroll
-            for (int g = 0; g < GMAX; g++) {
-                if (g < G) {
-                    const float* qg = qk + g * HD + d;
-                    float a = sc[g];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) a += qg[i] * kf[i];
-                    sc[g] = a;
-                }
+            for (int hh = 0; hh < HPW; hh++) {
+                const float* qh = q_lds + (wave * HPW + hh) * HD + d;
+                const float4 q0 = *reinterpret_cast<const float4*>(qh);
+                const float4 q1 = *reinterpret_cast<const float4*>(qh + 4);
+                float a = sc[hh];
+                a += q0.x * kf[0];
+                a += q0.y * kf[1];
+                a += q0.z * kf[2];
+                a += q0.w * kf[3];
+                a += q1.x * kf[4];
+                a += q1.y * kf[5];
+                a += q1.z * kf[6];
+                a += q1.w * kf[7];
+                sc[hh] = a;
             }
         }
-        // ---- online softmax per head
-        float alpha[GMAX];
+        // ---- online softmax per head (wave-uniform control flow)
+        float alpha[HPW];
 #pragma unroll
-        for (int g = 0; g < GMAX; g++) {
-            if (g < G) {
-                const float sv = tv ? sc[g] * scale : TF_NEG_BIG;
-                float mx = sv;
-                mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float m_new = fmaxf(m[g], mx);
-                alpha[g] = __expf(m[g] - m_new);
-                const float e = tv ? __expf(sv - m_new) : 0.f;
-                e_lds[wave][g][lane] = e;
-                const float tile_l = tf_group_sum<64>(e);
-                l[g] = l[g] * alpha[g] + tile_l;
-                m[g] = m_new;
-            }
+        for (int hh = 0; hh < HPW; hh++) {
+            const float sv = tv ? sc[hh] * scale : TF_NEG_BIG;
+            float mx = sv;
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m[hh], mx);
+            alpha[hh] = __expf(m[hh] - m_new);
+            const float e = tv ? __expf(sv - m_new) : 0.f;
+            p_lds[(wave * HPW + hh) * TF_FLASH_TILE + lane] = e;
+            l[hh] = l[hh] * alpha[hh] + tf_group_sum<64>(e);
+            m[hh] = m_new;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) o[hh][i] *= alpha[hh];
         }
-        __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // ---- PV (lane = DPL dims)
+        // ---- PV: lane = DPL dims
+        const int tlen = min(TF_FLASH_TILE, t_end - t0);
+        const uint16_t* vcol = v_lds + lane * DPL;
+        for (int tt = 0; tt < tlen; tt += 4) {
+            float pw[HPW][4];
 #pragma unroll
-        for (int g = 0; g < GMAX; g++)
-#pragma unroll
-            for (int i = 0; i < DPL; i++) o[g][i] *= (g < G) ? alpha[g] : 1.f;
-        const int tlen = min(TF_FLASH_STEP, t_end - t0);
-        const uint16_t* vbase = v_cache + (size_t)t0 * stride + (size_t)kv_h * HD + lane * DPL;
-        for (int tt = 0; tt < tlen; tt++) {
-            const uint16_t* vr = vbase + (size_t)tt * stride;
-            float vf[DPL];
-            if constexpr (DPL == 1) {
-                vf[0] = tf_h2f(vr[0]);
-            } else if constexpr (DPL == 2) {
-                const uint32_t vv = *reinterpret_cast<const uint32_t*>(vr);
-                vf[0] = tf_h2f(vv);
-                vf[1] = tf_h2f(vv >> 16);
-            } else {
-                const tf_u32x2 vv = *reinterpret_cast<const tf_u32x2*>(vr);
-                vf[0] = tf_h2f(vv.x);
-                vf[1] = tf_h2f(vv.x >> 16);
-                vf[2] = tf_h2f(vv.y);
-                vf[3] = tf_h2f(vv.y >> 16);
+            for (int hh = 0; hh < HPW; hh++) {
+                const float4 pv =
+                    *reinterpret_cast<const float4*>(p_lds + (wave * HPW + hh) * TF_FLASH_TILE + tt);
+                pw[hh][0] = pv.x;
+                pw[hh][1] = pv.y;
+                pw[hh][2] = pv.z;
+                pw[hh][3] = pv.w;
             }
 #pragma unroll
-            for (int g = 0; g < GMAX; g++) {
-                if (g < G) {
-                    const float e = e_lds[wave][g][tt];
-#pragma unroll
-                    for (int i = 0; i < DPL; i++) o[g][i] += e * vf[i];
+            for (int u = 0; u < 4; u++) {
+                const uint16_t* vr2 = vcol + (tt + u) * HD;
+                float vf[DPL];
+                if constexpr (DPL == 1) {
+                    vf[0] = tf_h2f(vr2[0]);
+                } else if constexpr (DPL == 2) {
+                    const uint32_t vv = *reinterpret_cast<const uint32_t*>(vr2);
+                    vf[0] = tf_h2f(vv);
+                    vf[1] = tf_h2f(vv >> 16);
+                } else {
+                    const tf_u32x2 vv = *reinterpret_cast<const tf_u32x2*>(vr2);
+                    vf[0] = tf_h2f(vv.x);
+                    vf[1] = tf_h2f(vv.x >> 16);
+                    vf[2] = tf_h2f(vv.y);
+                    vf[3] = tf_h2f(vv.y >> 16);
                 }
+#pragma unroll
+                for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+                    for (int i = 0; i < DPL; i++) o[hh][i] += pw[hh][u] * vf[i];
             }
         }
-        __builtin_amdgcn_wave_barrier();
     }
 
-    // ---- merge the four wave states (log-sum-exp)
+    // ---- write (m, l, O) of this wave's heads
+    const int po = 2 + HD;
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
+    for (int hh = 0; hh < HPW; hh++) {
+        const int g = wave * HPW + hh;
         if (g < G) {
+            float* base = partial + ((size_t)(kv_h * G + g) * n_split + s) * po;
             if (lane == 0) {
-                m_lds[wave][g] = m[g];
-                l_lds[wave][g] = l[g];
+                base[0] = m[hh];
+                base[1] = l[hh];
             }
 #pragma unroll
-            for (int i = 0; i < DPL; i++) o_lds[wave][g][lane * DPL + i] = o[g][i];
+            for (int i = 0; i < DPL; i++) base[2 + lane * DPL + i] = o[hh][i];
         }
-    }
-    __syncthreads();
-    const int po = 2 + HD;
-    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
-        const int g = idx / HD, d = idx - g * HD;
-        float M = TF_NEG_BIG;
-#pragma unroll
-        for (int w = 0; w < TF_FLASH_WAVES; w++) M = fmaxf(M, m_lds[w][g]);
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int w = 0; w < TF_FLASH_WAVES; w++) {
-            const float a = __expf(m_lds[w][g] - M);
-            L += a * l_lds[w][g];
-            O += a * o_lds[w][g][d];
-        }
-        float* base = partial + ((size_t)(kv_h * G + g) * n_split + s) * po;
-        if (d == 0) {
-            base[0] = M;
-            base[1] = L;
-        }
-        base[2 + d] = O;
     }
 }
 
+// Log-sum-exp merge of the partitions of one head per workgroup: the
+// partition weights e^(m_s - M) go to LDS once; each thread then owns one
+// dimension and a strided subset of partitions, and the subsets are summed
+// through LDS.
 __global__ __launch_bounds__(256) void tf_flash_reduce_kernel(const float* __restrict__ partial,
                                                               float* __restrict__ out,
                                                               int head_dim, int n_split) {
+    __shared__ float wts[1024];
+    __shared__ float red[256];
+    __shared__ float stat[2];
     const int h = blockIdx.x;
+    const int tid = threadIdx.x;
     const int po = 2 + head_dim;
     const float* ph = partial + (size_t)h * n_split * po;
-    float M = TF_NEG_BIG;
-    for (int s = 0; s < n_split; s++) M = fmaxf(M, ph[(size_t)s * po]);
-    for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
-        float L = 0.f, acc = 0.f;
-        for (int s = 0; s < n_split; s++) {
-            const float* b = ph + (size_t)s * po;
-            const float a = __expf(b[0] - M);
-            L += a * b[1];
-            acc += a * b[2 + d];
-        }
-        out[(size_t)h * head_dim + d] = acc / fmaxf(L, 1e-20f);
+    float mx = TF_NEG_BIG;
+    for (int s = tid; s < n_split; s += 256) mx = fmaxf(mx, ph[(size_t)s * po]);
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float lsum = 0.f;
+    for (int s = tid; s < n_split; s += 256) {
+        const float a = __expf(ph[(size_t)s * po] - M);
+        wts[s] = a;
+        lsum += a * ph[(size_t)s * po + 1];
+    }
+    lsum = tf_group_sum<64>(lsum);
+    if ((tid & 63) == 0) red[tid >> 6] = lsum;
+    __syncthreads();
+    if (tid == 0) stat[0] = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    const float L = stat[0];
+    const int subsets = 256 / head_dim;  // head_dim <= 256
+    const int d = tid % head_dim, sub = tid / head_dim;
+    float acc = 0.f;
+    if (sub < subsets) {
+#pragma unroll 8
+        for (int s = sub; s < n_split; s += subsets) acc += wts[s] * ph[(size_t)s * po + 2 + d];
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < head_dim) {
+        float tot = 0.f;
+        for (int k = 0; k < subsets; k++) tot += red[k * head_dim + tid];
+        out[(size_t)h * head_dim + tid] = tot / fmaxf(L, 1e-20f);
     }
 }
 
 // ---------------------------------------------------------------- dispatch
+
+template <int HD>
+static int tf_flash_lds_bytes(int hpw) {
+    const int gmax = 4 * hpw;
+    return gmax * HD * 4 + gmax * TF_FLASH_TILE * 4 + TF_FLASH_TILE * (HD + 8) * 2 +
+           TF_FLASH_TILE * HD * 2;
+}
 
 template <int HD>
 static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t* v,
@@ -213,15 +292,17 @@ static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t*
     const int G = n_head / n_kv;
     const dim3 grid(n_kv, n_split);
     if (G <= 4)
-        hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 4>), grid, dim3(256), 0,
-                           tf_stream(stream), q, k, v, partial, n_head, n_kv, pos0, pos0_dev,
-                           n_split, scale);
+        hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 1>), grid, dim3(256),
+                           tf_flash_lds_bytes<HD>(1), tf_stream(stream), q, k, v, partial, n_head,
+                           n_kv, pos0, pos0_dev, n_split, scale);
     else if (G <= 8)
-        hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 8>), grid, dim3(256), 0,
-                           tf_stream(stream), q, k, v, partial, n_head, n_kv, pos0, pos0_dev,
-                           n_split, scale);
+        hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 2>), grid, dim3(256),
+                           tf_flash_lds_bytes<HD>(2), tf_stream(stream), q, k, v, partial, n_head,
+                           n_kv, pos0, pos0_dev, n_split, scale);
     else
-        return (int)hipErrorInvalidValue;
+        hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 4>), grid, dim3(256),
+                           tf_flash_lds_bytes<HD>(4), tf_stream(stream), q, k, v, partial, n_head,
+                           n_kv, pos0, pos0_dev, n_split, scale);
     return TF_LAUNCH_RESULT();
 }
 
@@ -230,7 +311,7 @@ static int tf_flash_partial_any(const float* q, const uint16_t* k, const uint16_
                                 const int* pos0_dev, int n_q, int n_split, float scale,
                                 tf_stream_t stream) {
     TF_CHECK_ARG(q && k && v && partial && n_head > 0 && n_kv > 0 && n_head % n_kv == 0);
-    TF_CHECK_ARG(n_head / n_kv <= 8 && n_q == 1 && n_split >= 1 && n_split <= 1024);
+    TF_CHECK_ARG(n_head / n_kv <= 16 && n_q == 1 && n_split >= 1 && n_split <= 1024);
     TF_CHECK_ARG(pos0_dev || pos0 >= 0);
     TF_CHECK_ARG(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0);
     switch (head_dim) {
@@ -270,17 +351,17 @@ extern "C" int tf_flash_decode_partial_d(const float* q, const uint16_t* k_cache
 extern "C" int tf_flash_decode_reduce(const float* partial, float* out, int n_head,
                                       int head_dim, int n_split, int n_q, tf_stream_t stream) {
     TF_CHECK_ARG(partial && out && n_head > 0 && head_dim > 0 && n_split >= 1 && n_q == 1);
-    const int threads = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
-    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(threads), 0, tf_stream(stream), partial, out, head_dim, n_split);
+    TF_CHECK_ARG(head_dim <= 256 && n_split <= 1024);
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream), partial, out, head_dim, n_split);
     return TF_LAUNCH_RESULT();
 }
 
 extern "C" int tf_flash_decode_n_split(int n_kv, int max_seq) {
     if (n_kv <= 0 || max_seq <= 0) return 8;
     const int cus = tf_device_cus();
-    // at least one full 4-wave step (256 tokens) per split; aim for ~2
-    // workgroups per CU; multiples of 8 as in the reference's fixed split.
-    int by_len = max_seq / (TF_FLASH_WAVES * TF_FLASH_STEP);
+    // at least two 64-token tiles per split; aim for ~2 workgroups per CU;
+    // multiples of 8 as in the reference's fixed split.
+    int by_len = max_seq / (2 * TF_FLASH_TILE);
     int by_cus = (2 * cus + n_kv - 1) / n_kv;
     int n = by_len < by_cus ? by_len : by_cus;
     n = (n / 8) * 8;

@@ -28,43 +28,90 @@ struct TfQ4kMats {
     int n0, n1, n2;
 };
 
+// Row task helpers.  A wave task covers UNITS = 16/SPR rows at once; every
+// kernel below keeps the next task's weights in flight (registers) while it
+// computes the current one, and issues its first task's loads before the
+// workgroup stages the activation in LDS.
+
+struct TfRowSel {
+    const uint8_t* col;
+    bool valid;
+    int j;   // output index within its matrix
+    int mi;  // matrix index
+};
+
+__device__ __forceinline__ TfRowSel tf_sel3(const TfQ4kMats& m, int r, int n_total,
+                                            int col_bytes) {
+    TfRowSel s;
+    s.valid = r < n_total;
+    int j = s.valid ? r : 0, mi = 0;
+    if (j >= m.n0) {
+        j -= m.n0;
+        mi = 1;
+        if (j >= m.n1) {
+            j -= m.n1;
+            mi = 2;
+        }
+    }
+    s.j = j;
+    s.mi = mi;
+    s.col = (mi == 0 ? m.w0 : (mi == 1 ? m.w1 : m.w2)) + (size_t)j * col_bytes;
+    return s;
+}
+
 // Rows of up to three matrices that share K (global / pair / qkv).
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
     TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-    int nb, int col_bytes, int use_bias, int use_res,
+    const float* __restrict__ xf, int nb, int col_bytes, int use_bias, int use_res,
     const float* __restrict__ residual) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_q8(xq, xd, nb, lds);
-    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_total = m.n0 + m.n1 + m.n2;
-    for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
-        const int r = r0 + unit;
-        const bool valid = r < n_total;
-        int j = r, mi = 0;
-        if (j >= m.n0) {
-            j -= m.n0;
-            mi = 1;
-            if (j >= m.n1) {
-                j -= m.n1;
-                mi = 2;
-            }
+    const int n_tasks = (n_total + UNITS - 1) / UNITS;
+    int task = wave;
+    TfRowSel cs = tf_sel3(m, task * UNITS + unit, n_total, col_bytes);
+    TfQ4kRow<ITERS> cur, nxt;
+    if (ITERS > 0 && task < n_tasks) tf_q4k_row_load<SPR, ITERS>(cs.col, cs.valid, 0, nb, sir, t, cur);
+    if (xf) tf_quantize_to_lds(xf, nb, lds);
+    else tf_stage_q8(xq, xd, nb, lds);
+    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    for (; task < n_tasks; task += nwaves) {
+        const int nt = task + nwaves;
+        const TfRowSel ns = tf_sel3(m, nt * UNITS + unit, n_total, col_bytes);
+        float acc;
+        if constexpr (ITERS > 0) {
+            if (nt < n_tasks) tf_q4k_row_load<SPR, ITERS>(ns.col, ns.valid, 0, nb, sir, t, nxt);
+            acc = tf_q4k_row_partial<SPR, ITERS>(cur, cs.valid, 0, nb, sir, t, x);
+        } else {
+            acc = tf_q4k_row_partial_loop<SPR>(cs.col, cs.valid, 0, nb, sir, t, x);
         }
-        const uint8_t* w = mi == 0 ? m.w0 : (mi == 1 ? m.w1 : m.w2);
-        float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, 0, nb,
-                                               sir, t, x);
-        if (valid && (lane & (4 * SPR - 1)) == 0) {
+        acc = tf_group_sum<4 * SPR>(acc);
+        if (cs.valid && (lane & (4 * SPR - 1)) == 0) {
+            const int j = cs.j, mi = cs.mi;
             float* out = mi == 0 ? m.o0 : (mi == 1 ? m.o1 : m.o2);
             if (use_res == 1) acc += residual[j];
             else if (use_res == 2) acc += out[j];
             if (use_bias) acc += (mi == 0 ? m.b0 : (mi == 1 ? m.b1 : m.b2))[j];
             out[j] = acc;
         }
+        if constexpr (ITERS > 0) cur = nxt;
+        cs = ns;
+    }
+}
+
+template <int MODE>
+__device__ __forceinline__ void tf_pair_write(float g, float u, float* out_a, float* out_b,
+                                              int j) {
+    if constexpr (MODE == 0) {
+        out_a[j] = (g / (1.f + __expf(-g))) * u;
+    } else {
+        out_a[j] = g;
+        out_b[j] = u;
     }
 }
 
@@ -78,9 +125,6 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
     const float* __restrict__ xf, float* __restrict__ out_a,
     float* __restrict__ out_b, int nb, int n_cols, int col_bytes) {
     extern __shared__ __align__(16) uint8_t lds[];
-    if (xf) tf_quantize_to_lds(xf, nb, lds);
-    else tf_stage_q8(xq, xd, nb, lds);
-    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
@@ -88,35 +132,60 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
     if constexpr (SPR <= 8) {
         // even unit = gate row j, odd unit = up row j
         constexpr int JPW = 16 / SPR / 2;
-        for (int j0 = wave * JPW; j0 < n_cols; j0 += nwaves * JPW) {
-            const int j = j0 + (unit >> 1);
-            const bool valid = j < n_cols;
-            const uint8_t* w = (unit & 1) ? wb : wa;
-            const float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, 0,
-                                                         nb, sir, t, x);
+        const int n_tasks = (n_cols + JPW - 1) / JPW;
+        const uint8_t* w = (unit & 1) ? wb : wa;
+        int task = wave;
+        int j = task * JPW + (unit >> 1);
+        TfQ4kRow<ITERS> cur, nxt;
+        if (task < n_tasks)
+            tf_q4k_row_load<SPR, ITERS>(w + (size_t)j * col_bytes, j < n_cols, 0, nb, sir, t, cur);
+        if (xf) tf_quantize_to_lds(xf, nb, lds);
+        else tf_stage_q8(xq, xd, nb, lds);
+        const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+        for (; task < n_tasks; task += nwaves) {
+            const int nt = task + nwaves;
+            const int jn = nt * JPW + (unit >> 1);
+            if (nt < n_tasks)
+                tf_q4k_row_load<SPR, ITERS>(w + (size_t)jn * col_bytes, jn < n_cols, 0, nb, sir,
+                                            t, nxt);
+            float acc = tf_q4k_row_partial<SPR, ITERS>(cur, j < n_cols, 0, nb, sir, t, x);
+            acc = tf_group_sum<4 * SPR>(acc);
             const float other = __shfl(acc, (lane + 4 * SPR) & 63, 64);
-            if (valid && (unit & 1) == 0 && (lane & (4 * SPR - 1)) == 0) {
-                if (MODE == 0) {
-                    out_a[j] = (acc / (1.f + __expf(-acc))) * other;
-                } else {
-                    out_a[j] = acc;
-                    out_b[j] = other;
-                }
-            }
+            if (j < n_cols && (unit & 1) == 0 && (lane & (4 * SPR - 1)) == 0)
+                tf_pair_write<MODE>(acc, other, out_a, out_b, j);
+            cur = nxt;
+            j = jn;
         }
     } else {
-        for (int j = wave; j < n_cols; j += nwaves) {
-            const float g = tf_q4k_row_dot<SPR, ITERS>(wa + (size_t)j * col_bytes, true, 0,
-                                                       nb, sir, t, x);
-            const float u = tf_q4k_row_dot<SPR, ITERS>(wb + (size_t)j * col_bytes, true, 0,
-                                                       nb, sir, t, x);
-            if (lane == 0) {
-                if (MODE == 0) {
-                    out_a[j] = (g / (1.f + __expf(-g))) * u;
-                } else {
-                    out_a[j] = g;
-                    out_b[j] = u;
+        int j = wave;
+        TfQ4kRow<ITERS> cg, cu, ng, nu;
+        if (ITERS > 0 && j < n_cols) {
+            tf_q4k_row_load<SPR, ITERS>(wa + (size_t)j * col_bytes, true, 0, nb, sir, t, cg);
+            tf_q4k_row_load<SPR, ITERS>(wb + (size_t)j * col_bytes, true, 0, nb, sir, t, cu);
+        }
+        if (xf) tf_quantize_to_lds(xf, nb, lds);
+        else tf_stage_q8(xq, xd, nb, lds);
+        const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+        for (; j < n_cols; j += nwaves) {
+            const int jn = j + nwaves;
+            float g, u;
+            if constexpr (ITERS > 0) {
+                if (jn < n_cols) {
+                    tf_q4k_row_load<SPR, ITERS>(wa + (size_t)jn * col_bytes, true, 0, nb, sir, t, ng);
+                    tf_q4k_row_load<SPR, ITERS>(wb + (size_t)jn * col_bytes, true, 0, nb, sir, t, nu);
                 }
+                g = tf_q4k_row_partial<SPR, ITERS>(cg, true, 0, nb, sir, t, x);
+                u = tf_q4k_row_partial<SPR, ITERS>(cu, true, 0, nb, sir, t, x);
+            } else {
+                g = tf_q4k_row_partial_loop<SPR>(wa + (size_t)j * col_bytes, true, 0, nb, sir, t, x);
+                u = tf_q4k_row_partial_loop<SPR>(wb + (size_t)j * col_bytes, true, 0, nb, sir, t, x);
+            }
+            g = tf_group_sum<64>(g);
+            u = tf_group_sum<64>(u);
+            if (lane == 0) tf_pair_write<MODE>(g, u, out_a, out_b, j);
+            if constexpr (ITERS > 0) {
+                cg = ng;
+                cu = nu;
             }
         }
     }
@@ -144,8 +213,16 @@ __global__ __launch_bounds__(256) void tf_q4k_splitk_kernel(
         const int s = valid ? r / n_cols : 0;
         const int j = valid ? r - s * n_cols : 0;
         const int sb0 = (nb * s) / n_split, sb1 = (nb * (s + 1)) / n_split;
-        const float acc = tf_q4k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, sb0,
-                                                     sb1, sir, t, x);
+        const uint8_t* col = w + (size_t)j * col_bytes;
+        float acc;
+        if constexpr (ITERS > 0) {
+            TfQ4kRow<ITERS> rr;
+            tf_q4k_row_load<SPR, ITERS>(col, valid, sb0, sb1, sir, t, rr);
+            acc = tf_q4k_row_partial<SPR, ITERS>(rr, valid, sb0, sb1, sir, t, x);
+        } else {
+            acc = tf_q4k_row_partial_loop<SPR>(col, valid, sb0, sb1, sir, t, x);
+        }
+        acc = tf_group_sum<4 * SPR>(acc);
         if (valid && (lane & (4 * SPR - 1)) == 0) partial[(size_t)s * n_cols + j] = acc;
     }
 }
@@ -233,9 +310,9 @@ static bool tf_q4k_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 15) == 0 && (col_bytes & 15) == 0 && col_bytes >= nb * 144;
 }
 
-static int tf_q4k_rows(const TfQ4kMats& m, const int8_t* xq, const float* xd, int n_rows,
-                       int col_bytes, int use_bias, int use_res, const float* residual,
-                       tf_stream_t stream) {
+static int tf_q4k_rows(const TfQ4kMats& m, const int8_t* xq, const float* xd, const float* xf,
+                       int n_rows, int col_bytes, int use_bias, int use_res,
+                       const float* residual, tf_stream_t stream) {
     const int nb = n_rows / 256;
     const int n_total = m.n0 + m.n1 + m.n2;
     const int lds = tf_q8_lds_bytes(nb);
@@ -245,8 +322,8 @@ static int tf_q4k_rows(const TfQ4kMats& m, const int8_t* xq, const float* xd, in
         auto fn = tf_q4k_rows_kernel<SPR, IT>;
         const int tasks = (n_total + 16 / SPR - 1) / (16 / SPR);
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, xq, xd, nb,
-                           col_bytes, use_bias, use_res, residual);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, xq, xd, xf,
+                           nb, col_bytes, use_bias, use_res, residual);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -286,7 +363,20 @@ extern "C" int tf_gemv_q4k_q8(const uint8_t* w, const int8_t* xq, const float* x
     TF_CHECK_ARG(use_res != 1 || residual);
     TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
                 n_cols, 0, 0};
-    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, use_res, residual, stream);
+    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, use_res, residual, stream);
+}
+
+extern "C" int tf_gemv_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
+                               int n_cols, int col_bytes, int use_bias, const float* bias,
+                               int use_res, const float* residual, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q4k_weights_ok(w, nb, col_bytes));
+    TF_CHECK_ARG(x && out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
+    TF_CHECK_ARG(use_res != 1 || residual);
+    TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
+                n_cols, 0, 0};
+    return tf_q4k_rows(m, nullptr, nullptr, x, n_rows, col_bytes, use_bias, use_res, residual,
+                       stream);
 }
 
 extern "C" int tf_gemv_q4k_pair(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
@@ -298,7 +388,7 @@ extern "C" int tf_gemv_q4k_pair(const uint8_t* wa, const uint8_t* wb, const int8
     TF_CHECK_ARG(tf_q4k_weights_ok(wa, nb, col_bytes) && tf_q4k_weights_ok(wb, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && out_a && out_b && (!use_bias || (ba && bb)));
     TfQ4kMats m{wa, wb, nullptr, out_a, out_b, nullptr, ba, bb, nullptr, n_a, n_b, 0};
-    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, 0, nullptr, stream);
 }
 
 extern "C" int tf_gemv_q4k_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
@@ -312,7 +402,7 @@ extern "C" int tf_gemv_q4k_qkv(const uint8_t* wq, const uint8_t* wk, const uint8
                  tf_q4k_weights_ok(wv, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && q && k && v && (!use_bias || (bq && bk && bv)));
     TfQ4kMats m{wq, wk, wv, q, k, v, bq, bk, bv, n_q, n_k, n_v};
-    return tf_q4k_rows(m, xq, xd, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, 0, nullptr, stream);
 }
 
 extern "C" int tf_gemv_q4k_dual(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,

@@ -21,24 +21,43 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
     int col_bytes, int use_bias, const float* __restrict__ bias, int use_res,
     const float* __restrict__ residual) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_q6(xq, xd, nb, lds);
-    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
-    for (int r0 = wave * UNITS; r0 < n_cols; r0 += nwaves * UNITS) {
-        const int j = r0 + unit;
+    const int n_tasks = (n_cols + UNITS - 1) / UNITS;
+    int task = wave;
+    int j = task * UNITS + unit;
+    TfQ6kRow<ITERS> cur, nxt;
+    if (ITERS > 0 && task < n_tasks)
+        tf_q6k_row_load<SPR, ITERS>(w + (size_t)(j < n_cols ? j : 0) * col_bytes, j < n_cols, 0,
+                                    nb, sir, p, cur);
+    tf_stage_q6(xq, xd, nb, lds);
+    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
+    for (; task < n_tasks; task += nwaves) {
+        const int nt = task + nwaves;
+        const int jn = nt * UNITS + unit;
         const bool valid = j < n_cols;
-        float acc = tf_q6k_row_dot<SPR, ITERS>(w + (size_t)(valid ? j : 0) * col_bytes, valid, 0,
+        float acc;
+        if constexpr (ITERS > 0) {
+            if (nt < n_tasks)
+                tf_q6k_row_load<SPR, ITERS>(w + (size_t)(jn < n_cols ? jn : 0) * col_bytes,
+                                            jn < n_cols, 0, nb, sir, p, nxt);
+            acc = tf_q6k_row_partial<SPR, ITERS>(cur, valid, 0, nb, sir, p, x);
+        } else {
+            acc = tf_q6k_row_partial_loop<SPR>(w + (size_t)(valid ? j : 0) * col_bytes, valid, 0,
                                                nb, sir, p, x);
+        }
+        acc = tf_group_sum<4 * SPR>(acc);
         if (valid && (lane & (4 * SPR - 1)) == 0) {
             if (use_res == 1) acc += residual[j];
             else if (use_res == 2) acc += out[j];
             if (use_bias) acc += bias[j];
             out[j] = acc;
         }
+        if constexpr (ITERS > 0) cur = nxt;
+        j = jn;
     }
 }
 
@@ -62,8 +81,16 @@ __global__ __launch_bounds__(256) void tf_q6k_splitk_kernel(
         const int s = valid ? r / n_cols : 0;
         const int j = valid ? r - s * n_cols : 0;
         const int sb0 = (nb * s) / n_split, sb1 = (nb * (s + 1)) / n_split;
-        const float acc = tf_q6k_row_dot<SPR, ITERS>(w + (size_t)j * col_bytes, valid, sb0, sb1,
-                                                     sir, p, x);
+        const uint8_t* col = w + (size_t)j * col_bytes;
+        float acc;
+        if constexpr (ITERS > 0) {
+            TfQ6kRow<ITERS> rr;
+            tf_q6k_row_load<SPR, ITERS>(col, valid, sb0, sb1, sir, p, rr);
+            acc = tf_q6k_row_partial<SPR, ITERS>(rr, valid, sb0, sb1, sir, p, x);
+        } else {
+            acc = tf_q6k_row_partial_loop<SPR>(col, valid, sb0, sb1, sir, p, x);
+        }
+        acc = tf_group_sum<4 * SPR>(acc);
         if (valid && (lane & (4 * SPR - 1)) == 0) partial[(size_t)s * n_cols + j] = acc;
     }
 }

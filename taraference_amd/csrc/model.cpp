@@ -1,0 +1,327 @@
+// Decode-step runtime for dense Qwen2-style Q4_K_M models: the C++
+// restatement of the reference model runtime (cuda/forward.rs,
+// cuda/layer.rs, cuda/model.rs, cuda/kv.rs) for batch-1 greedy decode.
+//
+// Per token (layer.rs:99-709 attn_block, :1210-1456 ffn_block_dense,
+// :2125-2259 logits_from_last):
+//   x = embed(token)
+//   per layer: xb = rmsnorm(x) * attn_norm
+//              q, k = Wq xb + bq, Wk xb + bk        (Q4_K pair on Q8 xb)
+//              v = Wv xb + bv                        (f32 activation GEMV)
+//              rope(q), rope(k); K/V -> f16 cache at pos
+//              xb = flash_decode(q, K[0..pos], V[0..pos])
+//              x += Wo q8(xb)
+//              xb = rmsnorm(x) * ffn_norm
+//              hb = silu(Wg q8(xb)) * (Wu q8(xb))
+//              x += Wdown q8(hb)
+//   logits = lm_head q8(rmsnorm(x) * output_norm); next = argmax(logits)
+// The graph path keeps the position, the current token, the forced prompt
+// and the generated tokens in device memory (forward.rs:73-264), so a
+// captured step can be replayed back to back without host round trips.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <memory>
+#include <new>
+#include <vector>
+
+#include "op_api.hpp"
+#include "taraference_hip.h"
+
+namespace {
+
+using tf::GemvResidual;
+using tf::GpuMat;
+
+GpuMat to_mat(const tf_mat& m) {
+    GpuMat g;
+    g.data = m.data;
+    g.compact_data = m.compact;
+    g.n_rows = (size_t)m.n_rows;
+    g.n_cols = (size_t)m.n_cols;
+    g.col_bytes = (size_t)m.col_bytes;
+    g.compact_col_bytes = (size_t)m.compact_col_bytes;
+    g.wtype = m.type == TF_TYPE_Q6_K ? tf::WType::Q6K : tf::WType::Q4K;
+    return g;
+}
+
+struct Layer {
+    const float* attn_norm;
+    GpuMat wq, wk, wv, wo, gate, up, down;
+    const float *bq, *bk, *bv;
+    const float* ffn_norm;
+};
+
+// Advance the device-side decode state after one step: log the argmax,
+// select the next input token (forced prompt token or the argmax) and move
+// to the next position.
+__global__ void tf_decode_advance_kernel(int* pos, int* step, int* token, const int* argmax,
+                                         const int* forced, const int* n_forced, int* log) {
+    if (threadIdx.x != 0) return;
+    const int s = *step;
+    const int next = *argmax;
+    log[s] = next;
+    *token = (s + 1 < *n_forced) ? forced[s + 1] : next;
+    *pos += 1;
+    *step = s + 1;
+}
+
+template <class T>
+T* dev_alloc(size_t n) {
+    void* p = nullptr;
+    if (hipMalloc(&p, n * sizeof(T) + 256) != hipSuccess) throw std::bad_alloc();
+    return static_cast<T*>(p);
+}
+
+}  // namespace
+
+struct tf_model {
+    tf_model_config cfg{};
+    std::vector<Layer> layers;
+    GpuMat token_embd, output;
+    const float* output_norm = nullptr;
+    int embd_block_bytes = 210;
+    tf::FlashDims fd{};
+
+    // workspace (cuda/load.rs:502-607)
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr;
+    float *logits = nullptr, *flash_partial = nullptr, *gemv_partial = nullptr;
+    int8_t* q8_x = nullptr;
+    float* q8_d = nullptr;
+    size_t partial_stride = 0;
+    std::vector<uint16_t*> kc, vc;
+    // device decode state
+    int *d_pos = nullptr, *d_step = nullptr, *d_token = nullptr, *d_argmax = nullptr;
+    int *d_forced = nullptr, *d_nforced = nullptr, *d_log = nullptr;
+    std::vector<void*> allocs;
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    hipStream_t capture_stream = nullptr;
+
+    template <class T>
+    T* alloc(size_t n) {
+        T* p = dev_alloc<T>(n);
+        allocs.push_back(p);
+        return p;
+    }
+
+    ~tf_model() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (capture_stream) (void)hipStreamDestroy(capture_stream);
+        for (void* p : allocs) (void)hipFree(p);
+    }
+
+    // One decode step.  pos_dev == nullptr: host position `pos` and host
+    // token `token`; otherwise both are read from device memory.
+    void step(hipStream_t s, int token, int pos, bool device_state) {
+        const tf_model_config& c = cfg;
+        const int* pos_dev = device_state ? d_pos : nullptr;
+        const int* tok_dev = device_state ? d_token : nullptr;
+        tf::check(tf_embed_row(token_embd.data, embd_block_bytes, x, token, tok_dev, c.n_embd,
+                               (int)token_embd.col_bytes, s),
+                  "embed");
+        const int stride = c.n_kv * c.head_dim;
+        for (size_t li = 0; li < layers.size(); li++) {
+            const Layer& L = layers[li];
+            // ---- attention block
+            tf::check(tf_rms_norm(x, L.attn_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
+            if (!tf::try_gemv_qkv(s, L.wq, L.wk, L.wv, xb, q, k, v, L.bq, L.bk, L.bv, q8_x, q8_d)) {
+                if (tf::try_gemv_pair(s, L.wq, L.wk, xb, q, k, L.bq, L.bk, q8_x, q8_d)) {
+                    tf::gemv(s, L.wv, xb, v, L.bv, GemvResidual::none(), gemv_partial,
+                             partial_stride);
+                } else {
+                    tf::gemv(s, L.wq, xb, q, L.bq, GemvResidual::none(), gemv_partial, partial_stride);
+                    tf::gemv(s, L.wk, xb, k, L.bk, GemvResidual::none(), gemv_partial, partial_stride);
+                    tf::gemv(s, L.wv, xb, v, L.bv, GemvResidual::none(), gemv_partial, partial_stride);
+                }
+            }
+            tf::check(tf_rope_neox(q, c.n_head, c.head_dim, pos, pos_dev, c.rope_theta, s), "rope q");
+            tf::check(tf_rope_neox(k, c.n_kv, c.head_dim, pos, pos_dev, c.rope_theta, s), "rope k");
+            tf::check(tf_copy_kv_f16(k, kc[li], pos, pos_dev, stride, s), "copy k");
+            tf::check(tf_copy_kv_f16(v, vc[li], pos, pos_dev, stride, s), "copy v");
+            tf::launch_attn_flash(s, fd, q, kc[li], vc[li], flash_partial, xb, pos, pos_dev);
+            if (!tf::try_gemv_global_q8(s, L.wo, xb, x, nullptr, GemvResidual::in_place(), q8_x,
+                                        q8_d, gemv_partial, partial_stride))
+                tf::gemv(s, L.wo, xb, x, nullptr, GemvResidual::in_place(), gemv_partial,
+                         partial_stride);
+            // ---- FFN block
+            tf::check(tf_rms_norm(x, L.ffn_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
+            if (!tf::try_gemv_q4_ffn(s, L.gate, L.up, xb, hb, q8_x, q8_d))
+                throw tf::HipError(1, "ffn gate/up must be Q4_K");
+            if (!tf::try_gemv_global_q8(s, L.down, hb, x, nullptr, GemvResidual::in_place(), q8_x,
+                                        q8_d, gemv_partial, partial_stride))
+                tf::gemv(s, L.down, hb, x, nullptr, GemvResidual::in_place(), gemv_partial,
+                         partial_stride);
+        }
+        // ---- logits + argmax
+        tf::check(tf_rms_norm(x, output_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
+        if (!tf::try_gemv_global_q8(s, output, xb, logits, nullptr, GemvResidual::none(), q8_x,
+                                    q8_d, gemv_partial, partial_stride))
+            tf::gemv(s, output, xb, logits, nullptr, GemvResidual::none(), gemv_partial,
+                     partial_stride);
+        tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
+        if (device_state) {
+            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
+                               d_token, d_argmax, d_forced, d_nforced, d_log);
+            tf::check((int)hipGetLastError(), "advance");
+        }
+    }
+
+    void capture() {
+        if (graph_exec) return;
+        if (!capture_stream) tf::check((int)hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking), "stream");
+        tf::check((int)hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal), "capture");
+        try {
+            step(capture_stream, 0, 0, true);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(capture_stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        tf::check((int)hipStreamEndCapture(capture_stream, &graph), "end capture");
+        tf::check((int)hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "instantiate");
+    }
+
+    // Runs n_forced + n_gen steps from position pos0 with device-resident
+    // state; tokens[i] = argmax of step n_forced - 1 + i.
+    void run(hipStream_t s, const int* forced, int n_forced, int pos0, int n_gen, int* tokens,
+             bool use_graph) {
+        const int total = n_forced + n_gen;
+        if (n_forced < 1 || pos0 < 0 || pos0 + total > cfg.max_seq)
+            throw tf::HipError(1, "decode range outside the KV cache");
+        std::vector<int> h(4);
+        h[0] = pos0;
+        h[1] = 0;
+        h[2] = forced[0];
+        h[3] = n_forced;
+        tf::check((int)hipMemcpyAsync(d_forced, forced, sizeof(int) * n_forced,
+                                      hipMemcpyHostToDevice, s), "copy prompt");
+        tf::check((int)hipMemcpyAsync(d_pos, &h[0], sizeof(int), hipMemcpyHostToDevice, s), "copy");
+        tf::check((int)hipMemcpyAsync(d_step, &h[1], sizeof(int), hipMemcpyHostToDevice, s), "copy");
+        tf::check((int)hipMemcpyAsync(d_token, &h[2], sizeof(int), hipMemcpyHostToDevice, s), "copy");
+        tf::check((int)hipMemcpyAsync(d_nforced, &h[3], sizeof(int), hipMemcpyHostToDevice, s), "copy");
+        if (use_graph) capture();
+        for (int i = 0; i < total; i++) {
+            if (use_graph) tf::check((int)hipGraphLaunch(graph_exec, s), "graph launch");
+            else step(s, 0, 0, true);
+        }
+        if (n_gen > 0 && tokens)
+            tf::check((int)hipMemcpyAsync(tokens, d_log + n_forced - 1, sizeof(int) * n_gen,
+                                          hipMemcpyDeviceToHost, s), "copy tokens");
+        tf::check((int)hipStreamSynchronize(s), "sync");
+    }
+};
+
+extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layers,
+                               const tf_mat* token_embd, const tf_mat* output,
+                               const float* output_norm, tf_model** out) {
+    if (!cfg || !layers || !token_embd || !output || !output_norm || !out) return (int)hipErrorInvalidValue;
+    const tf_model_config& c = *cfg;
+    if (c.n_layer <= 0 || c.n_embd % 256 || c.n_ff % 256 || c.n_head <= 0 || c.n_kv <= 0 ||
+        c.n_head % c.n_kv || c.n_head * c.head_dim != c.n_embd || c.max_seq <= 0 || c.n_vocab <= 0)
+        return (int)hipErrorInvalidValue;
+    try {
+        std::unique_ptr<tf_model> m(new tf_model());
+        m->cfg = c;
+        for (int i = 0; i < c.n_layer; i++) {
+            const tf_layer& L = layers[i];
+            Layer l;
+            l.attn_norm = L.attn_norm;
+            l.ffn_norm = L.ffn_norm;
+            l.wq = to_mat(L.wq);
+            l.wk = to_mat(L.wk);
+            l.wv = to_mat(L.wv);
+            l.wo = to_mat(L.wo);
+            l.gate = to_mat(L.gate);
+            l.up = to_mat(L.up);
+            l.down = to_mat(L.down);
+            l.bq = L.bq;
+            l.bk = L.bk;
+            l.bv = L.bv;
+            m->layers.push_back(l);
+        }
+        m->token_embd = to_mat(*token_embd);
+        m->embd_block_bytes = token_embd->type == TF_TYPE_Q6_K ? 210 : 144;
+        m->output = to_mat(*output);
+        m->output_norm = output_norm;
+        const int n_split = tf_flash_decode_n_split(c.n_kv, c.max_seq);
+        m->fd = {c.n_head, c.n_kv, c.head_dim, n_split, 1.0f / std::sqrt((float)c.head_dim)};
+        const size_t widest = std::max<size_t>(std::max(c.n_ff, c.n_embd), c.n_vocab);
+        m->x = m->alloc<float>(c.n_embd);
+        m->xb = m->alloc<float>(c.n_embd);
+        m->q = m->alloc<float>(c.n_embd);
+        m->k = m->alloc<float>(c.n_kv * c.head_dim);
+        m->v = m->alloc<float>(c.n_kv * c.head_dim);
+        m->hb = m->alloc<float>(c.n_ff);
+        m->logits = m->alloc<float>(c.n_vocab);
+        m->q8_x = m->alloc<int8_t>(std::max(c.n_ff, c.n_embd));
+        m->q8_d = m->alloc<float>(std::max(c.n_ff, c.n_embd) / 32);
+        m->partial_stride = widest;
+        m->gemv_partial = m->alloc<float>(8 * widest);
+        m->flash_partial = m->alloc<float>((size_t)c.n_head * n_split * (2 + c.head_dim));
+        const size_t kv_elems = (size_t)c.max_seq * c.n_kv * c.head_dim;
+        for (int i = 0; i < c.n_layer; i++) {
+            m->kc.push_back(m->alloc<uint16_t>(kv_elems));
+            m->vc.push_back(m->alloc<uint16_t>(kv_elems));
+        }
+        m->d_pos = m->alloc<int>(1);
+        m->d_step = m->alloc<int>(1);
+        m->d_token = m->alloc<int>(1);
+        m->d_argmax = m->alloc<int>(1);
+        m->d_nforced = m->alloc<int>(1);
+        m->d_forced = m->alloc<int>(c.max_seq);
+        m->d_log = m->alloc<int>(c.max_seq);
+        *out = m.release();
+        return 0;
+    } catch (const tf::HipError& e) {
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        return (int)hipErrorOutOfMemory;
+    }
+}
+
+extern "C" void tf_model_destroy(tf_model* m) { delete m; }
+
+extern "C" int tf_model_forward(tf_model* m, int token, int pos, int* next_token,
+                                tf_stream_t stream) {
+    if (!m || token < 0 || token >= m->cfg.n_vocab || pos < 0 || pos >= m->cfg.max_seq)
+        return (int)hipErrorInvalidValue;
+    try {
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        m->step(s, token, pos, false);
+        if (next_token) {
+            tf::check((int)hipMemcpyAsync(next_token, m->d_argmax, sizeof(int),
+                                          hipMemcpyDeviceToHost, s), "copy");
+            tf::check((int)hipStreamSynchronize(s), "sync");
+        }
+        return 0;
+    } catch (const tf::HipError& e) {
+        return e.code;
+    }
+}
+
+extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, int pos0,
+                                 int n_gen, int* tokens, int use_graph, tf_stream_t stream) {
+    if (!m || !forced || n_forced < 1 || n_gen < 0) return (int)hipErrorInvalidValue;
+    for (int i = 0; i < n_forced; i++)
+        if (forced[i] < 0 || forced[i] >= m->cfg.n_vocab) return (int)hipErrorInvalidValue;
+    try {
+        m->run(reinterpret_cast<hipStream_t>(stream), forced, n_forced, pos0, n_gen, tokens,
+               use_graph != 0);
+        return 0;
+    } catch (const tf::HipError& e) {
+        return e.code;
+    }
+}
+
+extern "C" const float* tf_model_logits(const tf_model* m) { return m ? m->logits : nullptr; }
+extern "C" uint16_t* tf_model_k_cache(const tf_model* m, int li) {
+    return (m && li >= 0 && li < (int)m->kc.size()) ? m->kc[li] : nullptr;
+}
+extern "C" uint16_t* tf_model_v_cache(const tf_model* m, int li) {
+    return (m && li >= 0 && li < (int)m->vc.size()) ? m->vc[li] : nullptr;
+}

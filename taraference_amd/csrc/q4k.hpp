@@ -82,7 +82,8 @@ __device__ __forceinline__ void tf_stage_q8(const int8_t* __restrict__ xq,
 
 // Quantize an f32 activation (nb*256 values) straight into LDS, bit-identical
 // to tf_quantize_q8 (kernels/gemv.cu:16-40 quantize_q8_smem).  Each wave
-// quantizes two 32-value groups per step.  Ends with a barrier.
+// quantizes two 32-value groups per step (lanes 0-31 / 32-63); the loads of
+// eight steps are issued before any of them is used.  Ends with a barrier.
 __device__ __forceinline__ void tf_quantize_to_lds(const float* __restrict__ x,
                                                    int nb, uint8_t* lds) {
     int8_t* q8s = reinterpret_cast<int8_t*>(lds);
@@ -90,25 +91,40 @@ __device__ __forceinline__ void tf_quantize_to_lds(const float* __restrict__ x,
     float* dss = reinterpret_cast<float*>(lds + nb * 256 + nb * 32);
     const int groups = nb * 8;
     const int lane = threadIdx.x & 63;
-    const int half = lane >> 5;
     const int l32 = lane & 31;
     const int waves = blockDim.x >> 6;
-    for (int g0 = (threadIdx.x >> 6) * 2; g0 < groups; g0 += waves * 2) {
-        const int g = g0 + half;  // groups is a multiple of 8: always valid
-        const float xi = x[g * 32 + l32];
-        const float amax = tf_group32_max(fabsf(xi));
-        const float d = amax * (1.0f / 127.0f);
-        const int q = tf_q8_value(xi, amax, d);
-        q8s[g * 32 + l32] = (int8_t)q;
-        int s = q;
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        s += __shfl_xor(s, 8, 64);
-        s += __shfl_xor(s, 16, 64);
-        if (l32 == 0) {
-            d8s[g] = d;
-            dss[g] = d * (float)s;
+    const int gstep = 2 * waves;
+    const int g0 = (threadIdx.x >> 6) * 2 + (lane >> 5);
+    const int iters = (groups + gstep - 1) / gstep;
+    for (int i0 = 0; i0 < iters; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int g = g0 + gstep * (i0 + u);
+            v[u] = (i0 + u < iters && g < groups) ? x[g * 32 + l32] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (i0 + u < iters) {  // wave-uniform
+                const int g = g0 + gstep * (i0 + u);
+                const float xi = v[u];
+                const float amax = tf_group32_max(fabsf(xi));
+                const float d = amax * (1.0f / 127.0f);
+                const int q = tf_q8_value(xi, amax, d);
+                int s = q;
+                s += __shfl_xor(s, 1, 64);
+                s += __shfl_xor(s, 2, 64);
+                s += __shfl_xor(s, 4, 64);
+                s += __shfl_xor(s, 8, 64);
+                s += __shfl_xor(s, 16, 64);
+                if (g < groups) {
+                    q8s[g * 32 + l32] = (int8_t)q;
+                    if (l32 == 0) {
+                        d8s[g] = d;
+                        dss[g] = d * (float)s;
+                    }
+                }
+            }
         }
     }
     __syncthreads();
@@ -187,34 +203,51 @@ __device__ __forceinline__ float tf_q4k_part_dot(const TfQ4kPart& p, int t, int 
     return d * scale_term - dmin * min_term;
 }
 
-// Dot of one row (this lane's unit) over super-blocks [sb0, sb1) and the
-// reduction over the unit's 4*SPR lanes.  All lanes of the wave must call it
-// (the reduction uses DPP); `valid` masks a unit past the last row.
-// ITERS > 0: the loop is unrolled and all weight loads are issued first;
-// ITERS == 0: runtime loop.
+// Row dot split into a load phase and a compute phase so that kernels can
+// keep the next task's weights in flight while computing the current one.
+// A unit's lanes cover super-blocks sb0+sir, sb0+sir+SPR, ... < sb1; ITERS
+// is ceil(max range / SPR) and bounds the unrolled register set.
+template <int ITERS>
+struct TfQ4kRow {
+    TfQ4kPart p[ITERS];
+};
+
 template <int SPR, int ITERS>
-__device__ __forceinline__ float tf_q4k_row_dot(const uint8_t* __restrict__ col, bool valid,
+__device__ __forceinline__ void tf_q4k_row_load(const uint8_t* __restrict__ col, bool valid,
                                                 int sb0, int sb1, int sir, int t,
-                                                const TfQ8Lds& x) {
-    float acc = 0.f;
-    if constexpr (ITERS > 0) {
-        TfQ4kPart p[ITERS];
+                                                TfQ4kRow<ITERS>& r) {
 #pragma unroll
-        for (int i = 0; i < ITERS; i++) {
-            const int sb = sb0 + sir + i * SPR;
-            if (valid && sb < sb1) tf_q4k_load(col + (size_t)sb * 144, t, p[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < ITERS; i++) {
-            const int sb = sb0 + sir + i * SPR;
-            if (valid && sb < sb1) acc += tf_q4k_part_dot(p[i], t, sb, x);
-        }
-    } else {
-        for (int sb = sb0 + sir; valid && sb < sb1; sb += SPR) {
-            TfQ4kPart p;
-            tf_q4k_load(col + (size_t)sb * 144, t, p);
-            acc += tf_q4k_part_dot(p, t, sb, x);
-        }
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sb0 + sir + i * SPR;
+        if (valid && sb < sb1) tf_q4k_load(col + (size_t)sb * 144, t, r.p[i]);
     }
-    return tf_group_sum<4 * SPR>(acc);
+}
+
+// Sum of this lane's parts; reduce with tf_group_sum<4*SPR> afterwards (all
+// lanes of the wave must take part in that reduction).
+template <int SPR, int ITERS>
+__device__ __forceinline__ float tf_q4k_row_partial(const TfQ4kRow<ITERS>& r, bool valid,
+                                                    int sb0, int sb1, int sir, int t,
+                                                    const TfQ8Lds& x) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sb0 + sir + i * SPR;
+        if (valid && sb < sb1) acc += tf_q4k_part_dot(r.p[i], t, sb, x);
+    }
+    return acc;
+}
+
+// Runtime-length fallback for rows longer than the unrolled register set.
+template <int SPR>
+__device__ __forceinline__ float tf_q4k_row_partial_loop(const uint8_t* __restrict__ col,
+                                                         bool valid, int sb0, int sb1, int sir,
+                                                         int t, const TfQ8Lds& x) {
+    float acc = 0.f;
+    for (int sb = sb0 + sir; valid && sb < sb1; sb += SPR) {
+        TfQ4kPart p;
+        tf_q4k_load(col + (size_t)sb * 144, t, p);
+        acc += tf_q4k_part_dot(p, t, sb, x);
+    }
+    return acc;
 }

@@ -23,7 +23,7 @@ struct TfQ6kPart {
     tf_u32x4 a;   // ql[64n+16h ..]
     tf_u32x4 b;   // ql[64n+32+16h ..]
     tf_u32x4 hq;  // qh[32n+16h ..]
-    tf_u32x4 sc;  // scales[0..16)
+    tf_u32x2 sc;  // scales[8n .. 8n+8)
     uint32_t d;   // bytes 208..211 (d in the low half)
 };
 
@@ -33,7 +33,7 @@ __device__ __forceinline__ void tf_q6k_load_c(const uint8_t* blk, int p, TfQ6kPa
     q.a = tf_ld16_a4(blk + 64 * n + 16 * h);
     q.b = tf_ld16_a4(blk + 64 * n + 32 + 16 * h);
     q.hq = tf_ld16_a4(blk + 128 + 32 * n + 16 * h);
-    q.sc = tf_ld16_a4(blk + 192);
+    q.sc = tf_ld8_a4(blk + 192 + 8 * n);
     q.d = *reinterpret_cast<const uint32_t*>(blk + 208);
 }
 
@@ -52,7 +52,8 @@ __device__ __forceinline__ void tf_q6k_load_r(const uint8_t* blk, int p, TfQ6kPa
     q.a = tf_ld16_a2(blk + 64 * n + 16 * h);
     q.b = tf_ld16_a2(blk + 64 * n + 32 + 16 * h);
     q.hq = tf_ld16_a2(blk + 128 + 32 * n + 16 * h);
-    q.sc = tf_ld16_a2(blk + 192);
+    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * n);
+    q.sc = tf_u32x2{s2[0] | ((uint32_t)s2[1] << 16), s2[2] | ((uint32_t)s2[3] << 16)};
     q.d = reinterpret_cast<const uint16_t*>(blk + 208)[0];
 }
 
@@ -70,10 +71,8 @@ __device__ __forceinline__ uint32_t tf_q6k_word(const TfQ6kPart& q, int k, int i
 
 // Signed scale of value group k for lane part p.
 __device__ __forceinline__ int tf_q6k_scale(const TfQ6kPart& q, int p, int k) {
-    const int n = p >> 1, h = p & 1;
-    const uint32_t lo = n ? q.sc.z : q.sc.x;  // scales 8n .. 8n+3
-    const uint32_t hi = n ? q.sc.w : q.sc.y;  // scales 8n+4 .. 8n+7
-    const uint32_t w = k < 2 ? lo : hi;
+    const int h = p & 1;
+    const uint32_t w = k < 2 ? q.sc.x : q.sc.y;  // scales 8n..8n+3 / 8n+4..8n+7
     const int shift = 8 * h + 16 * (k & 1);
     return (int)__builtin_amdgcn_sbfe(w, shift, 8);
 }
@@ -161,29 +160,44 @@ __device__ __forceinline__ float tf_q6k_part_dot(const TfQ6kPart& q, int p, int 
     return d * acc;
 }
 
+template <int ITERS>
+struct TfQ6kRow {
+    TfQ6kPart q[ITERS];
+};
+
 template <int SPR, int ITERS>
-__device__ __forceinline__ float tf_q6k_row_dot(const uint8_t* __restrict__ col, bool valid,
+__device__ __forceinline__ void tf_q6k_row_load(const uint8_t* __restrict__ col, bool valid,
                                                 int sb0, int sb1, int sir, int p,
-                                                const TfQ6Lds& x) {
-    float acc = 0.f;
-    if constexpr (ITERS > 0) {
-        TfQ6kPart q[ITERS];
+                                                TfQ6kRow<ITERS>& r) {
 #pragma unroll
-        for (int i = 0; i < ITERS; i++) {
-            const int sb = sb0 + sir + i * SPR;
-            if (valid && sb < sb1) tf_q6k_load_c(col + (size_t)sb * 212, p, q[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < ITERS; i++) {
-            const int sb = sb0 + sir + i * SPR;
-            if (valid && sb < sb1) acc += tf_q6k_part_dot(q[i], p, sb, x);
-        }
-    } else {
-        for (int sb = sb0 + sir; valid && sb < sb1; sb += SPR) {
-            TfQ6kPart q;
-            tf_q6k_load_c(col + (size_t)sb * 212, p, q);
-            acc += tf_q6k_part_dot(q, p, sb, x);
-        }
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sb0 + sir + i * SPR;
+        if (valid && sb < sb1) tf_q6k_load_c(col + (size_t)sb * 212, p, r.q[i]);
     }
-    return tf_group_sum<4 * SPR>(acc);
+}
+
+template <int SPR, int ITERS>
+__device__ __forceinline__ float tf_q6k_row_partial(const TfQ6kRow<ITERS>& r, bool valid,
+                                                    int sb0, int sb1, int sir, int p,
+                                                    const TfQ6Lds& x) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sb0 + sir + i * SPR;
+        if (valid && sb < sb1) acc += tf_q6k_part_dot(r.q[i], p, sb, x);
+    }
+    return acc;
+}
+
+template <int SPR>
+__device__ __forceinline__ float tf_q6k_row_partial_loop(const uint8_t* __restrict__ col,
+                                                         bool valid, int sb0, int sb1, int sir,
+                                                         int p, const TfQ6Lds& x) {
+    float acc = 0.f;
+    for (int sb = sb0 + sir; valid && sb < sb1; sb += SPR) {
+        TfQ6kPart q;
+        tf_q6k_load_c(col + (size_t)sb * 212, p, q);
+        acc += tf_q6k_part_dot(q, p, sb, x);
+    }
+    return acc;
 }

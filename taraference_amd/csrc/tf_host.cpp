@@ -80,6 +80,7 @@ static const char* const k_symbols[] = {
     "tf_gemv_q4k_dual",
     "tf_gemv_q4k_ffn",
     "tf_gemv_q4k_ffn_f32",
+    "tf_gemv_q4k_f32",
     "tf_gemv_q4k_qkv",
     "tf_gemv_q6k_compact_q8",
     "tf_gemv_q6k_down_splitk",
@@ -90,6 +91,18 @@ static const char* const k_symbols[] = {
     "tf_flash_decode_partial_d",
     "tf_flash_decode_reduce",
     "tf_flash_decode_n_split",
+    "tf_embed_row",
+    "tf_rms_norm",
+    "tf_rope_neox",
+    "tf_copy_kv_f16",
+    "tf_argmax",
+    "tf_model_create",
+    "tf_model_destroy",
+    "tf_model_forward",
+    "tf_model_generate",
+    "tf_model_logits",
+    "tf_model_k_cache",
+    "tf_model_v_cache",
     "tf_q4k_block_dots",
     "tf_q6k_block_dots",
 };

@@ -97,3 +97,61 @@ def activation(rng, n: int) -> np.ndarray:
 def kv_cache(rng, seq: int, n_kv: int, head_dim: int) -> np.ndarray:
     """f16 cache [seq, n_kv*head_dim] ~ N(0,1), returned as uint16 bits."""
     return rng.standard_normal((seq, n_kv * head_dim)).astype(np.float16).view(np.uint16)
+
+
+# --------------------------------------------------------------- whole model
+
+QWEN25_3B = dict(n_layer=36, n_embd=2048, n_ff=11008, n_head=16, n_kv=2, head_dim=128,
+                 n_vocab=151936, rope_theta=1e6, rms_eps=1e-6)
+QWEN25_7B = dict(n_layer=28, n_embd=3584, n_ff=18944, n_head=28, n_kv=4, head_dim=128,
+                 n_vocab=152064, rope_theta=1e6, rms_eps=1e-6)
+
+
+def down_is_q6k(layer: int) -> bool:
+    """Q4_K_M placement used for the synthetic models: ffn_down is Q6_K on
+    odd layers (alternate layers), Q4_K on even ones."""
+    return layer % 2 == 1
+
+
+def qwen_layer(rng, cfg: dict, layer: int) -> dict:
+    """Random-init weights of one dense Qwen2 layer in the Q4_K_M mix:
+    Q4_K for q/k/o/gate/up, Q6_K for v, Q6_K or Q4_K for down; norms = 1,
+    q/k/v biases ~ N(0, 0.02)."""
+    e, f = cfg["n_embd"], cfg["n_ff"]
+    nq = cfg["n_head"] * cfg["head_dim"]
+    nkv = cfg["n_kv"] * cfg["head_dim"]
+    L = {}
+    L["attn_norm"] = np.ones(e, np.float32)
+    L["ffn_norm"] = np.ones(e, np.float32)
+    L["wq"] = q4k_matrix(rng, e, nq)
+    L["wk"] = q4k_matrix(rng, e, nkv)
+    L["wv"] = q6k_matrix(rng, e, nkv)
+    L["bq"] = (rng.standard_normal(nq) * 0.02).astype(np.float32)
+    L["bk"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
+    L["bv"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
+    L["wo"] = q4k_matrix(rng, nq, e)
+    L["gate"] = q4k_matrix(rng, e, f)
+    L["up"] = q4k_matrix(rng, e, f)
+    L["down"] = q6k_matrix(rng, f, e) if down_is_q6k(layer) else q4k_matrix(rng, f, e)
+    L["down_q6k"] = down_is_q6k(layer)
+    return L
+
+
+def qwen_embedding(rng, cfg: dict):
+    """Tied token embedding / lm_head: Q6_K [n_vocab, n_embd]."""
+    return q6k_matrix(rng, cfg["n_embd"], cfg["n_vocab"])
+
+
+def weight_bytes(cfg: dict) -> int:
+    """GGUF bytes streamed per decode token (lm_head counted once, embedding
+    row not counted)."""
+    e, f, hd = cfg["n_embd"], cfg["n_ff"], cfg["head_dim"]
+    nq, nkv = cfg["n_head"] * hd, cfg["n_kv"] * hd
+    q4 = lambda k, n: n * (k // 256) * Q4K_BYTES  # noqa: E731
+    q6 = lambda k, n: n * (k // 256) * Q6K_BYTES  # noqa: E731
+    tot = 0
+    for li in range(cfg["n_layer"]):
+        tot += q4(e, nq) + q4(e, nkv) + q6(e, nkv) + q4(nq, e) + 2 * q4(e, f)
+        tot += q6(f, e) if down_is_q6k(li) else q4(f, e)
+    tot += q6(e, cfg["n_vocab"])
+    return tot

@@ -13,7 +13,7 @@ HEADER = ROOT / "include" / "taraference_hip.h"
 
 def header_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(tf_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^[A-Za-z][\w \*]*?\b(tf_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
