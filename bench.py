@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark: batch-1 greedy decode of a random-init Qwen2.5-3B-shaped
+Q4_K_M model on one MI355X, plus the kernel roofline
+(config 1a, the fused Q4_K gate+up GEMV, the largest per-layer kernel) and
+the CPU-oracle baseline timed on this host.
+
+Workload: --warmup W forced decode steps build the synthetic context
+(W = 512 by default, the config's context), then --steps K greedy decode
+steps are timed (K = 256 by default).  Each step is one full decode forward
+(36 layers + lm_head + argmax) replayed from a captured HIP graph; the token
+feeds back on the device and the K generated tokens are copied to the host
+once at the end.  value = K / elapsed.
+
+Prints one JSON line on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "batch-1 decode tok/s, Qwen2.5-3B-shape Q4_K_M; Q4_K GEMV % of HBM peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(cfg, seed, max_seq):
+    from taraference_amd import synth
+    from taraference_amd.model import DecodeModel
+
+    rng = np.random.default_rng(seed)
+    t0 = time.time()
+    layers = (synth.qwen_layer(rng, cfg, li) for li in range(cfg["n_layer"]))
+    emb = synth.qwen_embedding(rng, cfg)
+    m = DecodeModel(dict(cfg, max_seq=max_seq), layers, emb)
+    log(f"[bench] model built in {time.time() - t0:.1f}s")
+    return m
+
+
+def decode_throughput(m, cfg, warmup, steps, seed):
+    import torch
+
+    rng = np.random.default_rng(seed + 1)
+    prompt = rng.integers(0, cfg["n_vocab"], max(1, warmup)).tolist()
+    # untimed: the forced context (graph capture happens on the first call)
+    first = m.generate(prompt, 1, pos0=0, use_graph=True)
+    torch.cuda.synchronize()
+    # timed: `steps` decode steps continuing from the greedy token
+    t0 = time.perf_counter()
+    toks = m.generate([int(first[0])], steps - 1, pos0=len(prompt), use_graph=True)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return dt, toks
+
+
+def kernel_roofline(iters):
+    """Config 1a: fused gate+up 2048 -> 2 x 11008 with the Q8 activation
+    prepared by tf_quantize_q8 (the decode runtime's path)."""
+    from taraference_amd import benchkit as B
+
+    r = B.report("q4k_gate_up", B.case_q4k_ffn(2048, 11008, 1, iters, f32_x=False))
+    return r
+
+
+def kernel_table(iters):
+    from taraference_amd import benchkit as B
+
+    rows = [
+        ("cfg0_q4k_896x4864", lambda: B.case_q4k_gemv(896, 4864, 0, iters)),
+        ("cfg1a_q4k_gate_up_2048x2x11008", lambda: B.case_q4k_ffn(2048, 11008, 1, iters, False)),
+        ("cfg1b_q6k_down_11008x2048", lambda: B.case_q6k(11008, 2048, 2, iters)),
+        ("cfg1c_q4k_qkv_2048x2560", lambda: B.case_q4k_qkv(2048, 2048, 256, 3, iters)),
+        ("lm_head_q6k_2048x151936", lambda: B.case_q6k(2048, 151936, 6, max(10, iters // 4),
+                                                       "tf_gemv_q6k_compact_q8", 0)),
+    ]
+    for L in (512, 4096, 32768):
+        rows.append((f"cfg2_flash_L{L}_split8", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters, 8)))
+        rows.append((f"cfg2_flash_L{L}_auto", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters)))
+    out = {}
+    for name, fn in rows:
+        r = B.report(name, fn())
+        out[name] = {"us": round(r["per_us"], 2), "us_b2b": round(r["b2b_us"], 2),
+                     "MB": round(r["bytes"] / 1e6, 3), "GBs": round(r["gbs"], 1),
+                     "frac_hbm": round(r["frac"], 4)}
+        if "n_split" in r:
+            out[name]["n_split"] = r["n_split"]
+        log(f"[bench] {name}: {out[name]}")
+    return out
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """The oracle's Q4_K/Q6_K x Q8 dequant-and-dot (the reference arithmetic
+    restated in C) on the host cores, on a bounded sample of the decode step:
+    the GEMVs of one even (Q4_K down) and one odd (Q6_K down) layer plus the
+    lm_head, repeated while the budget lasts; tok/s is extrapolated to the 36
+    layers.  Attention is not included (0.1% of the bytes at L = 512)."""
+    import oracle
+    from taraference_amd import synth
+
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    threads = max(1, min(16, avail))
+    rng = np.random.default_rng(99)
+    e, f = cfg["n_embd"], cfg["n_ff"]
+    nq, nkv = cfg["n_head"] * cfg["head_dim"], cfg["n_kv"] * cfg["head_dim"]
+    x_e = synth.activation(rng, e)
+    x_f = synth.activation(rng, f)
+    qe, de = oracle.quantize_q8(x_e)
+    qf, df = oracle.quantize_q8(x_f)
+    wq, cb = synth.q4k_matrix(rng, e, nq + 2 * nkv)  # q, k (Q4_K) and v-sized rows
+    wo, _ = synth.q4k_matrix(rng, nq, e)
+    g, _ = synth.q4k_matrix(rng, e, f)
+    u, _ = synth.q4k_matrix(rng, e, f)
+    d4, fcb = synth.q4k_matrix(rng, f, e)
+    d6raw, _ = synth.q6k_matrix(rng, f, e)
+    d6, d6cb = synth.q6k_compact(d6raw, f)
+    del d6raw
+    head_raw, _ = synth.q6k_matrix(rng, e, cfg["n_vocab"])
+    head, hcb = synth.q6k_compact(head_raw, e)
+    del head_raw
+
+    def layer_pair():
+        for down_q6 in (False, True):
+            oracle.gemv_q4k_q8_mt(wq, qe, de, e, nq + 2 * nkv, cb, threads)
+            oracle.gemv_q4k_q8_mt(wo, qe, de, nq, e, cb, threads)
+            oracle.gemv_q4k_ffn_mt(g, u, qe, de, e, f, cb, threads)
+            if down_q6:
+                oracle.gemv_q6k_compact_q8_kway_mt(d6, qf, df, f, e, d6cb, 8, threads)
+            else:
+                oracle.gemv_q4k_q8_mt(d4, qf, df, f, e, fcb, threads)
+
+    def lm_head():
+        oracle.gemv_q6k_compact_q8_kway_mt(head, qe, de, e, cfg["n_vocab"], hcb, 1, threads)
+
+    layer_pair()  # warm caches / threads
+    t_pairs, t_heads = [], []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(t_pairs) < 2:
+        t0 = time.perf_counter()
+        layer_pair()
+        t_pairs.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        lm_head()
+        t_heads.append(time.perf_counter() - t0)
+        if len(t_pairs) >= 20:
+            break
+    per_token = (cfg["n_layer"] / 2) * float(np.median(t_pairs)) + float(np.median(t_heads))
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle Q4_K/Q6_K x Q8 GEMVs of 2 layers (one Q4_K-down, one Q6_K-down)"
+                       f" + lm_head, {len(t_pairs)} reps, median, extrapolated to "
+                       f"{cfg['n_layer']} layers; attention excluded; CPU: {model}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=512)
+    ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the decode path is single-GPU; "
+              f"--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from taraference_amd import capi, synth
+
+    capi.load()
+    cfg = dict(synth.QWEN25_3B)
+    steps = max(2, args.steps)
+    max_seq = args.warmup + steps + 8
+    m = build_model(cfg, 0x7A7A0003, max_seq)
+    log("[bench] decode ...")
+    dt, toks = decode_throughput(m, cfg, args.warmup, steps, 3)
+    tok_s = steps / dt
+    log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    wbytes = synth.weight_bytes(cfg)
+    m.close()
+    del m
+    torch.cuda.empty_cache()
+
+    r = kernel_roofline(args.kernel_iters)
+    achieved = r["bytes"] / (r["per_us"] * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU)",
+            "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["per_us"], 3)}
+    table = {} if args.no_kernels else kernel_table(args.kernel_iters)
+    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k x q8 int8 dot, fp32 accumulate",
+        "data": "synthetic (random-init Qwen2.5-3B-shape Q4_K_M weights, seeded)",
+        "config": {"workload": "config 3: Qwen2.5-3B-shape Q4_K_M greedy decode, batch 1",
+                   "context": args.warmup, "decode_tokens": steps,
+                   "weight_bytes_per_token": wbytes,
+                   "effective_weight_GBs": round(wbytes * tok_s / 1e9, 1),
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": table,
+        "greedy_tokens_head": [int(t) for t in toks[:8]],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -219,6 +219,50 @@ int tf_copy_kv_f16(const float *src, uint16_t *cache, int pos,
  * (lowest index among exact ties). */
 int tf_argmax(const float *x, int n, int *out_idx, tf_stream_t stream);
 
+/* ------------------------------------------------------ fused decode kernels */
+/* Each fuses a chain of reference kernels that the reference launches back
+ * to back in its decode step; every stage keeps the arithmetic of its
+ * unfused counterpart (normalization and Q8 bytes are bit-identical, GEMV
+ * sums differ only in fp32 summation order). */
+
+/* layer.rs:171-645: rms_norm_f32 + quantize_q8 + gemv_q4_k_pair (Q, K, bias)
+ * + V projection (gemv_q6_k f32 activation when v_type is Q6_K, Q4_K x Q8
+ * otherwise; bias) + rope_neox_f32 on Q and K + copy_kv_f16 of K and V at
+ * position pos (or *pos_dev).  x is the residual stream (n_embd floats);
+ * norm_w may be NULL (no normalization).  q_out receives the rotated Q; the
+ * f16 K/V rows go to k_cache/v_cache [seq][n_kv*head_dim]. */
+int tf_fused_norm_qkv_rope_kv(const float *x, const float *norm_w, float eps,
+                              const uint8_t *wq, const uint8_t *wk,
+                              const uint8_t *wv, int v_type, const float *bq,
+                              const float *bk, const float *bv, int n_embd,
+                              int n_head, int n_kv, int head_dim,
+                              int col_bytes_qk, int col_bytes_v, float *q_out,
+                              uint16_t *k_cache, uint16_t *v_cache, int pos,
+                              const int *pos_dev, float theta,
+                              tf_stream_t stream);
+/* layer.rs:1220-1386: rms_norm_f32 (x * norm_w) + gemv_q4_k_ffn_mcol. */
+int tf_gemv_q4k_ffn_norm(const uint8_t *gate, const uint8_t *up,
+                         const float *x, const float *norm_w, float eps,
+                         float *out, int n_rows, int n_cols, int col_bytes,
+                         tf_stream_t stream);
+/* matmul.rs:191-223: quantize_q8 + the compact Q6_K GEMV (f32 activation
+ * quantized inside every workgroup); use_res 0 or 2 (in place). */
+int tf_gemv_q6k_compact_f32(const uint8_t *w, const float *x, float *out,
+                            int n_rows, int n_cols, int col_bytes, int use_res,
+                            tf_stream_t stream);
+/* layer.rs:2158-2257: rms_norm_f32 (when norm_w != NULL) + quantize_q8 +
+ * gemv_q6_k_compact_global (logits) + argmax_f32.  The argmax is
+ * accumulated into *amax_key, which must hold 0 at launch; read it with
+ * tf_argmax_key_finalize, which also resets it to 0. */
+int tf_gemv_q6k_head_argmax(const uint8_t *w, const float *x,
+                            const float *norm_w, float eps, float *logits,
+                            int n_rows, int n_cols, int col_bytes,
+                            unsigned long long *amax_key, tf_stream_t stream);
+/* *out_idx = index encoded in *amax_key (largest logit, lowest index among
+ * exact ties); *amax_key = 0. */
+int tf_argmax_key_finalize(unsigned long long *amax_key, int *out_idx,
+                           tf_stream_t stream);
+
 /* ----------------------------------------------------- decode-step runtime */
 /* C++ restatement of the reference model runtime for dense Qwen2-style
  * models (cuda/forward.rs:42-407, cuda/layer.rs:99-709,1210-1456,2125-2259,
@@ -269,7 +313,8 @@ void tf_model_destroy(tf_model *m);
  * host (blocks on the stream). */
 int tf_model_forward(tf_model *m, int token, int pos, int *next_token,
                      tf_stream_t stream);
-/* Runs n_forced + n_gen decode steps from position pos0 with the position,
+/* Runs n_forced + n_gen - 1 decode steps (n_forced if n_gen == 0) from
+ * position pos0 with the position,
  * token and outputs kept in device memory (forward.rs:73-264; replayed from
  * a captured HIP graph when use_graph).  Step i < n_forced consumes
  * forced[i] (a prompt fed through the decode path); later steps consume the
@@ -278,6 +323,11 @@ int tf_model_forward(tf_model *m, int token, int pos, int *next_token,
  * synchronized once, at the end. */
 int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
                       int n_gen, int *tokens, int use_graph, tf_stream_t stream);
+/* Select the kernel sequence of a step: fused != 0 (default) uses the fused
+ * decode kernels (six launches per layer); 0 uses the reference's sequence
+ * through the operator API (cuda/layer.rs order, one launch per reference
+ * kernel).  Both compute the same step. */
+int tf_model_set_path(tf_model *m, int fused);
 /* Device pointer of the last logits (n_vocab floats) and of the f16 K/V
  * cache of layer li. */
 const float *tf_model_logits(const tf_model *m);

@@ -39,6 +39,18 @@ SIGNATURES: dict[str, list] = {
     "tf_flash_decode_partial_d": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _F, _P],
     "tf_flash_decode_reduce": [_P, _P, _I, _I, _I, _I, _P],
     "tf_flash_decode_n_split": [_I, _I],
+    "tf_gemv_q4k_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q4k_ffn_norm": [_P, _P, _P, _P, _F, _P, _I, _I, _I, _P],
+    "tf_fused_norm_qkv_rope_kv": [_P, _P, _F, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
+                                  _I, _P, _P, _P, _I, _P, _F, _P],
+    "tf_gemv_q6k_compact_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_q6k_head_argmax": [_P, _P, _P, _F, _P, _I, _I, _I, _P, _P],
+    "tf_argmax_key_finalize": [_P, _P, _P],
+    "tf_embed_row": [_P, _I, _P, _I, _P, _I, _I, _P],
+    "tf_rms_norm": [_P, _P, _P, _I, _F, _P],
+    "tf_rope_neox": [_P, _I, _I, _I, _P, _F, _P],
+    "tf_copy_kv_f16": [_P, _P, _I, _P, _I, _P],
+    "tf_argmax": [_P, _I, _P, _P],
     "tf_q4k_block_dots": [_P, _P, _P, _P, _I, _I, _I, _P],
     "tf_q6k_block_dots": [_P, _I, _P, _P, _I, _I, _I, _P],
     "tf_version": [],
@@ -92,8 +104,19 @@ def stream_ptr(stream=None) -> int | None:
     return stream.cuda_stream or None
 
 
+# Entry points bound elsewhere with their own argtypes (taraference_amd/model.py).
+BOUND_ELSEWHERE = {"tf_model_create", "tf_model_destroy", "tf_model_forward",
+                   "tf_model_generate", "tf_model_set_path", "tf_model_logits",
+                   "tf_model_k_cache", "tf_model_v_cache", "tf_exported_symbol"}
+
+
 def call(name: str, *args) -> None:
-    """Call C-ABI entry point `name`; raise HipError on a non-zero status."""
+    """Call C-ABI entry point `name`; raise HipError on a non-zero status.
+
+    Only entry points with declared argument types may be called: without
+    them ctypes would pass device pointers as 32-bit C ints."""
+    if name not in SIGNATURES:
+        raise KeyError(f"{name} has no declared argtypes in capi.SIGNATURES")
     lib = load()
     rc = getattr(lib, name)(*args)
     if rc != 0:

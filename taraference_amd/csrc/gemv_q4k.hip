@@ -62,8 +62,7 @@ __device__ __forceinline__ TfRowSel tf_sel3(const TfQ4kMats& m, int r, int n_tot
 // Rows of up to three matrices that share K (global / pair / qkv).
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
-    TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-    const float* __restrict__ xf, int nb, int col_bytes, int use_bias, int use_res,
+    TfQ4kMats m, TfActSrc src, int nb, int col_bytes, int use_bias, int use_res,
     const float* __restrict__ residual) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int UNITS = 16 / SPR;
@@ -77,9 +76,8 @@ __global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
     TfRowSel cs = tf_sel3(m, task * UNITS + unit, n_total, col_bytes);
     TfQ4kRow<ITERS> cur, nxt;
     if (ITERS > 0 && task < n_tasks) tf_q4k_row_load<SPR, ITERS>(cs.col, cs.valid, 0, nb, sir, t, cur);
-    if (xf) tf_quantize_to_lds(xf, nb, lds);
-    else tf_stage_q8(xq, xd, nb, lds);
-    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    tf_stage_act<false>(src, nb, lds);
+    const TfAct x = tf_act_view(lds, nb);
     for (; task < n_tasks; task += nwaves) {
         const int nt = task + nwaves;
         const TfRowSel ns = tf_sel3(m, nt * UNITS + unit, n_total, col_bytes);
@@ -121,9 +119,8 @@ __device__ __forceinline__ void tf_pair_write(float g, float u, float* out_a, fl
 template <int SPR, int ITERS, int MODE>
 __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
     const uint8_t* __restrict__ wa, const uint8_t* __restrict__ wb,
-    const int8_t* __restrict__ xq, const float* __restrict__ xd,
-    const float* __restrict__ xf, float* __restrict__ out_a,
-    float* __restrict__ out_b, int nb, int n_cols, int col_bytes) {
+    TfActSrc src, float* __restrict__ out_a, float* __restrict__ out_b, int nb, int n_cols,
+    int col_bytes) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
@@ -139,9 +136,8 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
         TfQ4kRow<ITERS> cur, nxt;
         if (task < n_tasks)
             tf_q4k_row_load<SPR, ITERS>(w + (size_t)j * col_bytes, j < n_cols, 0, nb, sir, t, cur);
-        if (xf) tf_quantize_to_lds(xf, nb, lds);
-        else tf_stage_q8(xq, xd, nb, lds);
-        const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+        tf_stage_act<false>(src, nb, lds);
+        const TfAct x = tf_act_view(lds, nb);
         for (; task < n_tasks; task += nwaves) {
             const int nt = task + nwaves;
             const int jn = nt * JPW + (unit >> 1);
@@ -163,9 +159,8 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
             tf_q4k_row_load<SPR, ITERS>(wa + (size_t)j * col_bytes, true, 0, nb, sir, t, cg);
             tf_q4k_row_load<SPR, ITERS>(wb + (size_t)j * col_bytes, true, 0, nb, sir, t, cu);
         }
-        if (xf) tf_quantize_to_lds(xf, nb, lds);
-        else tf_stage_q8(xq, xd, nb, lds);
-        const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+        tf_stage_act<false>(src, nb, lds);
+        const TfAct x = tf_act_view(lds, nb);
         for (; j < n_cols; j += nwaves) {
             const int jn = j + nwaves;
             float g, u;
@@ -195,12 +190,11 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
 // [floor(nb*s/n_split), floor(nb*(s+1)/n_split)).
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(256) void tf_q4k_splitk_kernel(
-    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, float* __restrict__ partial, int nb,
+    const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ partial, int nb,
     int n_cols, int col_bytes, int n_split) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_q8(xq, xd, nb, lds);
-    const TfQ8Lds x = tf_q8_lds_view(lds, nb);
+    tf_stage_act<false>(src, nb, lds);
+    const TfAct x = tf_act_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
@@ -247,8 +241,8 @@ __global__ __launch_bounds__(256) void tf_q4k_block_dots_kernel(
     int32_t* __restrict__ dots, int32_t* __restrict__ sums, int nb, int n_cols,
     int col_bytes) {
     extern __shared__ __align__(16) uint8_t lds[];
-    int32_t* lsums = reinterpret_cast<int32_t*>(lds + tf_q8_lds_bytes(nb));
-    // Same copy-and-sum as tf_stage_q8; only the integer sums are kept.
+    int32_t* lsums = reinterpret_cast<int32_t*>(lds + nb * 256);
+    // Same copy-and-sum as tf_stage_act(TF_SRC_Q8); only the integer sums are kept.
     {
         int8_t* q8s = reinterpret_cast<int8_t*>(lds);
         for (int g = threadIdx.x; g < nb * 8; g += blockDim.x) {
@@ -310,31 +304,36 @@ static bool tf_q4k_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 15) == 0 && (col_bytes & 15) == 0 && col_bytes >= nb * 144;
 }
 
-static int tf_q4k_rows(const TfQ4kMats& m, const int8_t* xq, const float* xd, const float* xf,
-                       int n_rows, int col_bytes, int use_bias, int use_res,
-                       const float* residual, tf_stream_t stream) {
+static TfActSrc tf_src_q8(const int8_t* xq, const float* xd) {
+    return TfActSrc{TF_SRC_Q8, xq, xd, nullptr, nullptr, 0.f};
+}
+static TfActSrc tf_src_f32(const float* x) {
+    return TfActSrc{TF_SRC_F32, nullptr, nullptr, x, nullptr, 0.f};
+}
+
+static int tf_q4k_rows(const TfQ4kMats& m, const TfActSrc& src, int n_rows, int col_bytes,
+                       int use_bias, int use_res, const float* residual, tf_stream_t stream) {
     const int nb = n_rows / 256;
     const int n_total = m.n0 + m.n1 + m.n2;
-    const int lds = tf_q8_lds_bytes(nb);
+    const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q4k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         auto fn = tf_q4k_rows_kernel<SPR, IT>;
         const int tasks = (n_total + 16 / SPR - 1) / (16 / SPR);
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, xq, xd, xf,
-                           nb, col_bytes, use_bias, use_res, residual);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, src, nb,
+                           col_bytes, use_bias, use_res, residual);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
 }
 
-static int tf_q4k_pair_rows(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
-                            const float* xd, const float* xf, float* out_a, float* out_b,
-                            int n_rows, int n_cols, int col_bytes, int mode,
-                            tf_stream_t stream) {
+static int tf_q4k_pair_rows(const uint8_t* wa, const uint8_t* wb, const TfActSrc& src,
+                            float* out_a, float* out_b, int n_rows, int n_cols, int col_bytes,
+                            int mode, tf_stream_t stream) {
     const int nb = n_rows / 256;
-    const int lds = tf_q8_lds_bytes(nb);
+    const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q4k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
@@ -344,8 +343,8 @@ static int tf_q4k_pair_rows(const uint8_t* wa, const uint8_t* wb, const int8_t* 
         const int jpw = SPR <= 8 ? 16 / SPR / 2 : 1;
         const int tasks = (n_cols + jpw - 1) / jpw;
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), wa, wb, xq, xd,
-                           xf, out_a, out_b, nb, n_cols, col_bytes);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), wa, wb, src, out_a,
+                           out_b, nb, n_cols, col_bytes);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -363,7 +362,7 @@ extern "C" int tf_gemv_q4k_q8(const uint8_t* w, const int8_t* xq, const float* x
     TF_CHECK_ARG(use_res != 1 || residual);
     TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
                 n_cols, 0, 0};
-    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, use_res, residual, stream);
+    return tf_q4k_rows(m, tf_src_q8(xq, xd), n_rows, col_bytes, use_bias, use_res, residual, stream);
 }
 
 extern "C" int tf_gemv_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
@@ -375,8 +374,7 @@ extern "C" int tf_gemv_q4k_f32(const uint8_t* w, const float* x, float* out, int
     TF_CHECK_ARG(use_res != 1 || residual);
     TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
                 n_cols, 0, 0};
-    return tf_q4k_rows(m, nullptr, nullptr, x, n_rows, col_bytes, use_bias, use_res, residual,
-                       stream);
+    return tf_q4k_rows(m, tf_src_f32(x), n_rows, col_bytes, use_bias, use_res, residual, stream);
 }
 
 extern "C" int tf_gemv_q4k_pair(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
@@ -388,7 +386,7 @@ extern "C" int tf_gemv_q4k_pair(const uint8_t* wa, const uint8_t* wb, const int8
     TF_CHECK_ARG(tf_q4k_weights_ok(wa, nb, col_bytes) && tf_q4k_weights_ok(wb, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && out_a && out_b && (!use_bias || (ba && bb)));
     TfQ4kMats m{wa, wb, nullptr, out_a, out_b, nullptr, ba, bb, nullptr, n_a, n_b, 0};
-    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+    return tf_q4k_rows(m, tf_src_q8(xq, xd), n_rows, col_bytes, use_bias, 0, nullptr, stream);
 }
 
 extern "C" int tf_gemv_q4k_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
@@ -402,7 +400,7 @@ extern "C" int tf_gemv_q4k_qkv(const uint8_t* wq, const uint8_t* wk, const uint8
                  tf_q4k_weights_ok(wv, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && q && k && v && (!use_bias || (bq && bk && bv)));
     TfQ4kMats m{wq, wk, wv, q, k, v, bq, bk, bv, n_q, n_k, n_v};
-    return tf_q4k_rows(m, xq, xd, nullptr, n_rows, col_bytes, use_bias, 0, nullptr, stream);
+    return tf_q4k_rows(m, tf_src_q8(xq, xd), n_rows, col_bytes, use_bias, 0, nullptr, stream);
 }
 
 extern "C" int tf_gemv_q4k_dual(const uint8_t* wa, const uint8_t* wb, const int8_t* xq,
@@ -412,8 +410,8 @@ extern "C" int tf_gemv_q4k_dual(const uint8_t* wa, const uint8_t* wb, const int8
     TF_CHECK_ARG(nb > 0 && n_cols > 0);
     TF_CHECK_ARG(tf_q4k_weights_ok(wa, nb, col_bytes) && tf_q4k_weights_ok(wb, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && out_a && out_b);
-    return tf_q4k_pair_rows(wa, wb, xq, xd, nullptr, out_a, out_b, n_rows, n_cols, col_bytes,
-                            1, stream);
+    return tf_q4k_pair_rows(wa, wb, tf_src_q8(xq, xd), out_a, out_b, n_rows, n_cols, col_bytes, 1,
+                            stream);
 }
 
 extern "C" int tf_gemv_q4k_ffn(const uint8_t* gate, const uint8_t* up, const int8_t* xq,
@@ -423,8 +421,8 @@ extern "C" int tf_gemv_q4k_ffn(const uint8_t* gate, const uint8_t* up, const int
     TF_CHECK_ARG(nb > 0 && n_cols > 0);
     TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
     TF_CHECK_ARG(xq && xd && out);
-    return tf_q4k_pair_rows(gate, up, xq, xd, nullptr, out, nullptr, n_rows, n_cols, col_bytes,
-                            0, stream);
+    return tf_q4k_pair_rows(gate, up, tf_src_q8(xq, xd), out, nullptr, n_rows, n_cols, col_bytes, 0,
+                            stream);
 }
 
 extern "C" int tf_gemv_q4k_ffn_f32(const uint8_t* gate, const uint8_t* up, const float* x,
@@ -434,8 +432,19 @@ extern "C" int tf_gemv_q4k_ffn_f32(const uint8_t* gate, const uint8_t* up, const
     TF_CHECK_ARG(nb > 0 && n_cols > 0);
     TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
     TF_CHECK_ARG(x && out);
-    return tf_q4k_pair_rows(gate, up, nullptr, nullptr, x, out, nullptr, n_rows, n_cols,
-                            col_bytes, 0, stream);
+    return tf_q4k_pair_rows(gate, up, tf_src_f32(x), out, nullptr, n_rows, n_cols, col_bytes, 0,
+                            stream);
+}
+
+extern "C" int tf_gemv_q4k_ffn_norm(const uint8_t* gate, const uint8_t* up, const float* x,
+                                    const float* norm_w, float eps, float* out, int n_rows,
+                                    int n_cols, int col_bytes, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(nb > 0 && n_cols > 0);
+    TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
+    TF_CHECK_ARG(x && norm_w && out);
+    return tf_q4k_pair_rows(gate, up, TfActSrc{TF_SRC_NORM, nullptr, nullptr, x, norm_w, eps}, out,
+                            nullptr, n_rows, n_cols, col_bytes, 0, stream);
 }
 
 extern "C" int tf_gemv_q4k_q8_splitk(const uint8_t* w, const int8_t* xq, const float* xd,
@@ -444,7 +453,7 @@ extern "C" int tf_gemv_q4k_q8_splitk(const uint8_t* w, const int8_t* xq, const f
     const int nb = n_rows / 256;
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && n_split >= 1 && n_split <= 8);
     TF_CHECK_ARG(tf_q4k_weights_ok(w, nb, col_bytes) && xq && xd && partial);
-    const int lds = tf_q8_lds_bytes(nb);
+    const int lds = tf_act_lds_bytes(nb, false);
     const int len = (nb + n_split - 1) / n_split;
     int rc = 0;
     tf_q4k_dispatch(len, [&](auto spr, auto it) {
@@ -453,8 +462,8 @@ extern "C" int tf_gemv_q4k_q8_splitk(const uint8_t* w, const int8_t* xq, const f
         const long long total = (long long)n_split * n_cols;
         const int tasks = (int)((total + 16 / SPR - 1) / (16 / SPR));
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd,
-                           partial, nb, n_cols, col_bytes, n_split);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w,
+                           tf_src_q8(xq, xd), partial, nb, n_cols, col_bytes, n_split);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -478,7 +487,7 @@ extern "C" int tf_q4k_block_dots(const uint8_t* w, const int8_t* xq, int32_t* do
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q4k_weights_ok(w, nb, col_bytes));
     TF_CHECK_ARG(xq && ((uintptr_t)xq & 15) == 0 && dots && sums);
     const long long total = (long long)n_cols * nb * 4;
-    const int lds = tf_q8_lds_bytes(nb) + nb * 8 * 4;
+    const int lds = nb * 256 + nb * 8 * 4;
     hipLaunchKernelGGL(tf_q4k_block_dots_kernel, dim3((unsigned)((total + 255) / 256)),
                        dim3(256), lds, tf_stream(stream), w, xq, dots, sums, nb, n_cols,
                        col_bytes);

@@ -16,8 +16,7 @@
 
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
-    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, float* __restrict__ out, int nb, int n_cols,
+    const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ out, int nb, int n_cols,
     int col_bytes, int use_bias, const float* __restrict__ bias, int use_res,
     const float* __restrict__ residual) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -33,8 +32,8 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
     if (ITERS > 0 && task < n_tasks)
         tf_q6k_row_load<SPR, ITERS>(w + (size_t)(j < n_cols ? j : 0) * col_bytes, j < n_cols, 0,
                                     nb, sir, p, cur);
-    tf_stage_q6(xq, xd, nb, lds);
-    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
+    tf_stage_act<false>(src, nb, lds);
+    const TfAct x = tf_act_view(lds, nb);
     for (; task < n_tasks; task += nwaves) {
         const int nt = task + nwaves;
         const int jn = nt * UNITS + unit;
@@ -63,12 +62,11 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
 
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(256) void tf_q6k_splitk_kernel(
-    const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
-    const float* __restrict__ xd, float* __restrict__ partial, int nb, int n_cols,
-    int col_bytes, int n_split) {
+    const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ partial, int nb,
+    int n_cols, int col_bytes, int n_split) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_q6(xq, xd, nb, lds);
-    const TfQ6Lds x = tf_q6_lds_view(lds, nb);
+    tf_stage_act<false>(src, nb, lds);
+    const TfAct x = tf_act_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
@@ -234,22 +232,23 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212;
 }
 
-static int tf_q6k_rows(const uint8_t* w, const int8_t* xq, const float* xd, float* out,
-                       int n_rows, int n_cols, int col_bytes, int use_bias, const float* bias,
-                       int use_res, const float* residual, tf_stream_t stream) {
+static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_rows,
+                       int n_cols, int col_bytes, int use_bias, const float* bias, int use_res,
+                       const float* residual, tf_stream_t stream) {
     const int nb = n_rows / 256;
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q6c_weights_ok(w, nb, col_bytes));
-    TF_CHECK_ARG(xq && xd && out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
+    TF_CHECK_ARG(out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
     TF_CHECK_ARG(use_res != 1 || residual);
-    const int lds = tf_q6_lds_bytes(nb);
+    TF_CHECK_ARG(src.kind == TF_SRC_Q8 ? (src.xq && src.xd) : (src.x != nullptr));
+    const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q6k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         auto fn = tf_q6k_rows_kernel<SPR, IT>;
         const int tasks = (n_cols + 16 / SPR - 1) / (16 / SPR);
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd, out,
-                           nb, n_cols, col_bytes, use_bias, bias, use_res, residual);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, src, out, nb,
+                           n_cols, col_bytes, use_bias, bias, use_res, residual);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -261,8 +260,8 @@ extern "C" int tf_gemv_q6k_compact_q8(const uint8_t* w, const int8_t* xq, const 
                                       float* out, int n_rows, int n_cols, int col_bytes,
                                       int use_bias, const float* bias, int use_res,
                                       const float* residual, tf_stream_t stream) {
-    return tf_q6k_rows(w, xq, xd, out, n_rows, n_cols, col_bytes, use_bias, bias, use_res,
-                       residual, stream);
+    return tf_q6k_rows(w, TfActSrc{TF_SRC_Q8, xq, xd, nullptr, nullptr, 0.f}, out, n_rows, n_cols,
+                       col_bytes, use_bias, bias, use_res, residual, stream);
 }
 
 extern "C" int tf_gemv_q6k_down_splitk(const uint8_t* w, const int8_t* xq, const float* xd,
@@ -271,8 +270,8 @@ extern "C" int tf_gemv_q6k_down_splitk(const uint8_t* w, const int8_t* xq, const
                                        const float* residual, tf_stream_t stream) {
     // Full-K per row inside one wave: the reference's in-block 4/8-way merge
     // collapses into the wave reduction.
-    return tf_q6k_rows(w, xq, xd, out, n_rows, n_cols, col_bytes, use_bias, bias, use_res,
-                       residual, stream);
+    return tf_q6k_rows(w, TfActSrc{TF_SRC_Q8, xq, xd, nullptr, nullptr, 0.f}, out, n_rows, n_cols,
+                       col_bytes, use_bias, bias, use_res, residual, stream);
 }
 
 extern "C" int tf_gemv_q6k_compact_q8_splitk(const uint8_t* w, const int8_t* xq,
@@ -282,7 +281,7 @@ extern "C" int tf_gemv_q6k_compact_q8_splitk(const uint8_t* w, const int8_t* xq,
     const int nb = n_rows / 256;
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && n_split >= 1 && n_split <= 8);
     TF_CHECK_ARG(tf_q6c_weights_ok(w, nb, col_bytes) && xq && xd && partial);
-    const int lds = tf_q6_lds_bytes(nb);
+    const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q6k_dispatch((nb + n_split - 1) / n_split, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
@@ -290,8 +289,9 @@ extern "C" int tf_gemv_q6k_compact_q8_splitk(const uint8_t* w, const int8_t* xq,
         const long long total = (long long)n_split * n_cols;
         const int tasks = (int)((total + 16 / SPR - 1) / (16 / SPR));
         const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, xq, xd,
-                           partial, nb, n_cols, col_bytes, n_split);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w,
+                           TfActSrc{TF_SRC_Q8, xq, xd, nullptr, nullptr, 0.f}, partial, nb, n_cols,
+                           col_bytes, n_split);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;

@@ -57,10 +57,16 @@ struct Layer {
 // select the next input token (forced prompt token or the argmax) and move
 // to the next position.
 __global__ void tf_decode_advance_kernel(int* pos, int* step, int* token, const int* argmax,
-                                         const int* forced, const int* n_forced, int* log) {
+                                         unsigned long long* amax_key, const int* forced,
+                                         const int* n_forced, int* log) {
     if (threadIdx.x != 0) return;
     const int s = *step;
-    const int next = *argmax;
+    int next = *argmax;
+    if (amax_key) {  // fused head: decode and clear the argmax key
+        const unsigned long long k = *amax_key;
+        next = k ? (int)(0xFFFFFFFFu - (uint32_t)k) : 0;
+        *amax_key = 0ull;
+    }
     log[s] = next;
     *token = (s + 1 < *n_forced) ? forced[s + 1] : next;
     *pos += 1;
@@ -93,6 +99,8 @@ struct tf_model {
     std::vector<uint16_t*> kc, vc;
     // device decode state
     int *d_pos = nullptr, *d_step = nullptr, *d_token = nullptr, *d_argmax = nullptr;
+    unsigned long long* d_amax_key = nullptr;
+    bool fused = true;
     int *d_forced = nullptr, *d_nforced = nullptr, *d_log = nullptr;
     std::vector<void*> allocs;
 
@@ -165,9 +173,80 @@ struct tf_model {
         tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
         if (device_state) {
             hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
-                               d_token, d_argmax, d_forced, d_nforced, d_log);
+                               d_token, d_argmax, nullptr, d_forced, d_nforced, d_log);
             tf::check((int)hipGetLastError(), "advance");
         }
+    }
+
+    // The same step with the fused kernels (decode_fused.hip): six launches
+    // per layer.
+    void step_fused(hipStream_t s, int token, int pos, bool device_state) {
+        const tf_model_config& c = cfg;
+        const int* pos_dev = device_state ? d_pos : nullptr;
+        const int* tok_dev = device_state ? d_token : nullptr;
+        tf::check(tf_embed_row(token_embd.data, embd_block_bytes, x, token, tok_dev, c.n_embd,
+                               (int)token_embd.col_bytes, s),
+                  "embed");
+        for (size_t li = 0; li < layers.size(); li++) {
+            const Layer& L = layers[li];
+            if (L.wq.wtype != tf::WType::Q4K || L.wk.wtype != tf::WType::Q4K ||
+                L.wq.col_bytes != L.wk.col_bytes)
+                throw tf::HipError(1, "fused path needs Q4_K wq/wk");
+            tf::check(tf_fused_norm_qkv_rope_kv(
+                          x, L.attn_norm, c.rms_eps, L.wq.data, L.wk.data, L.wv.data,
+                          L.wv.wtype == tf::WType::Q6K ? TF_TYPE_Q6_K : TF_TYPE_Q4_K, L.bq, L.bk,
+                          L.bv, c.n_embd, c.n_head, c.n_kv, c.head_dim, (int)L.wq.col_bytes,
+                          (int)L.wv.col_bytes, q, kc[li], vc[li], pos, pos_dev, c.rope_theta,
+                          s),
+                      "fused qkv");
+            tf::launch_attn_flash(s, fd, q, kc[li], vc[li], flash_partial, xb, pos, pos_dev);
+            gemv_f32_inplace(s, L.wo, xb);
+            if (L.gate.wtype != tf::WType::Q4K || L.up.wtype != tf::WType::Q4K)
+                throw tf::HipError(1, "ffn gate/up must be Q4_K");
+            tf::check(tf_gemv_q4k_ffn_norm(L.gate.data, L.up.data, x, L.ffn_norm, c.rms_eps, hb,
+                                           c.n_embd, c.n_ff, (int)L.gate.col_bytes, s),
+                      "ffn");
+            gemv_f32_inplace(s, L.down, hb);
+        }
+        if (output.wtype == tf::WType::Q6K && output.compact_data) {
+            tf::check(tf_gemv_q6k_head_argmax(output.compact_data, x, output_norm, c.rms_eps,
+                                              logits, (int)output.n_rows, (int)output.n_cols,
+                                              (int)output.compact_col_bytes, d_amax_key, s),
+                      "head");
+            if (!device_state)
+                tf::check(tf_argmax_key_finalize(d_amax_key, d_argmax, s), "argmax");
+        } else {
+            tf::check(tf_rms_norm(x, output_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
+            tf::gemv(s, output, xb, logits, nullptr, GemvResidual::none(), gemv_partial,
+                     partial_stride);
+            tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
+        }
+        if (device_state) {
+            const bool keyed = output.wtype == tf::WType::Q6K && output.compact_data;
+            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
+                               d_token, d_argmax, keyed ? d_amax_key : nullptr, d_forced,
+                               d_nforced, d_log);
+            tf::check((int)hipGetLastError(), "advance");
+        }
+    }
+
+    // x += W a, with the f32 activation a quantized inside the GEMV.
+    void gemv_f32_inplace(hipStream_t s, const GpuMat& w, const float* a) {
+        if (w.wtype == tf::WType::Q4K)
+            tf::check(tf_gemv_q4k_f32(w.data, a, x, (int)w.n_rows, (int)w.n_cols,
+                                      (int)w.col_bytes, 0, nullptr, 2, nullptr, s),
+                      "gemv q4k");
+        else if (w.compact_data)
+            tf::check(tf_gemv_q6k_compact_f32(w.compact_data, a, x, (int)w.n_rows, (int)w.n_cols,
+                                              (int)w.compact_col_bytes, 2, s),
+                      "gemv q6k");
+        else
+            tf::gemv(s, w, a, x, nullptr, GemvResidual::in_place(), gemv_partial, partial_stride);
+    }
+
+    void run_step(hipStream_t s, int token, int pos, bool device_state) {
+        if (fused) step_fused(s, token, pos, device_state);
+        else step(s, token, pos, device_state);
     }
 
     void capture() {
@@ -175,7 +254,7 @@ struct tf_model {
         if (!capture_stream) tf::check((int)hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking), "stream");
         tf::check((int)hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal), "capture");
         try {
-            step(capture_stream, 0, 0, true);
+            run_step(capture_stream, 0, 0, true);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(capture_stream, &g);
@@ -186,11 +265,11 @@ struct tf_model {
         tf::check((int)hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "instantiate");
     }
 
-    // Runs n_forced + n_gen steps from position pos0 with device-resident
-    // state; tokens[i] = argmax of step n_forced - 1 + i.
+    // Runs n_forced + max(n_gen, 1) - 1 steps from position pos0 with
+    // device-resident state; tokens[i] = argmax of step n_forced - 1 + i.
     void run(hipStream_t s, const int* forced, int n_forced, int pos0, int n_gen, int* tokens,
              bool use_graph) {
-        const int total = n_forced + n_gen;
+        const int total = n_forced + (n_gen > 0 ? n_gen : 1) - 1;
         if (n_forced < 1 || pos0 < 0 || pos0 + total > cfg.max_seq)
             throw tf::HipError(1, "decode range outside the KV cache");
         std::vector<int> h(4);
@@ -207,7 +286,7 @@ struct tf_model {
         if (use_graph) capture();
         for (int i = 0; i < total; i++) {
             if (use_graph) tf::check((int)hipGraphLaunch(graph_exec, s), "graph launch");
-            else step(s, 0, 0, true);
+            else run_step(s, 0, 0, true);
         }
         if (n_gen > 0 && tokens)
             tf::check((int)hipMemcpyAsync(tokens, d_log + n_forced - 1, sizeof(int) * n_gen,
@@ -272,6 +351,8 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->d_step = m->alloc<int>(1);
         m->d_token = m->alloc<int>(1);
         m->d_argmax = m->alloc<int>(1);
+        m->d_amax_key = m->alloc<unsigned long long>(1);
+        tf::check((int)hipMemset(m->d_amax_key, 0, sizeof(unsigned long long)), "memset");
         m->d_nforced = m->alloc<int>(1);
         m->d_forced = m->alloc<int>(c.max_seq);
         m->d_log = m->alloc<int>(c.max_seq);
@@ -292,7 +373,7 @@ extern "C" int tf_model_forward(tf_model* m, int token, int pos, int* next_token
         return (int)hipErrorInvalidValue;
     try {
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-        m->step(s, token, pos, false);
+        m->run_step(s, token, pos, false);
         if (next_token) {
             tf::check((int)hipMemcpyAsync(next_token, m->d_argmax, sizeof(int),
                                           hipMemcpyDeviceToHost, s), "copy");
@@ -316,6 +397,18 @@ extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, i
     } catch (const tf::HipError& e) {
         return e.code;
     }
+}
+
+extern "C" int tf_model_set_path(tf_model* m, int fused) {
+    if (!m) return (int)hipErrorInvalidValue;
+    if (m->fused != (fused != 0)) {
+        m->fused = fused != 0;
+        if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+        if (m->graph) (void)hipGraphDestroy(m->graph);
+        m->graph_exec = nullptr;
+        m->graph = nullptr;
+    }
+    return 0;
 }
 
 extern "C" const float* tf_model_logits(const tf_model* m) { return m ? m->logits : nullptr; }

@@ -16,119 +16,11 @@
 // The Q8 activation lives in LDS: q8 bytes, d8[g], and ds[g] = d8[g]*sum(q8
 // over group g), the latter turning the dmin term into two FMAs per lane.
 #pragma once
-#include "tf_common.hpp"
+#include "stage.hpp"
 
-struct TfQ8Lds {
-    const int8_t* q8;   // nb*256 bytes
-    const float* d8;    // nb*8
-    const float* ds;    // nb*8: d8[g] * sum(q8 in group g)
-};
-
-// LDS bytes needed to stage the Q8 activation of nb super-blocks.
-__host__ __device__ constexpr int tf_q8_lds_bytes(int nb) { return nb * 256 + nb * 8 * 8; }
-
-__device__ __forceinline__ TfQ8Lds tf_q8_lds_view(uint8_t* lds, int nb) {
-    TfQ8Lds v;
-    v.q8 = reinterpret_cast<const int8_t*>(lds);
-    v.d8 = reinterpret_cast<const float*>(lds + nb * 256);
-    v.ds = reinterpret_cast<const float*>(lds + nb * 256 + nb * 32);
-    return v;
-}
-
-// Copy a pre-quantized activation (groups [0, nb*8)) into LDS and derive
-// ds[g].  Cooperative over the whole workgroup; ends with a barrier.
-__device__ __forceinline__ void tf_stage_q8(const int8_t* __restrict__ xq,
-                                            const float* __restrict__ xd,
-                                            int nb, uint8_t* lds,
-                                            int32_t* sums_out = nullptr) {
-    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
-    float* dss = reinterpret_cast<float*>(lds + nb * 256 + nb * 32);
-    const int groups = nb * 8;
-    const bool a16 = ((uintptr_t)xq & 15) == 0;
-    // one 32-byte group per thread: copy and sum in one pass
-    for (int g = threadIdx.x; g < groups; g += blockDim.x) {
-        tf_u32x4 a, b;
-        if (a16) {
-            a = tf_ld16(xq + g * 32);
-            b = tf_ld16(xq + g * 32 + 16);
-        } else {
-            uint32_t w[8];
-            for (int i = 0; i < 8; i++) {
-                const uint8_t* p = reinterpret_cast<const uint8_t*>(xq) + g * 32 + 4 * i;
-                w[i] = p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
-            }
-            a = tf_u32x4{w[0], w[1], w[2], w[3]};
-            b = tf_u32x4{w[4], w[5], w[6], w[7]};
-        }
-        reinterpret_cast<tf_u32x4*>(q8s + g * 32)[0] = a;
-        reinterpret_cast<tf_u32x4*>(q8s + g * 32)[1] = b;
-        const int one = 0x01010101;
-        int s = tf_dot4(one, (int)a.x, 0);
-        s = tf_dot4(one, (int)a.y, s);
-        s = tf_dot4(one, (int)a.z, s);
-        s = tf_dot4(one, (int)a.w, s);
-        s = tf_dot4(one, (int)b.x, s);
-        s = tf_dot4(one, (int)b.y, s);
-        s = tf_dot4(one, (int)b.z, s);
-        s = tf_dot4(one, (int)b.w, s);
-        const float d = xd[g];
-        d8s[g] = d;
-        dss[g] = d * (float)s;
-        if (sums_out) sums_out[g] = s;
-    }
-    __syncthreads();
-}
-
-// Quantize an f32 activation (nb*256 values) straight into LDS, bit-identical
-// to tf_quantize_q8 (kernels/gemv.cu:16-40 quantize_q8_smem).  Each wave
-// quantizes two 32-value groups per step (lanes 0-31 / 32-63); the loads of
-// eight steps are issued before any of them is used.  Ends with a barrier.
-__device__ __forceinline__ void tf_quantize_to_lds(const float* __restrict__ x,
-                                                   int nb, uint8_t* lds) {
-    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
-    float* dss = reinterpret_cast<float*>(lds + nb * 256 + nb * 32);
-    const int groups = nb * 8;
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31;
-    const int waves = blockDim.x >> 6;
-    const int gstep = 2 * waves;
-    const int g0 = (threadIdx.x >> 6) * 2 + (lane >> 5);
-    const int iters = (groups + gstep - 1) / gstep;
-    for (int i0 = 0; i0 < iters; i0 += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int g = g0 + gstep * (i0 + u);
-            v[u] = (i0 + u < iters && g < groups) ? x[g * 32 + l32] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            if (i0 + u < iters) {  // wave-uniform
-                const int g = g0 + gstep * (i0 + u);
-                const float xi = v[u];
-                const float amax = tf_group32_max(fabsf(xi));
-                const float d = amax * (1.0f / 127.0f);
-                const int q = tf_q8_value(xi, amax, d);
-                int s = q;
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
-                s += __shfl_xor(s, 8, 64);
-                s += __shfl_xor(s, 16, 64);
-                if (g < groups) {
-                    q8s[g * 32 + l32] = (int8_t)q;
-                    if (l32 == 0) {
-                        d8s[g] = d;
-                        dss[g] = d * (float)s;
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-}
+// The activation image in LDS (q8, d8, ds) is built by tf_stage_act
+// (stage.hpp).
+using TfQ8Lds = TfAct;
 
 struct TfQ4kPart {
     tf_u32x4 h;  // d, dmin, scales[12]

@@ -17,7 +17,7 @@
 // 64 values 128n + 32k + 16h + i (k = 0..3, i = 0..15): four 16-value scale
 // groups 8n + 2k + h, i.e. a quarter of the super-block.
 #pragma once
-#include "tf_common.hpp"
+#include "stage.hpp"
 
 struct TfQ6kPart {
     tf_u32x4 a;   // ql[64n+16h ..]
@@ -95,55 +95,9 @@ __device__ __forceinline__ void tf_q6k_idots(const TfQ6kPart& q, int p, const in
     }
 }
 
-// LDS image of a Q8 activation for the Q6_K kernels: q8 bytes, d8[g] and
-// s16[2g+h] = sum of q8 over the 16 values 32g+16h .. 32g+16h+15.
-__host__ __device__ constexpr int tf_q6_lds_bytes(int nb) { return nb * 256 + nb * 32 + nb * 64; }
-
-struct TfQ6Lds {
-    const int8_t* q8;
-    const float* d8;
-    const int32_t* s16;
-};
-
-__device__ __forceinline__ TfQ6Lds tf_q6_lds_view(uint8_t* lds, int nb) {
-    TfQ6Lds v;
-    v.q8 = reinterpret_cast<const int8_t*>(lds);
-    v.d8 = reinterpret_cast<const float*>(lds + nb * 256);
-    v.s16 = reinterpret_cast<const int32_t*>(lds + nb * 256 + nb * 32);
-    return v;
-}
-
-__device__ __forceinline__ void tf_stage_q6(const int8_t* __restrict__ xq,
-                                            const float* __restrict__ xd, int nb,
-                                            uint8_t* lds) {
-    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
-    int32_t* s16 = reinterpret_cast<int32_t*>(lds + nb * 256 + nb * 32);
-    const bool a16 = ((uintptr_t)xq & 15) == 0;
-    // one 16-value half-group per thread
-    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
-        tf_u32x4 a;
-        if (a16) {
-            a = tf_ld16(xq + i * 16);
-        } else {
-            uint32_t w[4];
-            for (int k = 0; k < 4; k++) {
-                const uint8_t* p = reinterpret_cast<const uint8_t*>(xq) + i * 16 + 4 * k;
-                w[k] = p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
-            }
-            a = tf_u32x4{w[0], w[1], w[2], w[3]};
-        }
-        reinterpret_cast<tf_u32x4*>(q8s)[i] = a;
-        const int one = 0x01010101;
-        int s = tf_dot4(one, (int)a.x, 0);
-        s = tf_dot4(one, (int)a.y, s);
-        s = tf_dot4(one, (int)a.z, s);
-        s = tf_dot4(one, (int)a.w, s);
-        s16[i] = s;
-        if ((i & 1) == 0) d8s[i >> 1] = xd[i >> 1];
-    }
-    __syncthreads();
-}
+// The activation image in LDS (q8, d8, s16 = per-16-value q8 sums) is built
+// by tf_stage_act (stage.hpp).
+using TfQ6Lds = TfAct;
 
 // fp32 contribution of this lane's quarter of super-block sb.
 __device__ __forceinline__ float tf_q6k_part_dot(const TfQ6kPart& q, int p, int sb,
@@ -200,4 +154,32 @@ __device__ __forceinline__ float tf_q6k_row_partial_loop(const uint8_t* __restri
         acc += tf_q6k_part_dot(q, p, sb, x);
     }
     return acc;
+}
+
+// f32-activation contribution of this lane's quarter of a raw (210-byte)
+// super-block sb (kernels/gemv.cu:233-264 arithmetic): per scale group,
+// sum(q*x) - 32*sum(x), scaled by d*sc.  act.xf / act.xs16 hold the
+// normalized activation and its 16-value sums.
+__device__ __forceinline__ float tf_q6k_f32_part_dot(const TfQ6kPart& q, int p, int sb,
+                                                     const TfAct& act) {
+    const int n = p >> 1, h = p & 1;
+    const float d = tf_h2f(q.d);
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float* xv = act.xf + sb * 256 + 128 * n + 32 * k + 16 * h;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t word = tf_q6k_word(q, k, i);
+            const float4 xx = *reinterpret_cast<const float4*>(xv + 4 * i);
+            s += (float)(word & 0xff) * xx.x;
+            s += (float)((word >> 8) & 0xff) * xx.y;
+            s += (float)((word >> 16) & 0xff) * xx.z;
+            s += (float)(word >> 24) * xx.w;
+        }
+        s -= 32.f * act.xs16[sb * 16 + 8 * n + 2 * k + h];
+        part += (float)tf_q6k_scale(q, p, k) * s;
+    }
+    return d * part;
 }

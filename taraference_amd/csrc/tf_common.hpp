@@ -97,6 +97,32 @@ __device__ __forceinline__ int tf_q8_value(float x, float amax, float d) {
     return amax == 0.f ? 0 : (int)__builtin_rintf(x / d);
 }
 
+// f32 -> f16 bits, truncating the mantissa and adding one ulp when the first
+// dropped bit is set (kernels/common.cu:9-38); subnormals, zero, inf and nan
+// as the reference.
+__device__ __forceinline__ uint16_t tf_f2h_halfup(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t absx = x & 0x7fffffffu;
+    if (absx == 0u) return (uint16_t)sign;
+    if (absx >= 0x7f800000u) return (uint16_t)(sign | (absx == 0x7f800000u ? 0x7c00u : 0x7e00u));
+    if (absx < 0x33000000u) return (uint16_t)sign;
+    if (absx >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
+    const int e = (int)((absx >> 23) & 0xff) - 127 + 15;
+    uint32_t mant = absx & 0x7fffffu;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        mant |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t hm = mant >> shift;
+        if ((mant >> (shift - 1)) & 1u) hm += 1u;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (mant >> 13);
+    if (mant & 0x1000u) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
 // ------------------------------------------------------------ host helpers
 
 

@@ -91,6 +91,11 @@ static const char* const k_symbols[] = {
     "tf_flash_decode_partial_d",
     "tf_flash_decode_reduce",
     "tf_flash_decode_n_split",
+    "tf_fused_norm_qkv_rope_kv",
+    "tf_gemv_q4k_ffn_norm",
+    "tf_gemv_q6k_compact_f32",
+    "tf_gemv_q6k_head_argmax",
+    "tf_argmax_key_finalize",
     "tf_embed_row",
     "tf_rms_norm",
     "tf_rope_neox",
@@ -100,6 +105,7 @@ static const char* const k_symbols[] = {
     "tf_model_destroy",
     "tf_model_forward",
     "tf_model_generate",
+    "tf_model_set_path",
     "tf_model_logits",
     "tf_model_k_cache",
     "tf_model_v_cache",

@@ -49,6 +49,8 @@ def _bind(lib):
     lib.tf_model_generate.argtypes = [C.c_void_p, C.POINTER(C.c_int), C.c_int, C.c_int,
                                       C.c_int, C.POINTER(C.c_int), C.c_int, C.c_void_p]
     lib.tf_model_generate.restype = C.c_int
+    lib.tf_model_set_path.argtypes = [C.c_void_p, C.c_int]
+    lib.tf_model_set_path.restype = C.c_int
     lib.tf_model_logits.argtypes = [C.c_void_p]
     lib.tf_model_logits.restype = C.c_void_p
     for n in ("tf_model_k_cache", "tf_model_v_cache"):
@@ -134,6 +136,12 @@ class DecodeModel:
         if rc != 0:
             raise capi.HipError(f"tf_model_forward returned {rc}")
         return nxt.value
+
+    def set_fused(self, fused: bool) -> None:
+        """Fused decode kernels (default) or the reference kernel sequence."""
+        rc = self.lib.tf_model_set_path(self.h, int(fused))
+        if rc != 0:
+            raise capi.HipError(f"tf_model_set_path returned {rc}")
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.cfg["n_vocab"], np.float32)

@@ -64,3 +64,31 @@ def test_invalid_args_rejected(capi):
     assert lib.tf_flash_decode_partial(16, 16, 16, 16, 16, 2, 128, 10, 2, 8, 0.1, None) == INVALID
     assert lib.tf_flash_decode_reduce(16, 16, 16, 128, 0, 1, None) == INVALID
     assert lib.tf_version() >= 100
+
+
+def test_every_export_has_argtypes(capi):
+    """A C-ABI function called without declared argtypes gets its pointer
+    arguments truncated to 32-bit C ints; every export must be declared."""
+    declared = set(capi.SIGNATURES) | capi.BOUND_ELSEWHERE
+    missing = [s for s in header_symbols() if s not in declared]
+    assert not missing, missing
+    for name, args in capi.SIGNATURES.items():
+        assert name in header_symbols(), name
+    import ctypes
+    lib = capi.load()
+    assert lib.tf_gemv_q6k_compact_f32.argtypes[0] is ctypes.c_void_p
+
+
+def header_param_counts():
+    text = HEADER.read_text()
+    out = {}
+    for m in re.finditer(r"^[A-Za-z][\w \*]*?\b(tf_\w+)\s*\(([^;]*?)\)\s*;", text, re.M | re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_argtypes_match_header_arity(capi):
+    counts = header_param_counts()
+    for name, args in capi.SIGNATURES.items():
+        assert counts[name] == len(args), (name, counts[name], len(args))

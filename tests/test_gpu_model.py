@@ -39,10 +39,12 @@ def build(cfg, seed, max_seq):
     return DecodeModel(c, layers, emb), RefModel(cfg, layers, emb, max_seq)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("ci", [0, 1])
-def test_decode_steps_match_reference(gpu, ci):
+def test_decode_steps_match_reference(gpu, ci, fused):
     cfg = TINY[ci]
     gm, rm = build(cfg, 100 + ci, 48)
+    gm.set_fused(fused)
     rng = np.random.default_rng(ci)
     prompt = rng.integers(0, cfg["n_vocab"], 12).tolist()
     tok = prompt[0]
@@ -69,9 +71,11 @@ def test_decode_steps_match_reference(gpu, ci):
     gm.close()
 
 
-def test_graph_replay_equals_eager(gpu):
+@pytest.mark.parametrize("fused", [True, False])
+def test_graph_replay_equals_eager(gpu, fused):
     cfg = TINY[1]
     gm, _ = build(cfg, 7, 64)
+    gm.set_fused(fused)
     prompt = list(range(5, 21))
     eager = gm.generate(prompt, 20, use_graph=False)
     graph = gm.generate(prompt, 20, use_graph=True)
