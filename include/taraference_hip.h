@@ -240,6 +240,33 @@ int tf_fused_norm_qkv_rope_kv(const float *x, const float *norm_w, float eps,
                               uint16_t *k_cache, uint16_t *v_cache, int pos,
                               const int *pos_dev, float theta,
                               tf_stream_t stream);
+/* The same as tf_fused_norm_qkv_rope_kv with the activation already
+ * normalized and quantized (tf_norm_quant): xq/xd its Q8, xb its f32 values
+ * (read by the Q6_K V projection; may be NULL when v_type is Q4_K). */
+int tf_fused_qkv_rope_kv(const int8_t *xq, const float *xd, const float *xb,
+                         const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
+                         int v_type, const float *bq, const float *bk,
+                         const float *bv, int n_embd, int n_head, int n_kv,
+                         int head_dim, int col_bytes_qk, int col_bytes_v,
+                         float *q_out, uint16_t *k_cache, uint16_t *v_cache,
+                         int pos, const int *pos_dev, float theta,
+                         tf_stream_t stream);
+/* ops.cu:4-34 rms_norm_f32 + gemv.cu:43-65 quantize_q8_global, one launch:
+ * xb = x * rsqrt(mean x^2 + eps) * w and its Q8 (q8[n], d8[n/32]). */
+int tf_norm_quant(const float *x, const float *w, float eps, float *xb,
+                  int8_t *q8, float *d8, int n, tf_stream_t stream);
+/* flash.cu:222 attn_flash_reduce + quantize_q8 of the attention output
+ * (layer.rs:2104-2119 then matmul.rs:191): also writes q8[n_head*head_dim]
+ * and d8[n_head*head_dim/32]; head_dim % 64 == 0. */
+int tf_flash_decode_reduce_q8(const float *partial, float *out, int8_t *q8,
+                              float *d8, int n_head, int head_dim,
+                              int n_split, tf_stream_t stream);
+/* layer.rs:2181-2257 with a pre-quantized activation:
+ * gemv_q6_k_compact_global (logits) + argmax into *amax_key (see
+ * tf_gemv_q6k_head_argmax). */
+int tf_gemv_q6k_q8_argmax(const uint8_t *w, const int8_t *xq, const float *xd,
+                          float *logits, int n_rows, int n_cols, int col_bytes,
+                          unsigned long long *amax_key, tf_stream_t stream);
 /* layer.rs:1220-1386: rms_norm_f32 (x * norm_w) + gemv_q4_k_ffn_mcol. */
 int tf_gemv_q4k_ffn_norm(const uint8_t *gate, const uint8_t *up,
                          const float *x, const float *norm_w, float eps,

@@ -782,7 +782,9 @@ void or_rms_norm(const float *x, const float *w, float *out, int n, float eps) {
     float buf[256];
     for (int t = 0; t < 256; t++) {
         float local = 0.f;
-        for (int i = t; i < n; i += 256) local += x[i] * x[i];
+        /* the reference is compiled with fmad=true (cuda/device.rs:114): the
+           square-accumulate is one fused multiply-add */
+        for (int i = t; i < n; i += 256) local = fmaf(x[i], x[i], local);
         buf[t] = local;
     }
     for (int s = 128; s > 0; s >>= 1)

@@ -44,6 +44,11 @@ SIGNATURES: dict[str, list] = {
     "tf_fused_norm_qkv_rope_kv": [_P, _P, _F, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                   _I, _P, _P, _P, _I, _P, _F, _P],
     "tf_gemv_q6k_compact_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_fused_qkv_rope_kv": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                             _P, _P, _P, _I, _P, _F, _P],
+    "tf_norm_quant": [_P, _P, _F, _P, _P, _P, _I, _P],
+    "tf_flash_decode_reduce_q8": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_gemv_q6k_q8_argmax": [_P, _P, _P, _P, _I, _I, _I, _P, _P],
     "tf_gemv_q6k_head_argmax": [_P, _P, _P, _F, _P, _I, _I, _I, _P, _P],
     "tf_argmax_key_finalize": [_P, _P, _P],
     "tf_embed_row": [_P, _I, _P, _I, _P, _I, _I, _P],

@@ -328,6 +328,54 @@ extern "C" int tf_fused_norm_qkv_rope_kv(
     return rc;
 }
 
+extern "C" int tf_fused_qkv_rope_kv(const int8_t* xq, const float* xd, const float* xb,
+                                    const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                                    int v_type, const float* bq, const float* bk, const float* bv,
+                                    int n_embd, int n_head, int n_kv, int head_dim,
+                                    int col_bytes_qk, int col_bytes_v, float* q_out,
+                                    uint16_t* k_cache, uint16_t* v_cache, int pos,
+                                    const int* pos_dev, float theta, tf_stream_t stream) {
+    const int nb = n_embd / 256;
+    TF_CHECK_ARG(xq && xd && wq && wk && wv && q_out && k_cache && v_cache && nb > 0);
+    TF_CHECK_ARG(n_head > 0 && n_kv > 0 && head_dim > 0 && (head_dim & 1) == 0);
+    TF_CHECK_ARG(v_type == TF_TYPE_Q4_K || (v_type == TF_TYPE_Q6_K && xb &&
+                                             ((uintptr_t)xb & 15) == 0));
+    TF_CHECK_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)wk & 15) == 0 && (col_bytes_qk & 15) == 0);
+    TF_CHECK_ARG(col_bytes_qk >= nb * 144);
+    if (v_type == TF_TYPE_Q6_K)
+        TF_CHECK_ARG(((uintptr_t)wv & 1) == 0 && (col_bytes_v & 1) == 0 && col_bytes_v >= nb * 210);
+    else
+        TF_CHECK_ARG(((uintptr_t)wv & 15) == 0 && (col_bytes_v & 15) == 0 && col_bytes_v >= nb * 144);
+    TF_CHECK_ARG(pos_dev || pos >= 0);
+    TfQkvArgs a{wq, wk, wv, bq, bk, bv, n_head * head_dim, n_kv * head_dim, n_kv * head_dim,
+                col_bytes_qk, col_bytes_v, v_type == TF_TYPE_Q6_K ? 1 : 0, q_out, k_cache, v_cache,
+                n_kv * head_dim, pos, pos_dev, theta, head_dim};
+    const TfActSrc src{TF_SRC_Q8, xq, xd, v_type == TF_TYPE_Q6_K ? xb : nullptr, nullptr, 0.f};
+    const int lds = tf_act_lds_bytes(nb, true);
+    int rc = 0;
+    tf_fused_dispatch(nb, [&](auto spr, auto it) {
+        constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
+        constexpr int UNITS = 16 / SPR;
+        constexpr int PPT = UNITS >= 2 ? UNITS / 2 : 1;
+        auto fn = tf_fused_qkv_kernel<SPR, IT>;
+        const int tasks = ((a.n_q + a.n_k) / 2 + PPT - 1) / PPT + (a.n_v + UNITS - 1) / UNITS;
+        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), a, src, nb);
+        rc = TF_LAUNCH_RESULT();
+    });
+    return rc;
+}
+
+extern "C" int tf_gemv_q6k_q8_argmax(const uint8_t* w, const int8_t* xq, const float* xd,
+                                     float* logits, int n_rows, int n_cols, int col_bytes,
+                                     unsigned long long* amax_key, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(w && xq && xd && logits && amax_key && nb > 0 && n_cols > 0);
+    TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212);
+    return tf_q6k_src_launch(w, TfActSrc{TF_SRC_Q8, xq, xd, nullptr, nullptr, 0.f}, logits,
+                             n_rows, n_cols, col_bytes, 0, amax_key, stream);
+}
+
 extern "C" int tf_gemv_q6k_compact_f32(const uint8_t* w, const float* x, float* out, int n_rows,
                                        int n_cols, int col_bytes, int use_res,
                                        tf_stream_t stream) {

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void tf_rms_norm_kernel(const float* __restric
     float local = 0.f;
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = x[i];
-        local += v * v;
+        local = fmaf(v, v, local);  // fused, as under fmad=true
     }
     buf[threadIdx.x] = local;
     __syncthreads();
@@ -91,6 +91,59 @@ __global__ __launch_bounds__(256) void tf_rms_norm_kernel(const float* __restric
     }
     const float scale = 1.0f / sqrtf(buf[0] / (float)n + eps);
     for (int i = threadIdx.x; i < n; i += 256) out[i] = x[i] * scale * w[i];
+}
+
+// rms_norm_f32 + quantize_q8_global in one launch (kernels/ops.cu:4-34 and
+// kernels/gemv.cu:43-65): xb = x * scale * w written in f32, then its Q8
+// bytes and scales.  The norm keeps the reference's summation order (256
+// strided partial sums, halving tree: levels 128 and 64 through LDS, the
+// rest as shfl_down pairs within wave 0, which adds the same pairs); the
+// quantization is bit-identical to tf_quantize_q8.
+__global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ xb,
+                                                            int8_t* __restrict__ q8,
+                                                            float* __restrict__ d8, int n,
+                                                            float eps) {
+    __shared__ float buf[256];
+    __shared__ float scale_s;
+    const int tid = threadIdx.x;
+    float local = 0.f;
+    for (int i = tid; i < n; i += 256) {
+        const float v = x[i];
+        local = fmaf(v, v, local);  // fused, as under fmad=true
+    }
+    buf[tid] = local;
+    __syncthreads();
+    if (tid < 128) buf[tid] += buf[tid + 128];
+    __syncthreads();
+    if (tid < 64) {
+        float v = buf[tid] + buf[tid + 64];
+        v += __shfl_down(v, 32, 64);
+        v += __shfl_down(v, 16, 64);
+        v += __shfl_down(v, 8, 64);
+        v += __shfl_down(v, 4, 64);
+        v += __shfl_down(v, 2, 64);
+        v += __shfl_down(v, 1, 64);
+        if (tid == 0) scale_s = 1.0f / sqrtf(v / (float)n + eps);
+    }
+    __syncthreads();
+    const float scale = scale_s;
+    // quantize: lanes 0-31 / 32-63 own one 32-value group per step
+    const int lane = tid & 63, l32 = lane & 31;
+    const int groups = n / 32;
+    for (int g2 = (tid >> 6) * 2; g2 < groups; g2 += 8) {  // wave-uniform trip count
+        const int g = g2 + (lane >> 5);
+        const bool live = g < groups;
+        const float xi = live ? x[g * 32 + l32] * scale * w[g * 32 + l32] : 0.f;
+        const float amax = tf_group32_max(fabsf(xi));
+        const float d = amax * (1.0f / 127.0f);
+        if (live) {
+            xb[g * 32 + l32] = xi;
+            q8[g * 32 + l32] = (int8_t)tf_q8_value(xi, amax, d);
+            if (l32 == 0) d8[g] = d;
+        }
+    }
 }
 
 // ------------------------------------------------------------ RoPE (NeoX)
@@ -192,6 +245,14 @@ extern "C" int tf_rms_norm(const float* x, const float* w, float* out, int n, fl
     TF_CHECK_ARG(x && w && out && n > 0);
     hipLaunchKernelGGL(tf_rms_norm_kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, out, n,
                        eps);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_norm_quant(const float* x, const float* w, float eps, float* xb, int8_t* q8,
+                             float* d8, int n, tf_stream_t stream) {
+    TF_CHECK_ARG(x && w && xb && q8 && d8 && n > 0 && (n % 32) == 0);
+    hipLaunchKernelGGL(tf_norm_quant_kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, xb,
+                       q8, d8, n, eps);
     return TF_LAUNCH_RESULT();
 }
 

@@ -227,6 +227,8 @@ __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
 // through LDS.
 __global__ __launch_bounds__(256) void tf_flash_reduce_kernel(const float* __restrict__ partial,
                                                               float* __restrict__ out,
+                                                              int8_t* __restrict__ q8,
+                                                              float* __restrict__ d8,
                                                               int head_dim, int n_split) {
     __shared__ float wts[1024];
     __shared__ float red[256];
@@ -268,10 +270,25 @@ __global__ __launch_bounds__(256) void tf_flash_reduce_kernel(const float* __res
     }
     red[tid] = acc;
     __syncthreads();
-    if (tid < head_dim) {
-        float tot = 0.f;
-        for (int k = 0; k < subsets; k++) tot += red[k * head_dim + tid];
-        out[(size_t)h * head_dim + tid] = tot / fmaxf(L, 1e-20f);
+    // waves that hold output dims (head_dim is a multiple of 64 when q8 is
+    // requested, so the test below is wave-uniform)
+    if (tid < head_dim || (q8 && (tid >> 6) * 64 < head_dim)) {
+        float v = 0.f;
+        if (tid < head_dim) {
+            float tot = 0.f;
+            for (int k = 0; k < subsets; k++) tot += red[k * head_dim + tid];
+            v = tot / fmaxf(L, 1e-20f);
+            out[(size_t)h * head_dim + tid] = v;
+        }
+        if (q8) {  // quantize_q8 of the attention output: 32-value groups
+            const float amax = tf_group32_max(fabsf(v));
+            const float d = amax * (1.0f / 127.0f);
+            const size_t i = (size_t)h * head_dim + tid;
+            if (tid < head_dim) {
+                q8[i] = (int8_t)tf_q8_value(v, amax, d);
+                if ((tid & 31) == 0) d8[i >> 5] = d;
+            }
+        }
     }
 }
 
@@ -352,7 +369,17 @@ extern "C" int tf_flash_decode_reduce(const float* partial, float* out, int n_he
                                       int head_dim, int n_split, int n_q, tf_stream_t stream) {
     TF_CHECK_ARG(partial && out && n_head > 0 && head_dim > 0 && n_split >= 1 && n_q == 1);
     TF_CHECK_ARG(head_dim <= 256 && n_split <= 1024);
-    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream), partial, out, head_dim, n_split);
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream), partial, out, nullptr, nullptr, head_dim, n_split);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_flash_decode_reduce_q8(const float* partial, float* out, int8_t* q8, float* d8,
+                                         int n_head, int head_dim, int n_split,
+                                         tf_stream_t stream) {
+    TF_CHECK_ARG(partial && out && q8 && d8 && n_head > 0 && n_split >= 1 && n_split <= 1024);
+    TF_CHECK_ARG(head_dim > 0 && head_dim <= 256 && (head_dim % 64) == 0);
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream),
+                       partial, out, q8, d8, head_dim, n_split);
     return TF_LAUNCH_RESULT();
 }
 

@@ -178,8 +178,10 @@ struct tf_model {
         }
     }
 
-    // The same step with the fused kernels (decode_fused.hip): six launches
-    // per layer.
+    // The same step with fused kernels: each activation is normalized and
+    // quantized once (tf_norm_quant, or the flash reduce for the attention
+    // output), QKV + RoPE + KV append run in one GEMV launch, and the head
+    // carries the argmax: nine launches per layer.
     void step_fused(hipStream_t s, int token, int pos, bool device_state) {
         const tf_model_config& c = cfg;
         const int* pos_dev = device_state ? d_pos : nullptr;
@@ -190,39 +192,55 @@ struct tf_model {
         for (size_t li = 0; li < layers.size(); li++) {
             const Layer& L = layers[li];
             if (L.wq.wtype != tf::WType::Q4K || L.wk.wtype != tf::WType::Q4K ||
-                L.wq.col_bytes != L.wk.col_bytes)
-                throw tf::HipError(1, "fused path needs Q4_K wq/wk");
-            tf::check(tf_fused_norm_qkv_rope_kv(
-                          x, L.attn_norm, c.rms_eps, L.wq.data, L.wk.data, L.wv.data,
+                L.wq.col_bytes != L.wk.col_bytes || L.gate.wtype != tf::WType::Q4K ||
+                L.up.wtype != tf::WType::Q4K)
+                throw tf::HipError(1, "fused path needs Q4_K q/k/gate/up");
+            tf::check(tf_norm_quant(x, L.attn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                      "norm_quant");
+            tf::check(tf_fused_qkv_rope_kv(
+                          q8_x, q8_d, xb, L.wq.data, L.wk.data, L.wv.data,
                           L.wv.wtype == tf::WType::Q6K ? TF_TYPE_Q6_K : TF_TYPE_Q4_K, L.bq, L.bk,
                           L.bv, c.n_embd, c.n_head, c.n_kv, c.head_dim, (int)L.wq.col_bytes,
-                          (int)L.wv.col_bytes, q, kc[li], vc[li], pos, pos_dev, c.rope_theta,
-                          s),
+                          (int)L.wv.col_bytes, q, kc[li], vc[li], pos, pos_dev, c.rope_theta, s),
                       "fused qkv");
-            tf::launch_attn_flash(s, fd, q, kc[li], vc[li], flash_partial, xb, pos, pos_dev);
-            gemv_f32_inplace(s, L.wo, xb);
-            if (L.gate.wtype != tf::WType::Q4K || L.up.wtype != tf::WType::Q4K)
-                throw tf::HipError(1, "ffn gate/up must be Q4_K");
-            tf::check(tf_gemv_q4k_ffn_norm(L.gate.data, L.up.data, x, L.ffn_norm, c.rms_eps, hb,
-                                           c.n_embd, c.n_ff, (int)L.gate.col_bytes, s),
+            if (pos_dev)
+                tf::check(tf_flash_decode_partial_d(q, kc[li], vc[li], flash_partial, fd.n_head,
+                                                    fd.n_kv, fd.head_dim, pos_dev, 1, fd.n_split,
+                                                    fd.scale, s),
+                          "flash partial");
+            else
+                tf::check(tf_flash_decode_partial(q, kc[li], vc[li], flash_partial, fd.n_head,
+                                                  fd.n_kv, fd.head_dim, pos, 1, fd.n_split,
+                                                  fd.scale, s),
+                          "flash partial");
+            tf::check(tf_flash_decode_reduce_q8(flash_partial, xb, q8_x, q8_d, fd.n_head,
+                                                fd.head_dim, fd.n_split, s),
+                      "flash reduce");
+            gemv_q8_inplace(s, L.wo);
+            tf::check(tf_norm_quant(x, L.ffn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                      "norm_quant");
+            tf::check(tf_gemv_q4k_ffn(L.gate.data, L.up.data, q8_x, q8_d, hb, c.n_embd, c.n_ff,
+                                      (int)L.gate.col_bytes, s),
                       "ffn");
-            gemv_f32_inplace(s, L.down, hb);
+            tf::check(tf_quantize_q8(hb, q8_x, q8_d, c.n_ff, s), "quantize h");
+            gemv_q8_inplace(s, L.down);
         }
-        if (output.wtype == tf::WType::Q6K && output.compact_data) {
-            tf::check(tf_gemv_q6k_head_argmax(output.compact_data, x, output_norm, c.rms_eps,
-                                              logits, (int)output.n_rows, (int)output.n_cols,
-                                              (int)output.compact_col_bytes, d_amax_key, s),
+        tf::check(tf_norm_quant(x, output_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                  "norm_quant");
+        const bool keyed = output.wtype == tf::WType::Q6K && output.compact_data;
+        if (keyed) {
+            tf::check(tf_gemv_q6k_q8_argmax(output.compact_data, q8_x, q8_d, logits,
+                                            (int)output.n_rows, (int)output.n_cols,
+                                            (int)output.compact_col_bytes, d_amax_key, s),
                       "head");
             if (!device_state)
                 tf::check(tf_argmax_key_finalize(d_amax_key, d_argmax, s), "argmax");
         } else {
-            tf::check(tf_rms_norm(x, output_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
             tf::gemv(s, output, xb, logits, nullptr, GemvResidual::none(), gemv_partial,
                      partial_stride);
             tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
         }
         if (device_state) {
-            const bool keyed = output.wtype == tf::WType::Q6K && output.compact_data;
             hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
                                d_token, d_argmax, keyed ? d_amax_key : nullptr, d_forced,
                                d_nforced, d_log);
@@ -230,18 +248,19 @@ struct tf_model {
         }
     }
 
-    // x += W a, with the f32 activation a quantized inside the GEMV.
-    void gemv_f32_inplace(hipStream_t s, const GpuMat& w, const float* a) {
+    // x += W a for the Q8 activation in q8_x/q8_d.
+    void gemv_q8_inplace(hipStream_t s, const GpuMat& w) {
         if (w.wtype == tf::WType::Q4K)
-            tf::check(tf_gemv_q4k_f32(w.data, a, x, (int)w.n_rows, (int)w.n_cols,
-                                      (int)w.col_bytes, 0, nullptr, 2, nullptr, s),
+            tf::check(tf_gemv_q4k_q8(w.data, q8_x, q8_d, x, (int)w.n_rows, (int)w.n_cols,
+                                     (int)w.col_bytes, 0, nullptr, 2, nullptr, s),
                       "gemv q4k");
         else if (w.compact_data)
-            tf::check(tf_gemv_q6k_compact_f32(w.compact_data, a, x, (int)w.n_rows, (int)w.n_cols,
-                                              (int)w.compact_col_bytes, 2, s),
+            tf::check(tf_gemv_q6k_down_splitk(w.compact_data, q8_x, q8_d, x, (int)w.n_rows,
+                                              (int)w.n_cols, (int)w.compact_col_bytes, 0, nullptr,
+                                              2, nullptr, s),
                       "gemv q6k");
         else
-            tf::gemv(s, w, a, x, nullptr, GemvResidual::in_place(), gemv_partial, partial_stride);
+            throw tf::HipError(1, "Q6_K matrix without its compact copy");
     }
 
     void run_step(hipStream_t s, int token, int pos, bool device_state) {

@@ -48,7 +48,8 @@ struct TfActSrc {
     int kind;             // TfSrc
     const int8_t* xq;     // TF_SRC_Q8
     const float* xd;      // TF_SRC_Q8
-    const float* x;       // TF_SRC_F32 / TF_SRC_NORM
+    const float* x;       // TF_SRC_F32 / TF_SRC_NORM; with TF_SRC_Q8 the f32
+                          // vector behind the Q8 bytes (copied when WITH_F32)
     const float* norm_w;  // TF_SRC_NORM
     float eps;            // TF_SRC_NORM
 };
@@ -60,7 +61,7 @@ __device__ __forceinline__ float tf_rms_scale_256(const float* __restrict__ x, i
     float local = 0.f;
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = x[i];
-        local += v * v;
+        local = fmaf(v, v, local);  // fused, as under fmad=true
     }
     red[threadIdx.x] = local;
     __syncthreads();
@@ -116,6 +117,20 @@ __device__ __forceinline__ void tf_stage_act(const TfActSrc& src, int nb, uint8_
             dss[g] = d * (float)(sa + sb);
             s16[2 * g] = sa;
             s16[2 * g + 1] = sb;
+        }
+        if (WITH_F32 && src.x) {
+            // one 16-value run per thread: copy, and sum as the pairwise tree
+            // that the xor butterfly of the f32 sources forms (bit-identical)
+            for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
+                float t[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float4 v = *reinterpret_cast<const float4*>(src.x + i * 16 + 4 * k);
+                    *reinterpret_cast<float4*>(xf + i * 16 + 4 * k) = v;
+                    t[k] = (v.x + v.y) + (v.z + v.w);
+                }
+                xs16[i] = (t[0] + t[1]) + (t[2] + t[3]);
+            }
         }
         __syncthreads();
         return;

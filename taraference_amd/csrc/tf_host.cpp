@@ -92,6 +92,10 @@ static const char* const k_symbols[] = {
     "tf_flash_decode_reduce",
     "tf_flash_decode_n_split",
     "tf_fused_norm_qkv_rope_kv",
+    "tf_fused_qkv_rope_kv",
+    "tf_norm_quant",
+    "tf_flash_decode_reduce_q8",
+    "tf_gemv_q6k_q8_argmax",
     "tf_gemv_q4k_ffn_norm",
     "tf_gemv_q6k_compact_f32",
     "tf_gemv_q6k_head_argmax",

@@ -145,3 +145,90 @@ def test_head_argmax(gpu, n_rows, n_cols):
     top2 = np.sort(y64)[-2:]
     if top2[1] - top2[0] > 1e-5 * absn.max():  # unambiguous in fp64 too
         assert i == int(np.argmax(y64))
+
+
+@pytest.mark.parametrize("n", [256, 2048, 3584, 11008])
+def test_norm_quant_bit_exact(gpu, n):
+    """RMSNorm in the reference's summation order + Q8: f32 output and Q8
+    bytes/scales bit-identical to the oracle (ops.cu:4-34, gemv.cu:43-65)."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.uniform(0.1, 30)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    xb, q8, d8 = empty(n), empty(n, torch.int8), empty(n // 32)
+    call("tf_norm_quant", P(dev(x)), P(dev(w)), 1e-6, P(xb), P(q8), P(d8), n, S())
+    rx = oracle.rms_norm(x, w, 1e-6)
+    rq, rd = oracle.quantize_q8(rx)
+    assert np.array_equal(host(xb).view(np.uint32), rx.view(np.uint32))
+    assert np.array_equal(host(q8), rq)
+    assert np.array_equal(host(d8).view(np.uint32), rd.view(np.uint32))
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_flash_reduce_q8(gpu, hd):
+    n_head, n_kv, L = 8, 2, 700
+    rng = np.random.default_rng(hd)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    K, V = synth.kv_cache(rng, L, n_kv, hd), synth.kv_cache(rng, L, n_kv, hd)
+    part, out = empty(n_head * 8 * (2 + hd)), empty(n_head * hd)
+    q8, d8 = empty(n_head * hd, torch.int8), empty(n_head * hd // 32)
+    call("tf_flash_decode_partial", P(dev(q)), P(dev(K)), P(dev(V)), P(part), n_head, n_kv, hd,
+         L - 1, 1, 8, 0.09, S())
+    call("tf_flash_decode_reduce_q8", P(part), P(out), P(q8), P(d8), n_head, hd, 8, S())
+    o = host(out)
+    ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, 0.09)
+    assert np.abs(o - ref).max() < 2e-3
+    rq, rd = oracle.quantize_q8(o)  # Q8 of exactly the f32 it wrote
+    assert np.array_equal(host(q8), rq)
+    assert np.array_equal(host(d8).view(np.uint32), rd.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", ["3b", "7b"])
+def test_fused_qkv_q8_source_matches_norm_source(gpu, shape):
+    """tf_fused_qkv_rope_kv on tf_norm_quant's output is bit-identical to the
+    prologue-normalizing tf_fused_norm_qkv_rope_kv (same Q8, same f32)."""
+    e, nh, nkv, hd = SHAPES[shape]
+    rng = np.random.default_rng(len(shape))
+    x = (rng.standard_normal(e) * 3).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, e).astype(np.float32)
+    wq, cb = synth.q4k_matrix(rng, e, nh * hd)
+    wk, _ = synth.q4k_matrix(rng, e, nkv * hd)
+    wv, cbv = synth.q6k_matrix(rng, e, nkv * hd)
+    b = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in (nh * hd, nkv * hd, nkv * hd)]
+    seq, stride, pos = 16, nkv * hd, 5
+    outs = []
+    for fused_norm in (True, False):
+        q = empty(nh * hd)
+        kc = torch.zeros(seq * stride, dtype=torch.int16, device="cuda")
+        vc = torch.zeros(seq * stride, dtype=torch.int16, device="cuda")
+        if fused_norm:
+            call("tf_fused_norm_qkv_rope_kv", P(dev(x)), P(dev(nw)), 1e-6, P(dev(wq)), P(dev(wk)),
+                 P(dev(wv)), 14, P(dev(b[0])), P(dev(b[1])), P(dev(b[2])), e, nh, nkv, hd, cb,
+                 cbv, P(q), P(kc), P(vc), pos, None, 1e6, S())
+        else:
+            xb, q8, d8 = empty(e), empty(e, torch.int8), empty(e // 32)
+            call("tf_norm_quant", P(dev(x)), P(dev(nw)), 1e-6, P(xb), P(q8), P(d8), e, S())
+            call("tf_fused_qkv_rope_kv", P(q8), P(d8), P(xb), P(dev(wq)), P(dev(wk)), P(dev(wv)),
+                 14, P(dev(b[0])), P(dev(b[1])), P(dev(b[2])), e, nh, nkv, hd, cb, cbv, P(q),
+                 P(kc), P(vc), pos, None, 1e6, S())
+        outs.append((host(q).copy(), host(kc).copy(), host(vc).copy()))
+    for a, c in zip(outs[0], outs[1]):
+        assert np.array_equal(a.view(np.uint8), c.view(np.uint8))
+
+
+def test_head_argmax_q8_source(gpu):
+    n_rows, n_cols = 2048, 151936
+    rng = np.random.default_rng(1)
+    raw, _ = synth.q6k_matrix(rng, n_rows, n_cols)
+    comp, ccb = synth.q6k_compact(raw, n_rows)
+    x = synth.activation(rng, n_rows)
+    q8, d8 = oracle.quantize_q8(x)
+    logits = empty(n_cols)
+    key = torch.zeros(1, dtype=torch.int64, device="cuda")
+    idx = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    call("tf_gemv_q6k_q8_argmax", P(dev(comp)), P(dev(q8)), P(dev(d8)), P(logits), n_rows,
+         n_cols, ccb, P(key), S())
+    call("tf_argmax_key_finalize", P(key), P(idx), S())
+    lg = host(logits)
+    y64, absn = oracle.gemv_q6k_q8_f64(comp, 212, q8, d8, n_rows, n_cols, ccb)
+    assert_gemv_close(lg, y64, absn, "head q8")
+    assert int(host(idx)[0]) == int(np.argmax(lg))
