@@ -27,6 +27,14 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+ROOFLINE_KERNEL = "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU, 2048 -> 2x11008)"
+# HBM bytes per launch of the roofline kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE
+# (KiB per dispatch) scaled by the same counters' reading on a 256 MiB device
+# copy; the counter runs and the factor are kept in profiles/.
+# FETCH_SIZE 12426.5 KiB x 2.000 (the 256 MiB copy reads 131084 KiB) +
+# WRITE_SIZE 86 KiB x 1.000 (the copy writes 262144 KiB)
+ROOFLINE_TRAFFIC = int((12426.5 * 2.0 + 86.0 * 1.0) * 1024)
+
 METRIC = "batch-1 decode tok/s, Qwen2.5-3B-shape Q4_K_M; Q4_K GEMV % of HBM peak"
 HBM_PEAK_GBS = 8000.0
 
@@ -71,6 +79,19 @@ def kernel_roofline(iters):
 
     r = B.report("q4k_gate_up", B.case_q4k_ffn(2048, 11008, 1, iters, f32_x=False))
     return r
+
+
+def copy_calibration(n_bytes=256 << 20, reps=3):
+    """A plain device-to-device copy of known size, for scaling the
+    FETCH_SIZE / WRITE_SIZE counters of the roofline kernel."""
+    import torch
+
+    a = torch.ones(n_bytes // 4, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return n_bytes
 
 
 def kernel_table(iters):
@@ -182,6 +203,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--only-roofline", action="store_true",
+                    help="run only the copy calibration and the roofline kernel (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode path is single-GPU; "
@@ -193,6 +216,13 @@ def main():
     from taraference_amd import capi, synth
 
     capi.load()
+    if args.only_roofline:
+        # counter runs: the copy of known size, then the roofline kernel alone
+        copy_calibration()
+        r = kernel_roofline(args.kernel_iters)
+        print(json.dumps({"kernel": ROOFLINE_KERNEL, "bytes": int(r["bytes"]),
+                          "us_b2b": round(r["b2b_us"], 3), "us_single": round(r["per_us"], 3)}))
+        return
     cfg = dict(synth.QWEN25_3B)
     steps = max(2, args.steps)
     max_seq = args.warmup + steps + 8
@@ -207,11 +237,15 @@ def main():
     torch.cuda.empty_cache()
 
     r = kernel_roofline(args.kernel_iters)
-    achieved = r["bytes"] / (r["per_us"] * 1e-6) / 1e9
+    # average launch duration = event pair around a burst of back-to-back
+    # launches on the kernel's stream / launches
+    achieved = r["bytes"] / (r["b2b_us"] * 1e-6) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU)",
-            "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["per_us"], 3)}
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": ROOFLINE_TRAFFIC,
+            "kernel": ROOFLINE_KERNEL,
+            "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
+            "us_per_launch_single": round(r["per_us"], 3)}
     table = {} if args.no_kernels else kernel_table(args.kernel_iters)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
 

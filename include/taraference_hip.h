@@ -40,6 +40,10 @@ extern "C" {
 
 typedef void *tf_stream_t; /* hipStream_t */
 
+/* Number of 64-bit key slots of an argmax key buffer (fused lm_head argmax):
+ * the caller allocates TF_ARGMAX_SLOTS zeroed unsigned long longs once. */
+#define TF_ARGMAX_SLOTS 1024
+
 /* Library version (major*10000 + minor*100 + patch). */
 int tf_version(void);
 
@@ -252,7 +256,8 @@ int tf_fused_qkv_rope_kv(const int8_t *xq, const float *xd, const float *xb,
                          int pos, const int *pos_dev, float theta,
                          tf_stream_t stream);
 /* ops.cu:4-34 rms_norm_f32 + gemv.cu:43-65 quantize_q8_global, one launch:
- * xb = x * rsqrt(mean x^2 + eps) * w and its Q8 (q8[n], d8[n/32]). */
+ * xb = x * rsqrt(mean x^2 + eps) * w and its Q8 (q8[n], d8[n/32]);
+ * n % 32 == 0, n <= 16384. */
 int tf_norm_quant(const float *x, const float *w, float eps, float *xb,
                   int8_t *q8, float *d8, int n, tf_stream_t stream);
 /* flash.cu:222 attn_flash_reduce + quantize_q8 of the attention output
@@ -262,7 +267,7 @@ int tf_flash_decode_reduce_q8(const float *partial, float *out, int8_t *q8,
                               float *d8, int n_head, int head_dim,
                               int n_split, tf_stream_t stream);
 /* layer.rs:2181-2257 with a pre-quantized activation:
- * gemv_q6_k_compact_global (logits) + argmax into *amax_key (see
+ * gemv_q6_k_compact_global (logits) + argmax into amax_key[TF_ARGMAX_SLOTS] (see
  * tf_gemv_q6k_head_argmax). */
 int tf_gemv_q6k_q8_argmax(const uint8_t *w, const int8_t *xq, const float *xd,
                           float *logits, int n_rows, int n_cols, int col_bytes,
@@ -279,14 +284,15 @@ int tf_gemv_q6k_compact_f32(const uint8_t *w, const float *x, float *out,
                             tf_stream_t stream);
 /* layer.rs:2158-2257: rms_norm_f32 (when norm_w != NULL) + quantize_q8 +
  * gemv_q6_k_compact_global (logits) + argmax_f32.  The argmax is
- * accumulated into *amax_key, which must hold 0 at launch; read it with
- * tf_argmax_key_finalize, which also resets it to 0. */
+ * accumulated as 64-bit keys into amax_key[TF_ARGMAX_SLOTS], which must
+ * hold zeros at launch; read it with tf_argmax_key_finalize, which also
+ * resets every slot to 0. */
 int tf_gemv_q6k_head_argmax(const uint8_t *w, const float *x,
                             const float *norm_w, float eps, float *logits,
                             int n_rows, int n_cols, int col_bytes,
                             unsigned long long *amax_key, tf_stream_t stream);
-/* *out_idx = index encoded in *amax_key (largest logit, lowest index among
- * exact ties); *amax_key = 0. */
+/* *out_idx = index of the largest key in amax_key[TF_ARGMAX_SLOTS] (largest
+ * logit, lowest index among exact ties); every slot is reset to 0. */
 int tf_argmax_key_finalize(unsigned long long *amax_key, int *out_idx,
                            tf_stream_t stream);
 

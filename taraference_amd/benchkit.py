@@ -33,28 +33,43 @@ def _copies(arr: np.ndarray, nbytes_each: int):
 
 
 def time_launches(launch, n_rot: int, iters: int, warmup: int = 3):
-    """launch(i) enqueues the kernel(s) on copy i % n_rot.  Returns
-    (per-launch mean us, back-to-back mean us)."""
+    """launch(i, stream) enqueues the kernel(s) on copy i % n_rot on `stream`.
+
+    Returns (per-launch mean us, back-to-back mean us):
+      - per-launch: an event pair around each eagerly launched kernel (this
+        includes the host launch latency of a lone launch);
+      - back-to-back: `iters` launches captured in one HIP graph, replayed
+        between one event pair on the stream the graph runs on, / iters —
+        the kernel's average launch duration with no host in the loop.
+    """
     stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
     for i in range(warmup):
-        launch(i % n_rot)
+        launch(i % n_rot, s)
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
         starts[i].record(stream)
-        launch(i % n_rot)
+        launch(i % n_rot, s)
         ends[i].record(stream)
     torch.cuda.synchronize()
-    per = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)])) * 1e3
+    per = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)])) * 1e3
+    cap = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for i in range(iters):
+            launch(i % n_rot, cap.cuda_stream)
+    graph.replay()  # upload + warm
+    torch.cuda.synchronize()
     b0 = torch.cuda.Event(enable_timing=True)
     b1 = torch.cuda.Event(enable_timing=True)
     b0.record(stream)
-    for i in range(iters):
-        launch(i % n_rot)
+    graph.replay()
     b1.record(stream)
     torch.cuda.synchronize()
     b2b = b0.elapsed_time(b1) * 1e3 / iters
+    del graph
     return per, b2b
 
 
@@ -73,10 +88,9 @@ def case_q4k_gemv(n_rows, n_cols, seed, iters):
     x = _dev(synth.activation(rng, n_rows))
     xq, xd = _q8(x)
     out = torch.empty(n_cols, device="cuda")
-    s = capi.stream_ptr()
     lib = capi.load()
 
-    def launch(i):
+    def launch(i, s):
         lib.tf_gemv_q4k_q8(ws[i].data_ptr(), xq.data_ptr(), xd.data_ptr(), out.data_ptr(),
                            n_rows, n_cols, cb, 0, None, 0, None, s)
 
@@ -96,15 +110,14 @@ def case_q4k_ffn(n_rows, n_cols, seed, iters, f32_x=True):
     x = _dev(synth.activation(rng, n_rows))
     xq, xd = _q8(x)
     out = torch.empty(n_cols, device="cuda")
-    s = capi.stream_ptr()
     lib = capi.load()
     if f32_x:
-        def launch(i):
+        def launch(i, s):
             lib.tf_gemv_q4k_ffn_f32(gs[i].data_ptr(), us[i].data_ptr(), x.data_ptr(),
                                     out.data_ptr(), n_rows, n_cols, cb, s)
         act = 4 * n_rows
     else:
-        def launch(i):
+        def launch(i, s):
             lib.tf_gemv_q4k_ffn(gs[i].data_ptr(), us[i].data_ptr(), xq.data_ptr(),
                                 xd.data_ptr(), out.data_ptr(), n_rows, n_cols, cb, s)
         act = n_rows + n_rows // 8
@@ -131,10 +144,9 @@ def case_q4k_qkv(n_rows, n_q, n_kv, seed, iters):
     v = torch.empty(n_kv, device="cuda")
     bq = torch.zeros(n_q, device="cuda")
     bk = torch.zeros(n_kv, device="cuda")
-    s = capi.stream_ptr()
     lib = capi.load()
 
-    def launch(i):
+    def launch(i, s):
         lib.tf_gemv_q4k_qkv(qs[i].data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
                             xq.data_ptr(), xd.data_ptr(), q.data_ptr(), k.data_ptr(),
                             v.data_ptr(), n_rows, n_q, n_kv, n_kv, cb, 1, bq.data_ptr(),
@@ -155,10 +167,9 @@ def case_q6k(n_rows, n_cols, seed, iters, entry="tf_gemv_q6k_down_splitk", use_r
     x = _dev(synth.activation(rng, n_rows))
     xq, xd = _q8(x)
     out = torch.zeros(n_cols, device="cuda")
-    s = capi.stream_ptr()
     fn = getattr(capi.load(), entry)
 
-    def launch(i):
+    def launch(i, s):
         fn(ws[i].data_ptr(), xq.data_ptr(), xd.data_ptr(), out.data_ptr(), n_rows, n_cols,
            ccb, 0, None, use_res, None, s)
 
@@ -181,10 +192,9 @@ def case_flash(L, n_head, n_kv, hd, seed, iters, n_split=None):
         n_split = lib.tf_flash_decode_n_split(n_kv, L)
     part = torch.empty(n_head * n_split * (2 + hd), device="cuda")
     out = torch.empty(n_head * hd, device="cuda")
-    s = capi.stream_ptr()
     scale = float(np.float32(1 / np.sqrt(hd)))
 
-    def launch(i):
+    def launch(i, s):
         lib.tf_flash_decode_partial(q.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
                                     part.data_ptr(), n_head, n_kv, hd, L - 1, 1, n_split,
                                     scale, s)

@@ -22,6 +22,7 @@
 
 #include "q4k.hpp"
 #include "q6k.hpp"
+#include "argmax_key.hpp"
 #include "tf_host.hpp"
 
 struct TfQkvArgs {
@@ -163,25 +164,8 @@ __global__ __launch_bounds__(256) void tf_fused_qkv_kernel(TfQkvArgs a, TfActSrc
 }
 
 // Q6_K compact rows with an activation source, a residual epilogue and an
-// optional argmax (ARGMAX: a 64-bit key max(value order, -index) is
-// accumulated per wave and merged with one atomicMax per wave).
-__device__ __forceinline__ unsigned long long tf_argmax_key(float v, int j) {
-    uint32_t u = __builtin_bit_cast(uint32_t, v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)j);
-}
-
-__device__ __forceinline__ unsigned long long tf_wave_max_u64(unsigned long long k) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)k, off, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), off, 64);
-        const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
+// optional argmax (ARGMAX: keys are max-merged per wave, then into the
+// wave's slot with one atomicMax).
 template <int SPR, int ITERS, bool ARGMAX>
 __global__ __launch_bounds__(256) void tf_q6k_rows_src_kernel(
     const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ out, int nb, int n_cols,
@@ -230,16 +214,14 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_src_kernel(
     }
     if (ARGMAX) {
         best = tf_wave_max_u64(best);
-        if (lane == 0 && best) atomicMax(amax, best);
+        if (lane == 0 && best) atomicMax(amax + (wave % TF_ARGMAX_SLOTS), best);
     }
 }
 
-__global__ void tf_argmax_key_finalize_kernel(unsigned long long* key, int* out_idx) {
-    if (threadIdx.x == 0) {
-        const unsigned long long k = *key;
-        *out_idx = k ? (int)(0xFFFFFFFFu - (uint32_t)k) : 0;
-        *key = 0ull;
-    }
+__global__ __launch_bounds__(256) void tf_argmax_key_finalize_kernel(unsigned long long* slots,
+                                                                     int* out_idx) {
+    const unsigned long long k = tf_argmax_slots_take(slots);
+    if (threadIdx.x == 0) *out_idx = tf_argmax_key_index(k);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -400,7 +382,7 @@ extern "C" int tf_gemv_q6k_head_argmax(const uint8_t* w, const float* x, const f
 extern "C" int tf_argmax_key_finalize(unsigned long long* amax_key, int* out_idx,
                                       tf_stream_t stream) {
     TF_CHECK_ARG(amax_key && out_idx);
-    hipLaunchKernelGGL(tf_argmax_key_finalize_kernel, dim3(1), dim3(64), 0, tf_stream(stream),
+    hipLaunchKernelGGL(tf_argmax_key_finalize_kernel, dim3(1), dim3(256), 0, tf_stream(stream),
                        amax_key, out_idx);
     return TF_LAUNCH_RESULT();
 }

@@ -99,6 +99,7 @@ __global__ __launch_bounds__(256) void tf_rms_norm_kernel(const float* __restric
 // strided partial sums, halving tree: levels 128 and 64 through LDS, the
 // rest as shfl_down pairs within wave 0, which adds the same pairs); the
 // quantization is bit-identical to tf_quantize_q8.
+template <int KMAX>  // KMAX * 256 >= n
 __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             float* __restrict__ xb,
@@ -108,11 +109,19 @@ __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restr
     __shared__ float buf[256];
     __shared__ float scale_s;
     const int tid = threadIdx.x;
-    float local = 0.f;
-    for (int i = tid; i < n; i += 256) {
-        const float v = x[i];
-        local = fmaf(v, v, local);  // fused, as under fmad=true
+    // Thread t owns x[t + 256k]: the reference's strided partial sums.  All
+    // loads are issued before the first use.
+    float xv[KMAX], wv[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        const int i = tid + 256 * k;
+        xv[k] = i < n ? x[i] : 0.f;
+        wv[k] = i < n ? w[i] : 0.f;
     }
+    float local = 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+        if (tid + 256 * k < n) local = fmaf(xv[k], xv[k], local);  // fused, as under fmad=true
     buf[tid] = local;
     __syncthreads();
     if (tid < 128) buf[tid] += buf[tid + 128];
@@ -129,19 +138,19 @@ __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restr
     }
     __syncthreads();
     const float scale = scale_s;
-    // quantize: lanes 0-31 / 32-63 own one 32-value group per step
-    const int lane = tid & 63, l32 = lane & 31;
-    const int groups = n / 32;
-    for (int g2 = (tid >> 6) * 2; g2 < groups; g2 += 8) {  // wave-uniform trip count
-        const int g = g2 + (lane >> 5);
-        const bool live = g < groups;
-        const float xi = live ? x[g * 32 + l32] * scale * w[g * 32 + l32] : 0.f;
+    // At step k, lanes 0-31 / 32-63 of a wave hold one whole 32-group
+    // (n % 32 == 0, so a group is either fully inside n or fully outside).
+    const int l32 = tid & 31;
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+        const int i = tid + 256 * k;
+        const float xi = xv[k] * scale * wv[k];
         const float amax = tf_group32_max(fabsf(xi));
         const float d = amax * (1.0f / 127.0f);
-        if (live) {
-            xb[g * 32 + l32] = xi;
-            q8[g * 32 + l32] = (int8_t)tf_q8_value(xi, amax, d);
-            if (l32 == 0) d8[g] = d;
+        if (i < n) {
+            xb[i] = xi;
+            q8[i] = (int8_t)tf_q8_value(xi, amax, d);
+            if (l32 == 0) d8[i >> 5] = d;
         }
     }
 }
@@ -250,9 +259,17 @@ extern "C" int tf_rms_norm(const float* x, const float* w, float* out, int n, fl
 
 extern "C" int tf_norm_quant(const float* x, const float* w, float eps, float* xb, int8_t* q8,
                              float* d8, int n, tf_stream_t stream) {
-    TF_CHECK_ARG(x && w && xb && q8 && d8 && n > 0 && (n % 32) == 0);
-    hipLaunchKernelGGL(tf_norm_quant_kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, xb,
-                       q8, d8, n, eps);
+    TF_CHECK_ARG(x && w && xb && q8 && d8 && n > 0 && (n % 32) == 0 && n <= 256 * 64);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, xb, q8, d8, n,
+                           eps);
+    };
+    const int per = (n + 255) / 256;
+    if (per <= 4) launch(tf_norm_quant_kernel<4>);
+    else if (per <= 8) launch(tf_norm_quant_kernel<8>);
+    else if (per <= 16) launch(tf_norm_quant_kernel<16>);
+    else if (per <= 32) launch(tf_norm_quant_kernel<32>);
+    else launch(tf_norm_quant_kernel<64>);
     return TF_LAUNCH_RESULT();
 }
 

@@ -26,6 +26,7 @@
 #include <new>
 #include <vector>
 
+#include "argmax_key.hpp"
 #include "op_api.hpp"
 #include "taraference_hip.h"
 
@@ -59,14 +60,11 @@ struct Layer {
 __global__ void tf_decode_advance_kernel(int* pos, int* step, int* token, const int* argmax,
                                          unsigned long long* amax_key, const int* forced,
                                          const int* n_forced, int* log) {
+    int next = 0;
+    if (amax_key) next = tf_argmax_key_index(tf_argmax_slots_take(amax_key));  // fused head
     if (threadIdx.x != 0) return;
     const int s = *step;
-    int next = *argmax;
-    if (amax_key) {  // fused head: decode and clear the argmax key
-        const unsigned long long k = *amax_key;
-        next = k ? (int)(0xFFFFFFFFu - (uint32_t)k) : 0;
-        *amax_key = 0ull;
-    }
+    if (!amax_key) next = *argmax;
     log[s] = next;
     *token = (s + 1 < *n_forced) ? forced[s + 1] : next;
     *pos += 1;
@@ -172,7 +170,7 @@ struct tf_model {
                      partial_stride);
         tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
         if (device_state) {
-            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
+            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(256), 0, s, d_pos, d_step,
                                d_token, d_argmax, nullptr, d_forced, d_nforced, d_log);
             tf::check((int)hipGetLastError(), "advance");
         }
@@ -241,7 +239,7 @@ struct tf_model {
             tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
         }
         if (device_state) {
-            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(64), 0, s, d_pos, d_step,
+            hipLaunchKernelGGL(tf_decode_advance_kernel, dim3(1), dim3(256), 0, s, d_pos, d_step,
                                d_token, d_argmax, keyed ? d_amax_key : nullptr, d_forced,
                                d_nforced, d_log);
             tf::check((int)hipGetLastError(), "advance");
@@ -370,8 +368,9 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->d_step = m->alloc<int>(1);
         m->d_token = m->alloc<int>(1);
         m->d_argmax = m->alloc<int>(1);
-        m->d_amax_key = m->alloc<unsigned long long>(1);
-        tf::check((int)hipMemset(m->d_amax_key, 0, sizeof(unsigned long long)), "memset");
+        m->d_amax_key = m->alloc<unsigned long long>(TF_ARGMAX_SLOTS);
+        tf::check((int)hipMemset(m->d_amax_key, 0, TF_ARGMAX_SLOTS * sizeof(unsigned long long)),
+                  "memset");
         m->d_nforced = m->alloc<int>(1);
         m->d_forced = m->alloc<int>(c.max_seq);
         m->d_log = m->alloc<int>(c.max_seq);
