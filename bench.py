@@ -203,6 +203,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--path", type=int, default=None,
+                    help="decode kernel sequence (tf_model_set_path); default: the library's")
     ap.add_argument("--only-roofline", action="store_true",
                     help="run only the copy calibration and the roofline kernel (for counter runs)")
     args = ap.parse_args()
@@ -227,6 +229,8 @@ def main():
     steps = max(2, args.steps)
     max_seq = args.warmup + steps + 8
     m = build_model(cfg, 0x7A7A0003, max_seq)
+    if args.path is not None:
+        m.set_path(args.path)
     log("[bench] decode ...")
     dt, toks = decode_throughput(m, cfg, args.warmup, steps, 3)
     tok_s = steps / dt

@@ -193,6 +193,31 @@ int tf_flash_decode_reduce(const float *partial, float *out, int n_head,
                            int head_dim, int n_split, int n_q,
                            tf_stream_t stream);
 
+/* kernels/attn/flash.cu:16/:119 + :222 in one launch (layer.rs:2040-2121):
+ * split-KV partials, then the log-sum-exp merge done by the last workgroup
+ * of each kv head to finish; when q8/d8 are non-NULL the merged output is
+ * also quantized to Q8 (quantize_q8 of the wo GEMV input, matmul.rs:191).
+ * pos0_dev non-NULL reads the position from device memory (graph capture).
+ * counters: n_kv unsigned ints, zero before the first call; every call
+ * leaves them zero.  partial as for tf_flash_decode_partial.  For
+ * n_split > 64 the merge runs as a second kernel. */
+int tf_flash_decode(const float *q, const uint16_t *k_cache,
+                    const uint16_t *v_cache, float *partial, unsigned *counters,
+                    float *out, int8_t *q8, float *d8, int n_head, int n_kv,
+                    int head_dim, int pos0, const int *pos0_dev, int n_split,
+                    float scale, tf_stream_t stream);
+/* flash.cu:222 attn_flash_reduce + quantize_q8 + gemv.cu:469
+ * gemv_q4_k_global (the attention output projection wo, layer.rs:2104-2119
+ * then matmul.rs:142): every workgroup merges the split-KV partials of all
+ * n_head heads (log-sum-exp, split order), quantizes the merged row to Q8 in
+ * LDS and runs the Q4_K GEMV on it; out[j] = dot (use_res 0) or out[j] +=
+ * dot (use_res 2).  n_head <= 32, n_head*head_dim % 256 == 0 and <= 4096,
+ * n_split <= 64, n_head*(n_split+1) <= 2048.  attn_out / attn_q8 / attn_d8
+ * (all NULL or all set) receive the merged row and its Q8. */
+int tf_gemv_q4k_flash_out(const uint8_t *w, const float *partial, int n_head,
+                          int head_dim, int n_split, float *out, int n_cols,
+                          int col_bytes, int use_res, float *attn_out,
+                          int8_t *attn_q8, float *attn_d8, tf_stream_t stream);
 /* Partition count this library recommends for a context of max_seq tokens
  * (a multiple of 8; 8 for short contexts).  The reference fixes 8
  * (cuda/decode.rs:38-41); on MI355X long contexts need more partitions to
@@ -257,7 +282,7 @@ int tf_fused_qkv_rope_kv(const int8_t *xq, const float *xd, const float *xb,
                          tf_stream_t stream);
 /* ops.cu:4-34 rms_norm_f32 + gemv.cu:43-65 quantize_q8_global, one launch:
  * xb = x * rsqrt(mean x^2 + eps) * w and its Q8 (q8[n], d8[n/32]);
- * n % 32 == 0, n <= 16384. */
+ * n % 128 == 0, n <= 8192; x, w, xb 8-byte aligned. */
 int tf_norm_quant(const float *x, const float *w, float eps, float *xb,
                   int8_t *q8, float *d8, int n, tf_stream_t stream);
 /* flash.cu:222 attn_flash_reduce + quantize_q8 of the attention output
@@ -356,11 +381,18 @@ int tf_model_forward(tf_model *m, int token, int pos, int *next_token,
  * synchronized once, at the end. */
 int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
                       int n_gen, int *tokens, int use_graph, tf_stream_t stream);
-/* Select the kernel sequence of a step: fused != 0 (default) uses the fused
- * decode kernels (six launches per layer); 0 uses the reference's sequence
- * through the operator API (cuda/layer.rs order, one launch per reference
- * kernel).  Both compute the same step. */
-int tf_model_set_path(tf_model *m, int fused);
+/* Select the kernel sequence of a step (all compute the same step):
+ *   0  the reference's sequence through the operator API (cuda/layer.rs
+ *      order, one launch per reference kernel);
+ *   1  fused kernels, each activation normalized / quantized once by its
+ *      own launch (nine launches per layer);
+ *   2  fused kernels with the normalization / quantization and
+ *      the attention merge in the consuming GEMV's prologue (five launches
+ *      per layer);
+ *   3  (default) as 2, with h quantized by its own launch before a Q8
+ *      ffn_down.
+ * Changing the path drops the captured graph. */
+int tf_model_set_path(tf_model *m, int path);
 /* Device pointer of the last logits (n_vocab floats) and of the f16 K/V
  * cache of layer li. */
 const float *tf_model_logits(const tf_model *m);

@@ -72,14 +72,14 @@ __device__ __forceinline__ float tf_q4k_row(const uint8_t* col, bool valid, int 
 // rotation happens in registers; V rows follow.  Task map: pair tasks first
 // (UNITS/2 pairs per wave pass, or one pair in two passes when a row takes
 // the whole wave), then V tasks (UNITS rows per pass).
-template <int SPR, int ITERS>
-__global__ __launch_bounds__(256) void tf_fused_qkv_kernel(TfQkvArgs a, TfActSrc src, int nb) {
+template <int SPR, int ITERS, int SK>
+__global__ __launch_bounds__(TF_BT_QKV) void tf_fused_qkv_kernel(TfQkvArgs a, TfActSrc src, int nb) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int UNITS = 16 / SPR;
     constexpr int PPT = UNITS >= 2 ? UNITS / 2 : 1;
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int hd = a.head_dim, half = hd / 2;
     const int n_pairs = (a.n_q + a.n_k) / 2;
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void tf_fused_qkv_kernel(TfQkvArgs a, TfActSrc
     const int v_tasks = (a.n_v + UNITS - 1) / UNITS;
     const int n_tasks = pair_tasks + v_tasks;
     const int pos = a.pos_dev ? a.pos_dev[0] : a.pos;
-    tf_stage_act<true>(src, nb, lds);
+    tf_stage_act<true, SK>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     const bool lead = (lane & (4 * SPR - 1)) == 0;
     for (int task = wave; task < n_tasks; task += nwaves) {
@@ -166,15 +166,15 @@ __global__ __launch_bounds__(256) void tf_fused_qkv_kernel(TfQkvArgs a, TfActSrc
 // Q6_K compact rows with an activation source, a residual epilogue and an
 // optional argmax (ARGMAX: keys are max-merged per wave, then into the
 // wave's slot with one atomicMax).
-template <int SPR, int ITERS, bool ARGMAX>
-__global__ __launch_bounds__(256) void tf_q6k_rows_src_kernel(
+template <int SPR, int ITERS, bool ARGMAX, int SK>
+__global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q6k_rows_src_kernel(
     const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ out, int nb, int n_cols,
     int col_bytes, int use_res, unsigned long long* __restrict__ amax) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_tasks = (n_cols + UNITS - 1) / UNITS;
     int task = wave;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_src_kernel(
     if (ITERS > 0 && task < n_tasks)
         tf_q6k_row_load<SPR, ITERS>(w + (size_t)(j < n_cols ? j : 0) * col_bytes, j < n_cols, 0,
                                     nb, sir, p, cur);
-    tf_stage_act<false>(src, nb, lds);
+    tf_stage_act<false, SK>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     unsigned long long best = 0;
     for (; task < n_tasks; task += nwaves) {
@@ -243,13 +243,14 @@ static void tf_fused_dispatch(int len, F&& f) {
     }
 }
 
-static TfActSrc tf_src_of(const float* x, const float* norm_w, float eps) {
-    return TfActSrc{norm_w ? TF_SRC_NORM : TF_SRC_F32, nullptr, nullptr, x, norm_w, eps};
+static TfActSrc tf_src_of(const float* x, const float* norm_w, float eps, int n_x) {
+    return TfActSrc{norm_w ? TF_SRC_NORM : TF_SRC_F32, nullptr, nullptr, x, norm_w, eps, n_x};
 }
 
 static int tf_q6k_src_launch(const uint8_t* w, const TfActSrc& src, float* out, int n_rows,
                              int n_cols, int col_bytes, int use_res, unsigned long long* amax,
                              tf_stream_t stream) {
+    TF_CHECK_ARG(tf_src_ok(src) && src.kind != TF_SRC_FLASH);
     const int nb = n_rows / 256;
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
@@ -257,14 +258,20 @@ static int tf_q6k_src_launch(const uint8_t* w, const TfActSrc& src, float* out, 
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         const int tasks = (n_cols + 16 / SPR - 1) / (16 / SPR);
         if (amax) {
-            auto fn = tf_q6k_rows_src_kernel<SPR, IT, true>;
-            const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-            hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, src, out, nb,
+            auto fn = tf_sk_pick(src.kind, tf_q6k_rows_src_kernel<SPR, IT, true, TF_SRC_Q8>,
+                                 tf_q6k_rows_src_kernel<SPR, IT, true, TF_SRC_F32>,
+                                 tf_q6k_rows_src_kernel<SPR, IT, true, TF_SRC_NORM>);
+            const int BT = tf_block_threads(tf_bt_rows(SPR), tasks);
+            const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+            hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), w, src, out, nb,
                                n_cols, col_bytes, use_res, amax);
         } else {
-            auto fn = tf_q6k_rows_src_kernel<SPR, IT, false>;
-            const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-            hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, src, out, nb,
+            auto fn = tf_sk_pick(src.kind, tf_q6k_rows_src_kernel<SPR, IT, false, TF_SRC_Q8>,
+                                 tf_q6k_rows_src_kernel<SPR, IT, false, TF_SRC_F32>,
+                                 tf_q6k_rows_src_kernel<SPR, IT, false, TF_SRC_NORM>);
+            const int BT = tf_block_threads(tf_bt_rows(SPR), tasks);
+            const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+            hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), w, src, out, nb,
                                n_cols, col_bytes, use_res, amax);
         }
         rc = TF_LAUNCH_RESULT();
@@ -294,17 +301,21 @@ extern "C" int tf_fused_norm_qkv_rope_kv(
     TfQkvArgs a{wq, wk, wv, bq, bk, bv, n_head * head_dim, n_kv * head_dim, n_kv * head_dim,
                 col_bytes_qk, col_bytes_v, v_type == TF_TYPE_Q6_K ? 1 : 0, q_out, k_cache, v_cache,
                 n_kv * head_dim, pos, pos_dev, theta, head_dim};
-    const TfActSrc src = tf_src_of(x, norm_w, eps);
+    const TfActSrc src = tf_src_of(x, norm_w, eps, n_embd);
+    TF_CHECK_ARG(tf_src_ok(src) && src.kind != TF_SRC_FLASH);
     const int lds = tf_act_lds_bytes(nb, true);
     int rc = 0;
     tf_fused_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         constexpr int UNITS = 16 / SPR;
         constexpr int PPT = UNITS >= 2 ? UNITS / 2 : 1;
-        auto fn = tf_fused_qkv_kernel<SPR, IT>;
+        auto fn = tf_sk_pick(src.kind, tf_fused_qkv_kernel<SPR, IT, TF_SRC_Q8>,
+                             tf_fused_qkv_kernel<SPR, IT, TF_SRC_F32>,
+                             tf_fused_qkv_kernel<SPR, IT, TF_SRC_NORM>);
         const int tasks = ((a.n_q + a.n_k) / 2 + PPT - 1) / PPT + (a.n_v + UNITS - 1) / UNITS;
-        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), a, src, nb);
+        const int BT = tf_block_threads(TF_BT_QKV, tasks);
+        const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), a, src, nb);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -339,10 +350,13 @@ extern "C" int tf_fused_qkv_rope_kv(const int8_t* xq, const float* xd, const flo
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         constexpr int UNITS = 16 / SPR;
         constexpr int PPT = UNITS >= 2 ? UNITS / 2 : 1;
-        auto fn = tf_fused_qkv_kernel<SPR, IT>;
+        auto fn = tf_sk_pick(src.kind, tf_fused_qkv_kernel<SPR, IT, TF_SRC_Q8>,
+                             tf_fused_qkv_kernel<SPR, IT, TF_SRC_F32>,
+                             tf_fused_qkv_kernel<SPR, IT, TF_SRC_NORM>);
         const int tasks = ((a.n_q + a.n_k) / 2 + PPT - 1) / PPT + (a.n_v + UNITS - 1) / UNITS;
-        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), a, src, nb);
+        const int BT = tf_block_threads(TF_BT_QKV, tasks);
+        const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), a, src, nb);
         rc = TF_LAUNCH_RESULT();
     });
     return rc;
@@ -364,7 +378,7 @@ extern "C" int tf_gemv_q6k_compact_f32(const uint8_t* w, const float* x, float* 
     const int nb = n_rows / 256;
     TF_CHECK_ARG(w && x && out && nb > 0 && n_cols > 0 && (use_res == 0 || use_res == 2));
     TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212);
-    return tf_q6k_src_launch(w, tf_src_of(x, nullptr, 0.f), out, n_rows, n_cols, col_bytes,
+    return tf_q6k_src_launch(w, tf_src_of(x, nullptr, 0.f, n_rows), out, n_rows, n_cols, col_bytes,
                              use_res, nullptr, stream);
 }
 
@@ -375,7 +389,7 @@ extern "C" int tf_gemv_q6k_head_argmax(const uint8_t* w, const float* x, const f
     const int nb = n_rows / 256;
     TF_CHECK_ARG(w && x && logits && amax_key && nb > 0 && n_cols > 0);
     TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212);
-    return tf_q6k_src_launch(w, tf_src_of(x, norm_w, eps), logits, n_rows, n_cols, col_bytes, 0,
+    return tf_q6k_src_launch(w, tf_src_of(x, norm_w, eps, n_rows), logits, n_rows, n_cols, col_bytes, 0,
                              amax_key, stream);
 }
 

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void tf_rms_norm_kernel(const float* __restric
 // strided partial sums, halving tree: levels 128 and 64 through LDS, the
 // rest as shfl_down pairs within wave 0, which adds the same pairs); the
 // quantization is bit-identical to tf_quantize_q8.
-template <int KMAX>  // KMAX * 256 >= n
+template <int STEPS>  // STEPS * 512 >= n
 __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             float* __restrict__ xb,
@@ -108,20 +108,31 @@ __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restr
                                                             float eps) {
     __shared__ float buf[256];
     __shared__ float scale_s;
-    const int tid = threadIdx.x;
-    // Thread t owns x[t + 256k]: the reference's strided partial sums.  All
-    // loads are issued before the first use.
-    float xv[KMAX], wv[KMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Quantization layout: at step k lane L of wave w holds the value pair
+    // e0 = 512k + 128w + 2L, e0 + 1 (16 lanes of a DPP row = one 32-group).
+    float2 xv[STEPS], wv[STEPS];
 #pragma unroll
-    for (int k = 0; k < KMAX; k++) {
-        const int i = tid + 256 * k;
-        xv[k] = i < n ? x[i] : 0.f;
-        wv[k] = i < n ? w[i] : 0.f;
+    for (int k = 0; k < STEPS; k++) {
+        const int e0 = 512 * k + 128 * wave + 2 * lane;
+        if (512 * k + 128 * wave < n) {
+            xv[k] = *reinterpret_cast<const float2*>(x + e0);
+            wv[k] = *reinterpret_cast<const float2*>(w + e0);
+        }
     }
+    // Sum of squares in the reference's order: thread t owns x[t + 256j].
     float local = 0.f;
+    {
+        float v[2 * STEPS];
 #pragma unroll
-    for (int k = 0; k < KMAX; k++)
-        if (tid + 256 * k < n) local = fmaf(xv[k], xv[k], local);  // fused, as under fmad=true
+        for (int j = 0; j < 2 * STEPS; j++) {
+            const int i = tid + 256 * j;
+            v[j] = i < n ? x[i] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 2 * STEPS; j++)
+            if (tid + 256 * j < n) local = fmaf(v[j], v[j], local);  // fused, as under fmad=true
+    }
     buf[tid] = local;
     __syncthreads();
     if (tid < 128) buf[tid] += buf[tid + 128];
@@ -138,20 +149,19 @@ __global__ __launch_bounds__(256) void tf_norm_quant_kernel(const float* __restr
     }
     __syncthreads();
     const float scale = scale_s;
-    // At step k, lanes 0-31 / 32-63 of a wave hold one whole 32-group
-    // (n % 32 == 0, so a group is either fully inside n or fully outside).
-    const int l32 = tid & 31;
+    const int m = lane & 15;
 #pragma unroll
-    for (int k = 0; k < KMAX; k++) {
-        const int i = tid + 256 * k;
-        const float xi = xv[k] * scale * wv[k];
-        const float amax = tf_group32_max(fabsf(xi));
-        const float d = amax * (1.0f / 127.0f);
-        if (i < n) {
-            xb[i] = xi;
-            q8[i] = (int8_t)tf_q8_value(xi, amax, d);
-            if (l32 == 0) d8[i >> 5] = d;
-        }
+    for (int k = 0; k < STEPS; k++) {
+        const int wbase = 512 * k + 128 * wave;
+        if (wbase >= n) break;  // n % 128 == 0 here: whole wave spans
+        const int e0 = wbase + 2 * lane;
+        const float x0 = xv[k].x * scale * wv[k].x;
+        const float x1 = xv[k].y * scale * wv[k].y;
+        const TfQ8Pair r = tf_q8_pair<false>(x0, x1);
+        *reinterpret_cast<float2*>(xb + e0) = make_float2(x0, x1);
+        q8[e0] = (int8_t)r.q0;
+        q8[e0 + 1] = (int8_t)r.q1;
+        if (m == 0) d8[e0 >> 5] = r.d;
     }
 }
 
@@ -259,17 +269,18 @@ extern "C" int tf_rms_norm(const float* x, const float* w, float* out, int n, fl
 
 extern "C" int tf_norm_quant(const float* x, const float* w, float eps, float* xb, int8_t* q8,
                              float* d8, int n, tf_stream_t stream) {
-    TF_CHECK_ARG(x && w && xb && q8 && d8 && n > 0 && (n % 32) == 0 && n <= 256 * 64);
+    TF_CHECK_ARG(x && w && xb && q8 && d8 && n > 0 && (n % 128) == 0 && n <= 8192);
+    TF_CHECK_ARG(((uintptr_t)x & 7) == 0 && ((uintptr_t)w & 7) == 0 && ((uintptr_t)xb & 7) == 0);
     auto launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(1), dim3(256), 0, tf_stream(stream), x, w, xb, q8, d8, n,
                            eps);
     };
-    const int per = (n + 255) / 256;
-    if (per <= 4) launch(tf_norm_quant_kernel<4>);
-    else if (per <= 8) launch(tf_norm_quant_kernel<8>);
-    else if (per <= 16) launch(tf_norm_quant_kernel<16>);
-    else if (per <= 32) launch(tf_norm_quant_kernel<32>);
-    else launch(tf_norm_quant_kernel<64>);
+    const int steps = (n + 511) / 512;
+    if (steps <= 1) launch(tf_norm_quant_kernel<1>);
+    else if (steps <= 2) launch(tf_norm_quant_kernel<2>);
+    else if (steps <= 4) launch(tf_norm_quant_kernel<4>);
+    else if (steps <= 8) launch(tf_norm_quant_kernel<8>);
+    else launch(tf_norm_quant_kernel<16>);
     return TF_LAUNCH_RESULT();
 }
 

@@ -5,9 +5,9 @@
 // gemv_q4_k_dual (:2401), gemv_q4_k_ffn{,_4way,_8way} (:2440-2619),
 // gemv_q4_k_ffn_mcol (:2546) and gemv_q4_k_qkv (:2662).
 //
-// Every kernel is a persistent grid of 256-thread workgroups sized from the
-// occupancy of the kernel: each workgroup stages the Q8 activation in LDS
-// once, then each wave loops over row tasks.  See q4k.hpp for the lane map.
+// Every kernel is a persistent grid of workgroups sized from the occupancy
+// of the kernel: each workgroup stages the activation in LDS once, then each
+// wave loops over row tasks.  See q4k.hpp for the lane map.
 #include <type_traits>
 
 #include "q4k.hpp"
@@ -60,15 +60,15 @@ __device__ __forceinline__ TfRowSel tf_sel3(const TfQ4kMats& m, int r, int n_tot
 }
 
 // Rows of up to three matrices that share K (global / pair / qkv).
-template <int SPR, int ITERS>
-__global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
+template <int SPR, int ITERS, int SK>
+__global__ __launch_bounds__(tf_bt_rows(SPR, SK)) void tf_q4k_rows_kernel(
     TfQ4kMats m, TfActSrc src, int nb, int col_bytes, int use_bias, int use_res,
     const float* __restrict__ residual) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_total = m.n0 + m.n1 + m.n2;
     const int n_tasks = (n_total + UNITS - 1) / UNITS;
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void tf_q4k_rows_kernel(
     TfRowSel cs = tf_sel3(m, task * UNITS + unit, n_total, col_bytes);
     TfQ4kRow<ITERS> cur, nxt;
     if (ITERS > 0 && task < n_tasks) tf_q4k_row_load<SPR, ITERS>(cs.col, cs.valid, 0, nb, sir, t, cur);
-    tf_stage_act<false>(src, nb, lds);
+    tf_stage_act<false, SK>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     for (; task < n_tasks; task += nwaves) {
         const int nt = task + nwaves;
@@ -116,15 +116,15 @@ __device__ __forceinline__ void tf_pair_write(float g, float u, float* out_a, fl
 // Equal-width pair on the same output index: MODE 0 writes
 // silu(gate)*up (ffn), MODE 1 writes both dots (dual).  xf != nullptr means
 // the activation is f32 and is quantized into LDS by each workgroup.
-template <int SPR, int ITERS, int MODE>
-__global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
+template <int SPR, int ITERS, int MODE, int SK>
+__global__ __launch_bounds__(tf_bt_pair(SPR)) void tf_q4k_pair_rows_kernel(
     const uint8_t* __restrict__ wa, const uint8_t* __restrict__ wb,
     TfActSrc src, float* __restrict__ out_a, float* __restrict__ out_b, int nb, int n_cols,
     int col_bytes) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     if constexpr (SPR <= 8) {
         // even unit = gate row j, odd unit = up row j
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
         TfQ4kRow<ITERS> cur, nxt;
         if (task < n_tasks)
             tf_q4k_row_load<SPR, ITERS>(w + (size_t)j * col_bytes, j < n_cols, 0, nb, sir, t, cur);
-        tf_stage_act<false>(src, nb, lds);
+        tf_stage_act<false, SK>(src, nb, lds);
         const TfAct x = tf_act_view(lds, nb);
         for (; task < n_tasks; task += nwaves) {
             const int nt = task + nwaves;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void tf_q4k_pair_rows_kernel(
             tf_q4k_row_load<SPR, ITERS>(wa + (size_t)j * col_bytes, true, 0, nb, sir, t, cg);
             tf_q4k_row_load<SPR, ITERS>(wb + (size_t)j * col_bytes, true, 0, nb, sir, t, cu);
         }
-        tf_stage_act<false>(src, nb, lds);
+        tf_stage_act<false, SK>(src, nb, lds);
         const TfAct x = tf_act_view(lds, nb);
         for (; j < n_cols; j += nwaves) {
             const int jn = j + nwaves;
@@ -193,12 +193,12 @@ __global__ __launch_bounds__(256) void tf_q4k_splitk_kernel(
     const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ partial, int nb,
     int n_cols, int col_bytes, int n_split) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_act<false>(src, nb, lds);
+    tf_stage_act<false, TF_SRC_Q8>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_total = n_split * n_cols;
     for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
@@ -313,16 +313,21 @@ static TfActSrc tf_src_f32(const float* x) {
 
 static int tf_q4k_rows(const TfQ4kMats& m, const TfActSrc& src, int n_rows, int col_bytes,
                        int use_bias, int use_res, const float* residual, tf_stream_t stream) {
+    TF_CHECK_ARG(tf_src_ok(src));
     const int nb = n_rows / 256;
     const int n_total = m.n0 + m.n1 + m.n2;
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q4k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
-        auto fn = tf_q4k_rows_kernel<SPR, IT>;
+        auto fn = tf_sk_pick(src.kind, tf_q4k_rows_kernel<SPR, IT, TF_SRC_Q8>,
+                             tf_q4k_rows_kernel<SPR, IT, TF_SRC_F32>,
+                             tf_q4k_rows_kernel<SPR, IT, TF_SRC_NORM>,
+                             tf_q4k_rows_kernel<SPR, IT, TF_SRC_FLASH>);
         const int tasks = (n_total + 16 / SPR - 1) / (16 / SPR);
-        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), m, src, nb,
+        const int BT = tf_block_threads(tf_bt_rows(SPR, src.kind), tasks);
+        const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), m, src, nb,
                            col_bytes, use_bias, use_res, residual);
         rc = TF_LAUNCH_RESULT();
     });
@@ -332,18 +337,23 @@ static int tf_q4k_rows(const TfQ4kMats& m, const TfActSrc& src, int n_rows, int 
 static int tf_q4k_pair_rows(const uint8_t* wa, const uint8_t* wb, const TfActSrc& src,
                             float* out_a, float* out_b, int n_rows, int n_cols, int col_bytes,
                             int mode, tf_stream_t stream) {
+    TF_CHECK_ARG(tf_src_ok(src) && src.kind != TF_SRC_FLASH);
     const int nb = n_rows / 256;
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
     tf_q4k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
-        auto fn0 = tf_q4k_pair_rows_kernel<SPR, IT, 0>;
-        auto fn1 = tf_q4k_pair_rows_kernel<SPR, IT, 1>;
-        auto fn = mode == 0 ? fn0 : fn1;
+        auto fn = mode == 0 ? tf_sk_pick(src.kind, tf_q4k_pair_rows_kernel<SPR, IT, 0, TF_SRC_Q8>,
+                                         tf_q4k_pair_rows_kernel<SPR, IT, 0, TF_SRC_F32>,
+                                         tf_q4k_pair_rows_kernel<SPR, IT, 0, TF_SRC_NORM>)
+                            : tf_sk_pick(src.kind, tf_q4k_pair_rows_kernel<SPR, IT, 1, TF_SRC_Q8>,
+                                         tf_q4k_pair_rows_kernel<SPR, IT, 1, TF_SRC_F32>,
+                                         tf_q4k_pair_rows_kernel<SPR, IT, 1, TF_SRC_NORM>);
         const int jpw = SPR <= 8 ? 16 / SPR / 2 : 1;
         const int tasks = (n_cols + jpw - 1) / jpw;
-        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), wa, wb, src, out_a,
+        const int BT = tf_block_threads(tf_bt_pair(SPR), tasks);
+        const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), wa, wb, src, out_a,
                            out_b, nb, n_cols, col_bytes);
         rc = TF_LAUNCH_RESULT();
     });
@@ -363,6 +373,22 @@ extern "C" int tf_gemv_q4k_q8(const uint8_t* w, const int8_t* xq, const float* x
     TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, bias, nullptr, nullptr,
                 n_cols, 0, 0};
     return tf_q4k_rows(m, tf_src_q8(xq, xd), n_rows, col_bytes, use_bias, use_res, residual, stream);
+}
+
+extern "C" int tf_gemv_q4k_flash_out(const uint8_t* w, const float* partial, int n_head,
+                                     int head_dim, int n_split, float* out, int n_cols,
+                                     int col_bytes, int use_res, float* attn_out,
+                                     int8_t* attn_q8, float* attn_d8, tf_stream_t stream) {
+    const int n_rows = n_head * head_dim;
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(n_head > 0 && n_head <= 32 && n_rows % 256 == 0 && n_rows <= 4096 && n_cols > 0);
+    TF_CHECK_ARG(n_split >= 1 && n_split <= 64 && n_head * (n_split + 1) <= TF_FLASH_STAGE_W);
+    TF_CHECK_ARG(tf_q4k_weights_ok(w, nb, col_bytes) && out && (use_res == 0 || use_res == 2));
+    TfQ4kMats m{w, nullptr, nullptr, out, nullptr, nullptr, nullptr, nullptr, nullptr,
+                n_cols, 0, 0};
+    const TfActSrc src{TF_SRC_FLASH, nullptr, nullptr, partial, nullptr, 0.f, n_split, head_dim,
+                       attn_out, attn_q8, attn_d8};
+    return tf_q4k_rows(m, src, n_rows, col_bytes, 0, use_res, nullptr, stream);
 }
 
 extern "C" int tf_gemv_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
@@ -443,7 +469,7 @@ extern "C" int tf_gemv_q4k_ffn_norm(const uint8_t* gate, const uint8_t* up, cons
     TF_CHECK_ARG(nb > 0 && n_cols > 0);
     TF_CHECK_ARG(tf_q4k_weights_ok(gate, nb, col_bytes) && tf_q4k_weights_ok(up, nb, col_bytes));
     TF_CHECK_ARG(x && norm_w && out);
-    return tf_q4k_pair_rows(gate, up, TfActSrc{TF_SRC_NORM, nullptr, nullptr, x, norm_w, eps}, out,
+    return tf_q4k_pair_rows(gate, up, TfActSrc{TF_SRC_NORM, nullptr, nullptr, x, norm_w, eps, n_rows}, out,
                             nullptr, n_rows, n_cols, col_bytes, 0, stream);
 }
 

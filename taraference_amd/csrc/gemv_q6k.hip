@@ -14,8 +14,8 @@
 #include "q6k.hpp"
 #include "tf_host.hpp"
 
-template <int SPR, int ITERS>
-__global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
+template <int SPR, int ITERS, int SK>
+__global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q6k_rows_kernel(
     const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ out, int nb, int n_cols,
     int col_bytes, int use_bias, const float* __restrict__ bias, int use_res,
     const float* __restrict__ residual) {
@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_tasks = (n_cols + UNITS - 1) / UNITS;
     int task = wave;
@@ -32,7 +32,7 @@ __global__ __launch_bounds__(256) void tf_q6k_rows_kernel(
     if (ITERS > 0 && task < n_tasks)
         tf_q6k_row_load<SPR, ITERS>(w + (size_t)(j < n_cols ? j : 0) * col_bytes, j < n_cols, 0,
                                     nb, sir, p, cur);
-    tf_stage_act<false>(src, nb, lds);
+    tf_stage_act<false, SK>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     for (; task < n_tasks; task += nwaves) {
         const int nt = task + nwaves;
@@ -65,12 +65,12 @@ __global__ __launch_bounds__(256) void tf_q6k_splitk_kernel(
     const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ partial, int nb,
     int n_cols, int col_bytes, int n_split) {
     extern __shared__ __align__(16) uint8_t lds[];
-    tf_stage_act<false>(src, nb, lds);
+    tf_stage_act<false, TF_SRC_Q8>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     constexpr int UNITS = 16 / SPR;
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int n_total = n_split * n_cols;
     for (int r0 = wave * UNITS; r0 < n_total; r0 += nwaves * UNITS) {
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void tf_q6k_f32_kernel(
     const int lane = threadIdx.x & 63;
     const int p = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
     const int n = p >> 1, h = p & 1;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int wave = tf_wave_id();
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     for (int r0 = wave * UNITS; r0 < n_cols; r0 += nwaves * UNITS) {
         const int j = r0 + unit;
@@ -235,6 +235,7 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
 static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_rows,
                        int n_cols, int col_bytes, int use_bias, const float* bias, int use_res,
                        const float* residual, tf_stream_t stream) {
+    TF_CHECK_ARG(tf_src_ok(src) && src.kind != TF_SRC_FLASH);
     const int nb = n_rows / 256;
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q6c_weights_ok(w, nb, col_bytes));
     TF_CHECK_ARG(out && (!use_bias || bias) && use_res >= 0 && use_res <= 2);
@@ -244,10 +245,13 @@ static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_
     int rc = 0;
     tf_q6k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
-        auto fn = tf_q6k_rows_kernel<SPR, IT>;
+        auto fn = tf_sk_pick(src.kind, tf_q6k_rows_kernel<SPR, IT, TF_SRC_Q8>,
+                             tf_q6k_rows_kernel<SPR, IT, TF_SRC_F32>,
+                             tf_q6k_rows_kernel<SPR, IT, TF_SRC_NORM>);
         const int tasks = (n_cols + 16 / SPR - 1) / (16 / SPR);
-        const int blocks = tf_persistent_blocks((const void*)fn, 256, lds, tasks);
-        hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, tf_stream(stream), w, src, out, nb,
+        const int BT = tf_block_threads(tf_bt_rows(SPR), tasks);
+        const int blocks = tf_persistent_blocks((const void*)fn, BT, lds, tasks);
+        hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), lds, tf_stream(stream), w, src, out, nb,
                            n_cols, col_bytes, use_bias, bias, use_res, residual);
         rc = TF_LAUNCH_RESULT();
     });

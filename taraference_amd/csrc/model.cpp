@@ -98,7 +98,12 @@ struct tf_model {
     // device decode state
     int *d_pos = nullptr, *d_step = nullptr, *d_token = nullptr, *d_argmax = nullptr;
     unsigned long long* d_amax_key = nullptr;
-    bool fused = true;
+    // 0: the reference operator sequence (step); 1: fused, each activation
+    // normalized and quantized once by its own kernel; 2: fused, the
+    // normalization / quantization / attention merge runs in the consuming
+    // GEMV's prologue; 3: as 2 but h is quantized by its own kernel.
+    int path = 3;
+    unsigned* d_flash_cnt = nullptr;  // per-kv-head tickets of tf_flash_decode
     int *d_forced = nullptr, *d_nforced = nullptr, *d_log = nullptr;
     std::vector<void*> allocs;
 
@@ -180,7 +185,8 @@ struct tf_model {
     // quantized once (tf_norm_quant, or the flash reduce for the attention
     // output), QKV + RoPE + KV append run in one GEMV launch, and the head
     // carries the argmax: nine launches per layer.
-    void step_fused(hipStream_t s, int token, int pos, bool device_state) {
+    void step_fused(hipStream_t s, int token, int pos, bool device_state, bool prologue,
+                    bool q8_down) {
         const tf_model_config& c = cfg;
         const int* pos_dev = device_state ? d_pos : nullptr;
         const int* tok_dev = device_state ? d_token : nullptr;
@@ -193,40 +199,85 @@ struct tf_model {
                 L.wq.col_bytes != L.wk.col_bytes || L.gate.wtype != tf::WType::Q4K ||
                 L.up.wtype != tf::WType::Q4K)
                 throw tf::HipError(1, "fused path needs Q4_K q/k/gate/up");
-            tf::check(tf_norm_quant(x, L.attn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
-                      "norm_quant");
-            tf::check(tf_fused_qkv_rope_kv(
-                          q8_x, q8_d, xb, L.wq.data, L.wk.data, L.wv.data,
-                          L.wv.wtype == tf::WType::Q6K ? TF_TYPE_Q6_K : TF_TYPE_Q4_K, L.bq, L.bk,
-                          L.bv, c.n_embd, c.n_head, c.n_kv, c.head_dim, (int)L.wq.col_bytes,
-                          (int)L.wv.col_bytes, q, kc[li], vc[li], pos, pos_dev, c.rope_theta, s),
-                      "fused qkv");
-            if (pos_dev)
-                tf::check(tf_flash_decode_partial_d(q, kc[li], vc[li], flash_partial, fd.n_head,
-                                                    fd.n_kv, fd.head_dim, pos_dev, 1, fd.n_split,
-                                                    fd.scale, s),
-                          "flash partial");
-            else
-                tf::check(tf_flash_decode_partial(q, kc[li], vc[li], flash_partial, fd.n_head,
-                                                  fd.n_kv, fd.head_dim, pos, 1, fd.n_split,
-                                                  fd.scale, s),
-                          "flash partial");
-            tf::check(tf_flash_decode_reduce_q8(flash_partial, xb, q8_x, q8_d, fd.n_head,
-                                                fd.head_dim, fd.n_split, s),
-                      "flash reduce");
-            gemv_q8_inplace(s, L.wo);
-            tf::check(tf_norm_quant(x, L.ffn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
-                      "norm_quant");
-            tf::check(tf_gemv_q4k_ffn(L.gate.data, L.up.data, q8_x, q8_d, hb, c.n_embd, c.n_ff,
-                                      (int)L.gate.col_bytes, s),
-                      "ffn");
-            tf::check(tf_quantize_q8(hb, q8_x, q8_d, c.n_ff, s), "quantize h");
-            gemv_q8_inplace(s, L.down);
+            const int v_type = L.wv.wtype == tf::WType::Q6K ? TF_TYPE_Q6_K : TF_TYPE_Q4_K;
+            if (prologue) {
+                tf::check(tf_fused_norm_qkv_rope_kv(
+                              x, L.attn_norm, c.rms_eps, L.wq.data, L.wk.data, L.wv.data, v_type,
+                              L.bq, L.bk, L.bv, c.n_embd, c.n_head, c.n_kv, c.head_dim,
+                              (int)L.wq.col_bytes, (int)L.wv.col_bytes, q, kc[li], vc[li], pos,
+                              pos_dev, c.rope_theta, s),
+                          "norm+qkv");
+            } else {
+                tf::check(tf_norm_quant(x, L.attn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                          "norm_quant");
+                tf::check(tf_fused_qkv_rope_kv(q8_x, q8_d, xb, L.wq.data, L.wk.data, L.wv.data,
+                                               v_type, L.bq, L.bk, L.bv, c.n_embd, c.n_head,
+                                               c.n_kv, c.head_dim, (int)L.wq.col_bytes,
+                                               (int)L.wv.col_bytes, q, kc[li], vc[li], pos,
+                                               pos_dev, c.rope_theta, s),
+                          "fused qkv");
+            }
+            const bool wo_merge = prologue && L.wo.wtype == tf::WType::Q4K && fd.n_split <= 64 &&
+                                  c.n_head <= 32 &&
+                                  c.n_head * (fd.n_split + 1) <= 2048 &&
+                                  c.n_head * c.head_dim <= 4096 &&
+                                  (c.n_head * c.head_dim) % 256 == 0;
+            if (wo_merge) {
+                // split-KV partials, then wo with the merge in its prologue
+                if (pos_dev)
+                    tf::check(tf_flash_decode_partial_d(q, kc[li], vc[li], flash_partial,
+                                                        fd.n_head, fd.n_kv, fd.head_dim, pos_dev,
+                                                        1, fd.n_split, fd.scale, s),
+                              "flash partial");
+                else
+                    tf::check(tf_flash_decode_partial(q, kc[li], vc[li], flash_partial, fd.n_head,
+                                                      fd.n_kv, fd.head_dim, pos, 1, fd.n_split,
+                                                      fd.scale, s),
+                              "flash partial");
+                tf::check(tf_gemv_q4k_flash_out(L.wo.data, flash_partial, fd.n_head, fd.head_dim,
+                                                fd.n_split, x, (int)L.wo.n_cols,
+                                                (int)L.wo.col_bytes, 2, nullptr, nullptr,
+                                                nullptr, s),
+                          "merge+wo");
+            } else {
+                // attention with its merge and the Q8 of the merged output
+                tf::check(tf_flash_decode(q, kc[li], vc[li], flash_partial, d_flash_cnt, xb, q8_x,
+                                          q8_d, fd.n_head, fd.n_kv, fd.head_dim, pos, pos_dev,
+                                          fd.n_split, fd.scale, s),
+                          "flash");
+                gemv_q8_inplace(s, L.wo);
+            }
+            if (prologue) {
+                tf::check(tf_gemv_q4k_ffn_norm(L.gate.data, L.up.data, x, L.ffn_norm, c.rms_eps,
+                                               hb, c.n_embd, c.n_ff, (int)L.gate.col_bytes, s),
+                          "norm+ffn");
+                if (q8_down) {
+                    tf::check(tf_quantize_q8(hb, q8_x, q8_d, c.n_ff, s), "quantize h");
+                    gemv_q8_inplace(s, L.down);
+                } else {
+                    gemv_f32_inplace(s, L.down, hb);
+                }
+            } else {
+                tf::check(tf_norm_quant(x, L.ffn_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                          "norm_quant");
+                tf::check(tf_gemv_q4k_ffn(L.gate.data, L.up.data, q8_x, q8_d, hb, c.n_embd,
+                                          c.n_ff, (int)L.gate.col_bytes, s),
+                          "ffn");
+                tf::check(tf_quantize_q8(hb, q8_x, q8_d, c.n_ff, s), "quantize h");
+                gemv_q8_inplace(s, L.down);
+            }
         }
-        tf::check(tf_norm_quant(x, output_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
-                  "norm_quant");
         const bool keyed = output.wtype == tf::WType::Q6K && output.compact_data;
-        if (keyed) {
+        if (keyed && prologue) {
+            tf::check(tf_gemv_q6k_head_argmax(output.compact_data, x, output_norm, c.rms_eps,
+                                              logits, (int)output.n_rows, (int)output.n_cols,
+                                              (int)output.compact_col_bytes, d_amax_key, s),
+                      "norm+head");
+            if (!device_state)
+                tf::check(tf_argmax_key_finalize(d_amax_key, d_argmax, s), "argmax");
+        } else if (keyed) {
+            tf::check(tf_norm_quant(x, output_norm, c.rms_eps, xb, q8_x, q8_d, c.n_embd, s),
+                      "norm_quant");
             tf::check(tf_gemv_q6k_q8_argmax(output.compact_data, q8_x, q8_d, logits,
                                             (int)output.n_rows, (int)output.n_cols,
                                             (int)output.compact_col_bytes, d_amax_key, s),
@@ -234,6 +285,7 @@ struct tf_model {
             if (!device_state)
                 tf::check(tf_argmax_key_finalize(d_amax_key, d_argmax, s), "argmax");
         } else {
+            tf::check(tf_rms_norm(x, output_norm, xb, c.n_embd, c.rms_eps, s), "norm");
             tf::gemv(s, output, xb, logits, nullptr, GemvResidual::none(), gemv_partial,
                      partial_stride);
             tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
@@ -261,9 +313,23 @@ struct tf_model {
             throw tf::HipError(1, "Q6_K matrix without its compact copy");
     }
 
+    // x += W a for the f32 activation a (quantized in the GEMV's prologue).
+    void gemv_f32_inplace(hipStream_t s, const GpuMat& w, const float* a) {
+        if (w.wtype == tf::WType::Q4K)
+            tf::check(tf_gemv_q4k_f32(w.data, a, x, (int)w.n_rows, (int)w.n_cols,
+                                      (int)w.col_bytes, 0, nullptr, 2, nullptr, s),
+                      "gemv q4k f32");
+        else if (w.compact_data)
+            tf::check(tf_gemv_q6k_compact_f32(w.compact_data, a, x, (int)w.n_rows, (int)w.n_cols,
+                                              (int)w.compact_col_bytes, 2, s),
+                      "gemv q6k f32");
+        else
+            throw tf::HipError(1, "Q6_K matrix without its compact copy");
+    }
+
     void run_step(hipStream_t s, int token, int pos, bool device_state) {
-        if (fused) step_fused(s, token, pos, device_state);
-        else step(s, token, pos, device_state);
+        if (path == 0) step(s, token, pos, device_state);
+        else step_fused(s, token, pos, device_state, path >= 2, path == 3);
     }
 
     void capture() {
@@ -371,6 +437,8 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->d_amax_key = m->alloc<unsigned long long>(TF_ARGMAX_SLOTS);
         tf::check((int)hipMemset(m->d_amax_key, 0, TF_ARGMAX_SLOTS * sizeof(unsigned long long)),
                   "memset");
+        m->d_flash_cnt = m->alloc<unsigned>(c.n_kv);
+        tf::check((int)hipMemset(m->d_flash_cnt, 0, c.n_kv * sizeof(unsigned)), "memset");
         m->d_nforced = m->alloc<int>(1);
         m->d_forced = m->alloc<int>(c.max_seq);
         m->d_log = m->alloc<int>(c.max_seq);
@@ -417,10 +485,10 @@ extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, i
     }
 }
 
-extern "C" int tf_model_set_path(tf_model* m, int fused) {
-    if (!m) return (int)hipErrorInvalidValue;
-    if (m->fused != (fused != 0)) {
-        m->fused = fused != 0;
+extern "C" int tf_model_set_path(tf_model* m, int path) {
+    if (!m || path < 0 || path > 3) return (int)hipErrorInvalidValue;
+    if (m->path != path) {
+        m->path = path;
         if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
         if (m->graph) (void)hipGraphDestroy(m->graph);
         m->graph_exec = nullptr;

@@ -41,6 +41,15 @@ int tf_device_cus() {
     return g_cus[dev];
 }
 
+int tf_block_threads(int max_threads, long long tasks) {
+    const long long cus = tf_device_cus();
+    const long long waves_per_cu = (tasks + cus - 1) / cus;
+    long long threads = ((waves_per_cu + 3) / 4) * 256;
+    if (threads < 256) threads = 256;
+    if (threads > max_threads) threads = max_threads;
+    return (int)threads;
+}
+
 int tf_persistent_blocks(const void* kernel, int threads, int lds_bytes, int tasks) {
     if (tasks <= 0) return 1;
     const int cus = tf_device_cus();
@@ -61,11 +70,12 @@ int tf_persistent_blocks(const void* kernel, int threads, int lds_bytes, int tas
             g_occ[key] = per_cu;
         }
     }
+    // every resident slot, but no workgroup without a task for each wave
+    // (tasks are dealt out block-major, so the blocks share them evenly)
     const int waves_per_block = threads / 64;
-    const long long max_waves = (long long)cus * per_cu * waves_per_block;
-    const long long per_wave = (tasks + max_waves - 1) / max_waves;
-    const long long waves = (tasks + per_wave - 1) / per_wave;
-    return (int)((waves + waves_per_block - 1) / waves_per_block);
+    const long long max_blocks = (long long)cus * per_cu;
+    const long long needed = (tasks + waves_per_block - 1) / waves_per_block;
+    return (int)(needed < max_blocks ? needed : max_blocks);
 }
 
 static const char* const k_symbols[] = {
@@ -95,6 +105,8 @@ static const char* const k_symbols[] = {
     "tf_fused_qkv_rope_kv",
     "tf_norm_quant",
     "tf_flash_decode_reduce_q8",
+    "tf_flash_decode",
+    "tf_gemv_q4k_flash_out",
     "tf_gemv_q6k_q8_argmax",
     "tf_gemv_q4k_ffn_norm",
     "tf_gemv_q6k_compact_f32",

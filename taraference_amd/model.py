@@ -137,9 +137,11 @@ class DecodeModel:
             raise capi.HipError(f"tf_model_forward returned {rc}")
         return nxt.value
 
-    def set_fused(self, fused: bool) -> None:
-        """Fused decode kernels (default) or the reference kernel sequence."""
-        rc = self.lib.tf_model_set_path(self.h, int(fused))
+    def set_path(self, path: int) -> None:
+        """0 = reference kernel sequence, 1 = fused (quantize once),
+        2 = fused with GEMV prologues, 3 = as 2 with a separate h quantize
+        (default)."""
+        rc = self.lib.tf_model_set_path(self.h, int(path))
         if rc != 0:
             raise capi.HipError(f"tf_model_set_path returned {rc}")
 

@@ -63,8 +63,8 @@ def test_invalid_args_rejected(capi):
     assert lib.tf_flash_decode_partial(16, 16, 16, 16, 16, 2, 96, 10, 1, 8, 0.1, None) == INVALID
     assert lib.tf_flash_decode_partial(16, 16, 16, 16, 16, 2, 128, 10, 2, 8, 0.1, None) == INVALID
     assert lib.tf_flash_decode_reduce(16, 16, 16, 128, 0, 1, None) == INVALID
-    assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 48, None) == INVALID   # n % 32
-    assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 16416, None) == INVALID  # n > 16384
+    assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 96, None) == INVALID   # n % 128
+    assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 8320, None) == INVALID  # n > 8192
     assert lib.tf_version() >= 100
 
 

@@ -75,3 +75,36 @@ def test_flash_prefix_of_longer_cache(gpu):
     _, out = run_gpu(q, K, V, n_head, n_kv, hd, 600, 8, 0.088)
     ref = oracle.attn_f64(q, K[:601].copy(), V[:601].copy(), n_head, n_kv, hd, 601, 0.088)
     assert np.abs(out - ref).max() < ATOL
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,L,n_split", [
+    (16, 2, 128, 1, 8), (16, 2, 128, 5, 8), (16, 2, 128, 777, 8), (16, 2, 128, 4096, 32),
+    (16, 2, 128, 5000, 64), (16, 2, 128, 32768, 256),      # 256: merge as a second kernel
+    (28, 4, 128, 3000, 16), (8, 8, 64, 100, 8), (32, 2, 128, 600, 8), (16, 4, 256, 700, 24)])
+def test_flash_decode_fused_merge(gpu, n_head, n_kv, hd, L, n_split):
+    """tf_flash_decode: partials + merge by the last workgroup of each kv head
+    (+ Q8 of the merged output).  Attention within 2e-3 of fp64 softmax
+    attention, the Q8 bit-exact against quantizing the f32 it wrote, and
+    the per-kv-head counters back at zero after each call (two calls in a
+    row give the same result; the second reads the position from device
+    memory)."""
+    q, K, V = case(L, n_head, n_kv, hd, L + n_split)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    part = empty(n_head * n_split * (2 + hd))
+    cnt = torch.zeros(n_kv, dtype=torch.int32, device="cuda")
+    qd, kd, vd = dev(q), dev(K), dev(V)
+    outs = []
+    for call_no in range(2):
+        out, q8, d8 = empty(n_head * hd), empty(n_head * hd, torch.int8), empty(n_head * hd // 32)
+        pd = dev(np.array([L - 1], np.int32)) if call_no else None
+        call("tf_flash_decode", P(qd), P(kd), P(vd), P(part), P(cnt), P(out), P(q8), P(d8),
+             n_head, n_kv, hd, L - 1 if call_no == 0 else 0, P(pd), n_split, scale, S())
+        o = host(out)
+        assert not host(cnt).any()
+        rq, rd = oracle.quantize_q8(o)
+        assert np.array_equal(host(q8), rq)
+        assert np.array_equal(host(d8).view(np.uint32), rd.view(np.uint32))
+        outs.append(o)
+    ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)
+    assert np.abs(outs[0] - ref).max() < ATOL
+    assert np.array_equal(outs[0], outs[1])

@@ -147,7 +147,7 @@ def test_head_argmax(gpu, n_rows, n_cols):
         assert i == int(np.argmax(y64))
 
 
-@pytest.mark.parametrize("n", [256, 896, 2048, 3584, 11008, 16384])
+@pytest.mark.parametrize("n", [256, 896, 2048, 3584, 5120, 8192])
 def test_norm_quant_bit_exact(gpu, n):
     """RMSNorm in the reference's summation order + Q8: f32 output and Q8
     bytes/scales bit-identical to the oracle (ops.cu:4-34, gemv.cu:43-65)."""
@@ -232,3 +232,38 @@ def test_head_argmax_q8_source(gpu):
     y64, absn = oracle.gemv_q6k_q8_f64(comp, 212, q8, d8, n_rows, n_cols, ccb)
     assert_gemv_close(lg, y64, absn, "head q8")
     assert int(host(idx)[0]) == int(np.argmax(lg))
+
+
+@pytest.mark.parametrize("n_head,n_kv,L,n_split", [(16, 2, 700, 8), (28, 4, 300, 8),
+                                                   (2, 1, 50, 8), (16, 2, 5, 1),
+                                                   (16, 2, 4096, 32), (16, 2, 9000, 64)])
+def test_gemv_q4k_flash_out(gpu, n_head, n_kv, L, n_split):
+    """wo with the attention merge in its prologue (flash.cu:222 reduce +
+    quantize_q8 + gemv_q4_k_global, residual in place): merged row within
+    2e-3 of the oracle reduce and of fp64 attention, its Q8 bit-exact against
+    quantizing that row, and the GEMV within the GEMV tolerance of the
+    oracle on that Q8."""
+    hd = 128
+    rng = np.random.default_rng(L + n_head)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    K, V = synth.kv_cache(rng, L, n_kv, hd), synth.kv_cache(rng, L, n_kv, hd)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    part = empty(n_head * n_split * (2 + hd))
+    call("tf_flash_decode_partial", P(dev(q)), P(dev(K)), P(dev(V)), P(part), n_head, n_kv, hd,
+         L - 1, 1, n_split, scale, S())
+    n_rows, n_cols = n_head * hd, 2048
+    w, cb = synth.q4k_matrix(rng, n_rows, n_cols)
+    res = rng.standard_normal(n_cols).astype(np.float32)
+    y = dev(res.copy())
+    ao, aq, ad = empty(n_rows), empty(n_rows, torch.int8), empty(n_rows // 32)
+    call("tf_gemv_q4k_flash_out", P(dev(w)), P(part), n_head, hd, n_split, P(y), n_cols, cb, 2,
+         P(ao), P(aq), P(ad), S())
+    o = host(ao)
+    ref = oracle.flash_reduce(host(part), n_head, hd, n_split)
+    assert np.abs(o - ref).max() < 2e-3
+    assert np.abs(o - oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)).max() < 2e-3
+    rq, rd = oracle.quantize_q8(o)
+    assert np.array_equal(host(aq), rq)
+    assert np.array_equal(host(ad).view(np.uint32), rd.view(np.uint32))
+    y64, absn = oracle.gemv_q4k_q8_f64(w, rq, rd, n_rows, n_cols, cb)
+    assert_gemv_close(host(y) - res, y64, absn, "flash_out wo")

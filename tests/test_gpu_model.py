@@ -26,6 +26,11 @@ TINY = [
          rope_theta=1e6, rms_eps=1e-6),
     dict(n_layer=3, n_embd=512, n_ff=768, n_head=4, n_kv=2, head_dim=128, n_vocab=1000,
          rope_theta=1e4, rms_eps=1e-6),
+    # the real 3B and 7B widths (two layers, small vocabulary)
+    dict(n_layer=2, n_embd=2048, n_ff=11008, n_head=16, n_kv=2, head_dim=128, n_vocab=2000,
+         rope_theta=1e6, rms_eps=1e-6),
+    dict(n_layer=2, n_embd=3584, n_ff=18944, n_head=28, n_kv=4, head_dim=128, n_vocab=2000,
+         rope_theta=1e6, rms_eps=1e-6),
 ]
 
 
@@ -39,12 +44,12 @@ def build(cfg, seed, max_seq):
     return DecodeModel(c, layers, emb), RefModel(cfg, layers, emb, max_seq)
 
 
-@pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("ci", [0, 1])
-def test_decode_steps_match_reference(gpu, ci, fused):
+@pytest.mark.parametrize("path", [0, 1, 2, 3])
+@pytest.mark.parametrize("ci", [0, 1, 2, 3])
+def test_decode_steps_match_reference(gpu, ci, path):
     cfg = TINY[ci]
     gm, rm = build(cfg, 100 + ci, 48)
-    gm.set_fused(fused)
+    gm.set_path(path)
     rng = np.random.default_rng(ci)
     prompt = rng.integers(0, cfg["n_vocab"], 12).tolist()
     tok = prompt[0]
@@ -71,11 +76,11 @@ def test_decode_steps_match_reference(gpu, ci, fused):
     gm.close()
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_graph_replay_equals_eager(gpu, fused):
+@pytest.mark.parametrize("path", [0, 1, 2, 3])
+def test_graph_replay_equals_eager(gpu, path):
     cfg = TINY[1]
     gm, _ = build(cfg, 7, 64)
-    gm.set_fused(fused)
+    gm.set_path(path)
     prompt = list(range(5, 21))
     eager = gm.generate(prompt, 20, use_graph=False)
     graph = gm.generate(prompt, 20, use_graph=True)
