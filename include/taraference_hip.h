@@ -389,8 +389,12 @@ int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
  *   2  fused kernels with the normalization / quantization and
  *      the attention merge in the consuming GEMV's prologue (five launches
  *      per layer);
- *   3  (default) as 2, with h quantized by its own launch before a Q8
- *      ffn_down.
+ *   3  as 2, with h quantized by its own launch before a Q8 ffn_down
+ *      (the default where path 4 does not apply);
+ *   4  the whole step (embedding to argmax) in one persistent launch, one
+ *      workgroup per CU, stages exchanging tagged vectors (no barriers); returns
+ *      hipErrorNotSupported for a model shape or weight mix it has no
+ *      instantiation for (the default where it applies).
  * Changing the path drops the captured graph. */
 int tf_model_set_path(tf_model *m, int path);
 /* Device pointer of the last logits (n_vocab floats) and of the f16 K/V

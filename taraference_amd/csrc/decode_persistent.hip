@@ -1,0 +1,1467 @@
+// Persistent decode step for gfx950: one launch runs a whole batch-1 greedy
+// decode step (embedding, every layer, lm_head and argmax) of a dense
+// Qwen2-style Q4_K_M model.  It performs the same operator sequence as the
+// multi-launch fused path (model.cpp step_fused), which restates
+// cuda/forward.rs:73-264 and cuda/layer.rs:99-709, 1210-1456, 2125-2259:
+//
+//   per layer: [norm + Q8 + QKV + RoPE + K/V append] | [split-KV attention
+//   with its log-sum-exp merge] | [wo, residual] | [norm + Q8 + gate/up +
+//   SiLU] | [Q8 + down, residual];  then [norm + Q8 + lm_head + argmax].
+//
+// Why one launch: at batch 1 every stage streams a few MB of weights, so a
+// launch per stage pays the launch gap plus the ramp of its first HBM
+// requests each time.  Here one workgroup per CU stays resident and the
+// stages are separated by grid barriers.  The weights a wave needs for its
+// first task of the next stage do not depend on the barrier, so each wave
+// issues those loads BEFORE it waits: HBM keeps streaming across every
+// dependency.
+//
+// Cross-XCD coherence.  The eight XCDs have private L2s.  Everything a stage
+// produces for another workgroup (q, K/V rows, attention partials and
+// output, x, h, argmax keys, barrier words) is written with device-scope
+// atomic stores and read with device-scope atomic loads, which bypass the
+// non-coherent L2 state; each thread drains its stores (s_waitcnt) before
+// its workgroup signals a barrier.  No L2 write-back fence is needed, which
+// is what makes a barrier cost about 2 us instead of 7-15 us.  Data written by
+// earlier launches (weights, K/V rows below the current position) is read
+// with ordinary loads.
+//
+// Barrier: flag array.  Workgroup b stores the epoch into its own 128-byte
+// line; workgroup 0 polls all lines (one thread each) and then stores the
+// epoch into the release word that everybody polls.  Epochs grow
+// monotonically across launches (a generation word advances once per
+// launch), compared with wrap-around arithmetic.  Every spin is bounded: on a
+// time-out the workgroup raises the abort word and the error word and
+// returns, and every other wait sees the abort word and returns too, so the
+// grid always drains.
+#include <math.h>
+
+#include <type_traits>
+
+#include "argmax_key.hpp"
+#include "decode_persistent.hpp"
+#include "dequant.hpp"
+#include "q4k.hpp"
+#include "q6k.hpp"
+#include "tf_host.hpp"
+
+// The argument and layer tables are copied into LDS when a launch starts and
+// read from there (address space 3).  A table field read from global memory
+// inside a stage would be a vector load, and vector loads complete in
+// order: it would wait for every weight load the wave had issued before it,
+// i.e. for the whole prefetch of the stage.
+#define TF_LAS __attribute__((address_space(3)))
+typedef const TF_LAS TfPArgs TfPA;
+typedef const TF_LAS TfPLayer TfPL;
+#define TF_P_MAX_LAYERS 64
+static_assert(sizeof(TfPArgs) % 4 == 0 && sizeof(TfPLayer) % 4 == 0, "tables copy as words");
+__shared__ TfPArgs tf_p_args;
+__shared__ TfPLayer tf_p_layers[TF_P_MAX_LAYERS];
+
+// The dynamic LDS of the kernel, named at file scope so that every stage
+// function addresses it as LDS.
+extern __shared__ __align__(16) uint8_t tf_p_lds[];
+__shared__ int tf_p_ok, tf_p_flag;  // tf_p_flag: sticky per-launch abort
+
+#define TF_P_THREADS 512
+#define TF_P_WAVES (TF_P_THREADS / 64)
+#define TF_P_NQ (TF_P_THREADS / 256)  // 256-thread attention quarters
+#define TF_SPIN_LIMIT (1 << 20)
+#define TF_P_TILE 64
+#define TF_P_HD 128
+#define TF_P_NEG_BIG (-1e30f)
+
+// ------------------------------------------------------ coherent access
+
+__device__ __forceinline__ TfPL& tf_p_layer(TfPA& a, int li) {
+    return ((TfPL*)tf_p_layers)[li];
+}
+
+__device__ __forceinline__ unsigned tf_ldu(const unsigned* p) {
+    return __hip_atomic_load((TF_GAS unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tf_stu(unsigned* p, unsigned v) {
+    __hip_atomic_store((TF_GAS unsigned*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float tf_ldc(const float* p) {
+    return __hip_atomic_load((TF_GAS float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tf_stc(float* p, float v) {
+    __hip_atomic_store((TF_GAS float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long tf_ldc64(const void* p) {
+    return __hip_atomic_load((TF_GAS unsigned long long*)p, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tf_stc64(void* p, unsigned long long v) {
+    __hip_atomic_store((TF_GAS unsigned long long*)p, v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 tf_ldc2(const float* p) {
+    const unsigned long long v = tf_ldc64(p);
+    return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
+}
+__device__ __forceinline__ tf_u32x4 tf_ldc16(const void* p) {
+    const unsigned long long a = tf_ldc64(p);
+    const unsigned long long b = tf_ldc64(reinterpret_cast<const uint8_t*>(p) + 8);
+    return tf_u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+__device__ __forceinline__ void tf_stc_h(uint16_t* p, uint16_t v) {
+    __hip_atomic_store((TF_GAS uint16_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------ lane ids
+//
+// threadIdx.x through an empty volatile asm: the compiler cannot hoist what
+// is derived from it out of the layer loop, so each stage's lane geometry
+// is recomputed where it is used instead of staying live (in registers)
+// across the whole loop.
+__device__ __forceinline__ int tf_p_tid() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+__device__ __forceinline__ int tf_p_wid() {
+    return (tf_p_tid() >> 6) * (int)gridDim.x + (int)blockIdx.x;
+}
+
+// ------------------------------------------------ flagged vectors
+//
+// Stage outputs travel as 64-bit words: low half the value bits, high half a
+// tag naming the (launch, layer, vector) that wrote it.  A producer stores
+// each element with one 64-bit device-scope atomic store; a consumer loads
+// the words it needs and retries the ones whose tag is not yet the expected
+// one.  The 64-bit access is single-copy atomic, so a matching tag
+// guarantees the value beside it; no barrier, fence or store drain separates
+// the stages.  Each vector is double-buffered by layer parity, and every
+// workgroup both reads a vector and contributes to the vectors computed from
+// it, so a buffer is not rewritten before every reader is done with it.
+// Tags grow with the launch generation; the runtime zeroes the buffers
+// (tag 0, never expected) whenever it resets the generation.
+
+enum TfPKind { TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5 };
+
+__device__ __forceinline__ unsigned tf_p_tag(unsigned tb, int li, int kind) {
+    return tb + 8u * (unsigned)li + (unsigned)kind + 1u;
+}
+
+__device__ __forceinline__ void tf_p_put(unsigned long long* p, uint32_t bits, unsigned tag) {
+    tf_stc64(p, (unsigned long long)bits | ((unsigned long long)tag << 32));
+}
+__device__ __forceinline__ void tf_p_putf(unsigned long long* p, float v, unsigned tag) {
+    tf_p_put(p, __float_as_uint(v), tag);
+}
+
+__device__ __forceinline__ void tf_p_abort(TfPA& a) {
+    tf_stu(a.bar + TF_BAR_ABORT, 1u);
+    __hip_atomic_fetch_or((TF_GAS int*)a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Stage timeline (diagnostics): stage k of this workgroup started (0), had
+// its activation staged (2) and finished (3).
+__device__ __forceinline__ void tf_p_stamp(TfPA& a, int k, int which) {
+    if (a.trace && tf_p_tid() == 0)
+        a.trace[((size_t)k * gridDim.x + blockIdx.x) * 4 + which] = __builtin_amdgcn_s_memrealtime();
+}
+
+// dst(i, bits) for i < n once word i of src carries `tag`; threads r, r + R,
+// r + 2R, ... of a group of R threads (r = rank), P passes of K words per
+// thread (K R P >= n, checked: a longer vector aborts the launch).  The
+// passes are unrolled and every load is issued unconditionally (past-the-end
+// words reload word 0): a load under a branch, or a loop back edge, makes
+// the compiler drain all loads in flight (the weight prefetch included)
+// before issuing the next one.  Must be called by every thread of the
+// workgroup; returns false (everywhere) if the wait timed out or the launch
+// was aborted.
+template <int K, int P, class Dst>
+__device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src, int n,
+                                          unsigned tag, int rank, int R, TfPA& a) {
+    int bad = n > K * R * P;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const int i0 = rank + p * K * R;
+        unsigned long long v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = i0 + k * R;
+            v[k] = tf_ldc64(src + (i < n ? i : 0));
+        }
+        for (int spins = 0; !bad;) {
+            bool miss = false;
+#pragma unroll
+            for (int k = 0; k < K; k++) miss |= (unsigned)(v[k] >> 32) != tag && i0 + k * R < n;
+            if (!miss) break;
+            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                bad = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const int i = i0 + k * R;
+                v[k] = tf_ldc64(src + (i < n ? i : 0));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = i0 + k * R;
+            if (i < n) dst(i, (uint32_t)v[k]);
+        }
+    }
+    if (bad) {
+        tf_p_abort(a);
+        tf_p_flag = 1;
+    }
+    __syncthreads();
+    const bool ok = tf_p_flag == 0;
+    __syncthreads();
+    return ok;
+}
+
+// ------------------------------------------------- activation staging
+//
+// The LDS image has the layout of tf_act_view (stage.hpp): q8 | d8 | ds |
+// s16 | xf | xs16 for nb super-blocks.  The staging is bit-identical to
+// tf_quantize_q8 / tf_norm_quant / tf_stage_act: the Q8 of a 32-value group
+// depends only on its values (d = amax fl(1/127), q = rint_even(x / d) with
+// an IEEE-exact quotient, kernels/gemv.cu:16-65); integer sums are exact in
+// any order; the f32 16-value sums keep the pairwise tree
+// ((x0+x1)+(x2+x3))+((x4+x5)+(x6+x7)) + ... of the reference staging; and
+// the RMS scale keeps the reference's summation order (below).
+//
+// Lane map: four lanes per 32-value group, lane j of the quad holding values
+// 8j .. 8j+7, so a wave stages 16 groups per step and every group reduction
+// is two quad DPP steps.
+
+// Q8 of eight values held by one lane of a group quad.
+struct TfQ8Oct {
+    int q[8];
+    float d;
+    int s_half, s_other;  // int sums of q over this lane's 16-value half / the other
+    float f_half;         // f32 sum of x over the half (pairwise tree)
+};
+
+template <bool F32>
+__device__ __forceinline__ TfQ8Oct tf_q8_oct(const float (&x)[8]) {
+    TfQ8Oct r;
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
+    uint32_t u = __builtin_bit_cast(uint32_t, am);  // magnitudes order as unsigned ints
+    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)u));
+    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_2301>((int)u));
+    const float amax = __builtin_bit_cast(float, u);
+    r.d = amax * (1.0f / 127.0f);
+    const float rcp = __builtin_amdgcn_rcpf(r.d);
+    // y = x * rcp is within 2^-15 of RN(x / d); far from a .5 tie both round
+    // alike, otherwise (rare) the IEEE quotient decides (as tf_q8_value_r)
+    float y[8];
+    bool rk[8], any = false;
+    const bool tiny = !(r.d >= 1.17549435e-38f);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        y[i] = x[i] * rcp;
+        const float fr = fabsf(y[i] - __builtin_truncf(y[i]));
+        rk[i] = tiny || fabsf(fr - 0.5f) < 6.103515625e-05f;
+        any |= rk[i];
+    }
+    if (any) {
+        const float dd = amax == 0.f ? 1.f : r.d;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (rk[i]) y[i] = x[i] / dd;
+    }
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        r.q[i] = amax == 0.f ? 0 : (int)__builtin_rintf(y[i]);
+        s += r.q[i];
+    }
+    r.s_half = s + tf_dppi<TF_DPP_QUAD_1032>(s);
+    r.s_other = tf_dppi<TF_DPP_QUAD_2301>(r.s_half);
+    r.f_half = 0.f;
+    if (F32) {
+        const float t = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+        r.f_half = t + tf_dpp<TF_DPP_QUAD_1032>(t);
+    }
+    return r;
+}
+
+// Builds the image from the n = 256 nb values src[0 .. n) in LDS.  NORM
+// multiplies each value by `scale` and by its norm weight first (w holds the
+// lane's 8 weights; rows up to 128 groups, one step) and, with F32, keeps
+// the normalized row and its 16-value sums for the Q6_K x f32 path.  Ends
+// with a workgroup barrier.
+template <bool F32, bool NORM>
+__device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* src, float scale,
+                                            const float (&w)[8]) {
+    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
+    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
+    float* dss = d8s + nb * 8;
+    int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
+    float* xf = reinterpret_cast<float*>(s16 + nb * 16);
+    float* xs16 = xf + nb * 256;
+    const int Gq = nb * 8;
+    const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6, j = lane & 3;
+    constexpr int STEP = 16 * TF_P_WAVES;  // groups per step
+    for (int s0 = 0; s0 < Gq; s0 += STEP) {
+        const int g = s0 + wave * 16 + (lane >> 2);
+        const int e = 32 * (g < Gq ? g : Gq - 1) + 8 * j;
+        const float4 a = *reinterpret_cast<const float4*>(src + e);
+        const float4 b = *reinterpret_cast<const float4*>(src + e + 4);
+        float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        if (NORM) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) x[i] = x[i] * scale * w[i];
+        }
+        const TfQ8Oct r = tf_q8_oct<F32>(x);
+        if (g < Gq) {
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
+                hi |= (uint32_t)(r.q[4 + i] & 0xff) << (8 * i);
+            }
+            *reinterpret_cast<uint2*>(q8s + e) = make_uint2(lo, hi);
+            if ((j & 1) == 0) {
+                s16[2 * g + (j >> 1)] = r.s_half;
+                if (F32) xs16[2 * g + (j >> 1)] = r.f_half;
+            }
+            if (j == 0) {
+                d8s[g] = r.d;
+                dss[g] = r.d * (float)(r.s_half + r.s_other);
+            }
+            if (F32 && NORM) {
+                *reinterpret_cast<float4*>(xf + e) = make_float4(x[0], x[1], x[2], x[3]);
+                *reinterpret_cast<float4*>(xf + e + 4) = make_float4(x[4], x[5], x[6], x[7]);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// 1 / sqrt(mean(x^2) + eps) of the n values x[0 .. n) in LDS, computed by
+// each wave on its own in the reference's order (kernels/ops.cu:4-34):
+// partial t (t < 256) = fused square-accumulate of x[t], x[t + 256], ... in
+// turn; then red[t] = p(t) + p(t + 128) (t < 128), v = red[t] + red[t + 64]
+// (t < 64), then the shift-down tree over 32, 16, ..., 1 -- the same
+// additions tf_norm_quant performs through LDS.
+__device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps) {
+    const int lane = tf_p_tid() & 63;
+    float p[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float acc = 0.f;
+        for (int i = lane + 64 * c; i < n; i += 256) acc = fmaf(x[i], x[i], acc);
+        p[c] = acc;
+    }
+    float v = (p[0] + p[2]) + (p[1] + p[3]);
+    v += __shfl_down(v, 32, 64);
+    v += __shfl_down(v, 16, 64);
+    v += __shfl_down(v, 8, 64);
+    v += __shfl_down(v, 4, 64);
+    v += __shfl_down(v, 2, 64);
+    v += __shfl_down(v, 1, 64);
+    v = tf_readlane(v, 0);
+    return 1.0f / sqrtf(v / (float)n + eps);
+}
+
+// The 8 norm weights a lane applies in tf_p_stage8's single step (values
+// 512 wave + 8 lane .. +7), loaded with the stage's weight prefetch.
+__device__ __forceinline__ void tf_p_norm_wload(const float* w, int n, float (&r)[8]) {
+    const int e0 = 8 * tf_p_tid();
+    const int e = e0 < n ? e0 : 0;
+    const tf_u32x4 a = tf_ld16(w + e), b = tf_ld16(w + e + 4);
+    r[0] = __uint_as_float(a.x);
+    r[1] = __uint_as_float(a.y);
+    r[2] = __uint_as_float(a.z);
+    r[3] = __uint_as_float(a.w);
+    r[4] = __uint_as_float(b.x);
+    r[5] = __uint_as_float(b.y);
+    r[6] = __uint_as_float(b.z);
+    r[7] = __uint_as_float(b.w);
+}
+
+// Weights argument of the stages without a norm (unused).
+__device__ constexpr float tf_p_now[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+
+// Raw (unnormalized) row of a norm stage: an LDS area after the image.
+__device__ __forceinline__ float* tf_p_raw(uint8_t* lds, int nbE) {
+    return reinterpret_cast<float*>(lds + tf_act_lds_bytes(nbE, true));
+}
+
+// ------------------------------------------------------------ lane map
+
+struct TfPLane {
+    int lane, t, slot, unit, sir;
+};
+template <int SPR>
+__device__ __forceinline__ TfPLane tf_p_lane() {
+    TfPLane l;
+    l.lane = tf_p_tid() & 63;
+    l.t = l.lane & 3;
+    l.slot = l.lane >> 2;
+    l.unit = l.slot / SPR;
+    l.sir = l.slot % SPR;
+    return l;
+}
+
+// --------------------------------------------- QKV + RoPE + K/V append
+//
+// Task map as tf_fused_qkv_kernel (decode_fused.hip): Q/K rows in RoPE
+// pairs (i, i + hd/2) of one head, then V rows.
+
+// cos/sin of the NeoX rotation angles at this launch's position
+// (kernels/ops.cu:374-398: freq = theta^(-2i/hd), angle = pos * freq),
+// computed once per launch into tf_p_rope_cs[2i] = cos, [2i+1] = sin.
+__shared__ float tf_p_rope_cs[TF_P_HD];
+
+__device__ __forceinline__ void tf_p_rope_table(int hd, int pos, float theta) {
+    const int i = tf_p_tid();
+    if (i < hd / 2) {
+        const float freq = powf(theta, -2.f * (float)i / (float)hd);
+        const float ang = (float)pos * freq;
+        float s, c;
+        sincosf(ang, &s, &c);
+        tf_p_rope_cs[2 * i] = c;
+        tf_p_rope_cs[2 * i + 1] = s;
+    }
+}
+
+__device__ __forceinline__ void tf_p_rope(float x0, float x1, int i, float& y0, float& y1) {
+    const float2 cs = *reinterpret_cast<const float2*>(tf_p_rope_cs + 2 * i);
+    y0 = x0 * cs.x - x1 * cs.y;
+    y1 = x0 * cs.y + x1 * cs.x;
+}
+
+// Flagged new K/V row: per kv head, its K row (head_dim values) then its V row.
+__device__ __forceinline__ int tf_p_kv_k(int idx, int hd) { return (idx / hd) * 2 * hd + idx % hd; }
+
+template <int SPR, int IT>
+struct TfPQkvRegs {
+    TfQ4kRow<IT> a, b;
+    TfQ6kPart v[IT];
+};
+
+struct TfPQkvGeo {
+    int n_q, n_k, n_v, n_pairs, pair_tasks, n_tasks;
+};
+
+template <int SPR>
+__device__ __forceinline__ TfPQkvGeo tf_p_qkv_geo(TfPA& a) {
+    constexpr int UNITS = 16 / SPR, PPT = UNITS >= 2 ? UNITS / 2 : 1;
+    TfPQkvGeo g;
+    g.n_q = a.H * a.HD;
+    g.n_k = a.KV * a.HD;
+    g.n_v = g.n_k;
+    g.n_pairs = (g.n_q + g.n_k) / 2;
+    g.pair_tasks = (g.n_pairs + PPT - 1) / PPT;
+    g.n_tasks = g.pair_tasks + (g.n_v + UNITS - 1) / UNITS;
+    return g;
+}
+
+template <int SPR, int IT>
+__device__ __forceinline__ void tf_p_qkv_load(TfPA& a, TfPL& L, int task,
+                                              TfPQkvRegs<SPR, IT>& r) {
+    constexpr int UNITS = 16 / SPR, PPT = UNITS >= 2 ? UNITS / 2 : 1;
+    const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int nb = a.E / 256, hd = a.HD, half = hd / 2;
+    if (task >= g.n_tasks) return;
+    if (task < g.pair_tasks) {
+        if constexpr (UNITS >= 2) {
+            const int pair = task * PPT + ln.unit / 2, member = ln.unit & 1;
+            const bool valid = pair < g.n_pairs;
+            const int p = valid ? pair : 0;
+            const int row = (p / half) * hd + p % half + member * half;
+            const uint8_t* col = row < g.n_q ? L.wq + (size_t)row * L.cb_qk
+                                             : L.wk + (size_t)(row - g.n_q) * L.cb_qk;
+            tf_q4k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r.a);
+        } else {
+            const int r0 = (task / half) * hd + task % half, r1 = r0 + half;
+            const bool is_q = r0 < g.n_q;
+            const uint8_t* base = is_q ? L.wq : L.wk;
+            const int off = is_q ? 0 : g.n_q;
+            tf_q4k_row_load<SPR, IT>(base + (size_t)(r0 - off) * L.cb_qk, true, 0, nb, ln.sir, ln.t,
+                                     r.a);
+            tf_q4k_row_load<SPR, IT>(base + (size_t)(r1 - off) * L.cb_qk, true, 0, nb, ln.sir, ln.t,
+                                     r.b);
+        }
+    } else {
+        const int j = (task - g.pair_tasks) * UNITS + ln.unit;
+        const bool valid = j < g.n_v;
+        const uint8_t* col = L.wv + (size_t)(valid ? j : 0) * L.cb_v;
+        if (L.v_q6k) {
+#pragma unroll
+            for (int i = 0; i < IT; i++) {
+                const int sb = ln.sir + i * SPR;
+                if (valid && sb < nb) tf_q6k_load_r(col + (size_t)sb * 210, ln.t, r.v[i]);
+            }
+        } else {
+            tf_q4k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r.a);
+        }
+    }
+}
+
+template <int SPR, int IT>
+__device__ __forceinline__ void tf_p_qkv_task(TfPA& a, TfPL& L, int task, int pos,
+                                              const TfAct& x, TfPQkvRegs<SPR, IT>& r,
+                                              unsigned long long* fq, unsigned long long* fkv,
+                                              unsigned tq, unsigned tkv) {
+    constexpr int UNITS = 16 / SPR, PPT = UNITS >= 2 ? UNITS / 2 : 1;
+    const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int nb = a.E / 256, hd = a.HD, half = hd / 2;
+    const int stride = a.KV * hd;
+    const bool lead = (ln.lane & (4 * SPR - 1)) == 0;
+    if (task < g.pair_tasks) {
+        if constexpr (UNITS >= 2) {
+            const int pair = task * PPT + ln.unit / 2, member = ln.unit & 1;
+            const bool valid = pair < g.n_pairs;
+            const int p = valid ? pair : 0;
+            const int i = p % half;
+            const int row = (p / half) * hd + i + member * half;
+            const bool is_q = row < g.n_q;
+            float acc = tf_q4k_row_partial<SPR, IT>(r.a, valid, 0, nb, ln.sir, ln.t, x);
+            acc = tf_group_sum<4 * SPR>(acc);
+            const float* bias = is_q ? L.bq : L.bk;
+            if (valid && bias) acc += tf_gld(bias + (is_q ? row : row - g.n_q));
+            const float other = __shfl(acc, ln.lane ^ (4 * SPR), 64);
+            const float x0 = member == 0 ? acc : other;
+            const float x1 = member == 0 ? other : acc;
+            float y0, y1;
+            tf_p_rope(x0, x1, i, y0, y1);
+            const float y = member == 0 ? y0 : y1;
+            if (valid && lead) {
+                if (is_q) {
+                    tf_p_putf(fq + row, y, tq);
+                } else {
+                    const uint16_t hv = tf_f2h_halfup(y);
+                    *(TF_GAS uint16_t*)(L.k_cache + (size_t)pos * stride + (row - g.n_q)) = hv;
+                    tf_p_put(fkv + tf_p_kv_k(row - g.n_q, hd), hv, tkv);
+                }
+            }
+        } else {
+            const int i = task % half;
+            const int r0 = (task / half) * hd + i, r1 = r0 + half;
+            const bool is_q = r0 < g.n_q;
+            const int off = is_q ? 0 : g.n_q;
+            float x0 = tf_group_sum<64>(tf_q4k_row_partial<SPR, IT>(r.a, true, 0, nb, ln.sir, ln.t, x));
+            float x1 = tf_group_sum<64>(tf_q4k_row_partial<SPR, IT>(r.b, true, 0, nb, ln.sir, ln.t, x));
+            const float* bias = is_q ? L.bq : L.bk;
+            if (bias) {
+                x0 += tf_gld(bias + (r0 - off));
+                x1 += tf_gld(bias + (r1 - off));
+            }
+            float y0, y1;
+            tf_p_rope(x0, x1, i, y0, y1);
+            if (ln.lane == 0) {
+                if (is_q) {
+                    tf_p_putf(fq + r0, y0, tq);
+                    tf_p_putf(fq + r1, y1, tq);
+                } else {
+                    const uint16_t h0 = tf_f2h_halfup(y0), h1 = tf_f2h_halfup(y1);
+                    *(TF_GAS uint16_t*)(L.k_cache + (size_t)pos * stride + (r0 - off)) = h0;
+                    *(TF_GAS uint16_t*)(L.k_cache + (size_t)pos * stride + (r1 - off)) = h1;
+                    tf_p_put(fkv + tf_p_kv_k(r0 - off, hd), h0, tkv);
+                    tf_p_put(fkv + tf_p_kv_k(r1 - off, hd), h1, tkv);
+                }
+            }
+        }
+    } else {
+        const int j = (task - g.pair_tasks) * UNITS + ln.unit;
+        const bool valid = j < g.n_v;
+        float acc = 0.f;
+        if (L.v_q6k) {
+#pragma unroll
+            for (int i = 0; i < IT; i++) {
+                const int sb = ln.sir + i * SPR;
+                if (valid && sb < nb) acc += tf_q6k_f32_part_dot(r.v[i], ln.t, sb, x);
+            }
+            acc = tf_group_sum<4 * SPR>(acc);
+        } else {
+            acc = tf_group_sum<4 * SPR>(tf_q4k_row_partial<SPR, IT>(r.a, valid, 0, nb, ln.sir, ln.t, x));
+        }
+        if (valid && lead) {
+            if (L.bv) acc += tf_gld(L.bv + j);
+            const uint16_t hv = tf_f2h_halfup(acc);
+            *(TF_GAS uint16_t*)(L.v_cache + (size_t)pos * stride + j) = hv;
+            tf_p_put(fkv + tf_p_kv_k(j, hd) + hd, hv, tkv);
+        }
+    }
+}
+
+// ------------------------------------------------------ row GEMV stages
+
+template <int IT, bool Q6>
+using TfPRow = std::conditional_t<Q6, TfQ6kRow<IT>, TfQ4kRow<IT>>;
+
+template <int SPR, int IT, bool Q6>
+__device__ __forceinline__ void tf_p_rows_load(const uint8_t* w, int cb, int nb, int n_rows,
+                                               int task, TfPRow<IT, Q6>& r) {
+    constexpr int UNITS = 16 / SPR;
+    const TfPLane ln = tf_p_lane<SPR>();
+    if (task >= (n_rows + UNITS - 1) / UNITS) return;
+    const int j = task * UNITS + ln.unit;
+    const bool valid = j < n_rows;
+    const uint8_t* col = w + (size_t)(valid ? j : 0) * cb;
+    if constexpr (Q6) tf_q6k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r);
+    else tf_q4k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r);
+}
+
+// Rows of one matrix.  EPI 0: residual stream (see below); EPI 1:
+// out[j] = dot and the argmax key (lm_head).  The wave's tasks run
+// through a ring of D register sets: r[d] holds task wid + (k D + d) nwv,
+// and is refilled with the task D steps ahead as soon as it is consumed, so
+// D tasks' weights are in flight.  tf_p_rows_prefetch fills the ring (before
+// the stage's wait).
+template <int SPR, int IT, bool Q6, int D>
+__device__ __forceinline__ void tf_p_rows_prefetch(const uint8_t* w, int cb, int nb, int n_rows,
+                                                   TfPRow<IT, Q6> (&r)[D]) {
+    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
+#pragma unroll
+    for (int d = 0; d < D; d++) tf_p_rows_load<SPR, IT, Q6>(w, cb, nb, n_rows, wid + d * nwv, r[d]);
+}
+
+// EPI 0 reads the residual from `res` (res(j) -> x_in[j]) and writes
+// out[j] = x_in[j] + dot as a flagged word with tag `tag`.
+template <int SPR, int IT, bool Q6, int D, int EPI, class Res>
+__device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, int n_rows,
+                                              const TfAct& x, TfPRow<IT, Q6> (&r)[D], Res res,
+                                              unsigned long long* fout, unsigned tag,
+                                              float* out, unsigned long long* amax) {
+    constexpr int UNITS = 16 / SPR;
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
+    const int n_tasks = (n_rows + UNITS - 1) / UNITS;
+    const bool lead = (ln.lane & (4 * SPR - 1)) == 0;
+    unsigned long long best = 0;
+    for (int base = wid; base < n_tasks; base += D * nwv) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int task = base + d * nwv;
+            if (task >= n_tasks) break;  // wave-uniform
+            const int j = task * UNITS + ln.unit;
+            const bool valid = j < n_rows;
+            float acc;
+            if constexpr (Q6) acc = tf_q6k_row_partial<SPR, IT>(r[d], valid, 0, nb, ln.sir, ln.t, x);
+            else acc = tf_q4k_row_partial<SPR, IT>(r[d], valid, 0, nb, ln.sir, ln.t, x);
+            tf_p_rows_load<SPR, IT, Q6>(w, cb, nb, n_rows, task + D * nwv, r[d]);
+            acc = tf_group_sum<4 * SPR>(acc);
+            if (valid && lead) {
+                if constexpr (EPI == 0) {
+                    tf_p_putf(fout + j, acc + res(j), tag);
+                } else {
+                    *(TF_GAS float*)(out + j) = acc;
+                    const unsigned long long k = tf_argmax_key(acc, j);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    }
+    if constexpr (EPI == 1) {
+        best = tf_wave_max_u64(best);
+        if (ln.lane == 0 && best)
+            __hip_atomic_fetch_max((TF_GAS unsigned long long*)amax + (wid % TF_ARGMAX_SLOTS), best,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// --------------------------------------------------- gate/up + SiLU
+//
+// Task map as tf_q4k_pair_rows_kernel (gemv_q4k.hip): with SPR <= 8 the even
+// units of a wave take gate rows and the odd units the up rows of the same
+// outputs; with SPR = 16 a lane loads both rows of one output.
+
+template <int IT>
+struct TfPGuRegs {
+    TfQ4kRow<IT> a, b;
+};
+
+template <int SPR, int IT>
+__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int task,
+                                             TfPGuRegs<IT>& r) {
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int nb = a.E / 256, F = a.F;
+    if constexpr (SPR <= 8) {
+        constexpr int JPW = 16 / SPR / 2;
+        if (task >= (F + JPW - 1) / JPW) return;
+        const int j = task * JPW + (ln.unit >> 1);
+        const bool valid = j < F;
+        const uint8_t* w = (ln.unit & 1) ? L.up : L.gate;
+        tf_q4k_row_load<SPR, IT>(w + (size_t)(valid ? j : 0) * L.cb_gu, valid, 0, nb, ln.sir, ln.t,
+                                 r.a);
+    } else {
+        if (task >= F) return;
+        tf_q4k_row_load<SPR, IT>(L.gate + (size_t)task * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
+        tf_q4k_row_load<SPR, IT>(L.up + (size_t)task * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.b);
+    }
+}
+
+template <int SPR, int IT, int D>
+__device__ __forceinline__ void tf_p_gu_prefetch(TfPA& a, TfPL& L, TfPGuRegs<IT> (&r)[D]) {
+    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
+#pragma unroll
+    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, wid + d * nwv, r[d]);
+}
+
+// The wave's gate/up tasks through a ring of D register sets (as
+// tf_p_rows_run).
+template <int SPR, int IT, int D>
+__device__ __forceinline__ void tf_p_gu_run(TfPA& a, TfPL& L, const TfAct& x,
+                                            TfPGuRegs<IT> (&r)[D], unsigned long long* fh,
+                                            unsigned tag) {
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int nb = a.E / 256, F = a.F;
+    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
+    constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;
+    const int n_tasks = (F + JPW - 1) / JPW;
+    for (int base = wid; base < n_tasks; base += D * nwv) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int task = base + d * nwv;
+            if (task >= n_tasks) break;  // wave-uniform
+            if constexpr (SPR <= 8) {
+                const int j = task * JPW + (ln.unit >> 1);
+                const bool valid = j < F;
+                float acc = tf_q4k_row_partial<SPR, IT>(r[d].a, valid, 0, nb, ln.sir, ln.t, x);
+                tf_p_gu_load<SPR, IT>(a, L, task + D * nwv, r[d]);
+                acc = tf_group_sum<4 * SPR>(acc);
+                const float other = __shfl(acc, (ln.lane + 4 * SPR) & 63, 64);
+                if (valid && (ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0)
+                    tf_p_putf(fh + j, (acc / (1.f + __expf(-acc))) * other, tag);
+            } else {
+                float g = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
+                float u = tf_q4k_row_partial<SPR, IT>(r[d].b, true, 0, nb, ln.sir, ln.t, x);
+                tf_p_gu_load<SPR, IT>(a, L, task + D * nwv, r[d]);
+                g = tf_group_sum<64>(g);
+                u = tf_group_sum<64>(u);
+                if (ln.lane == 0) tf_p_putf(fh + task, (g / (1.f + __expf(-g))) * u, tag);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ attention
+//
+// A workgroup serves one (kv head, split) pair; its four 256-thread
+// quarters walk four consecutive runs of 64-token tiles of that split with
+// the tile code of tf_flash_partial_kernel (flash.hip): K/V tiles staged in
+// LDS, next tile in registers, lane = token for the scores, lane = dims for
+// PV, HPW query heads per wave.  The quarters run in lockstep (same tile
+// count) so workgroup barriers stay uniform.  The four quarter results are
+// merged in LDS; with one split per kv head that is the attention output,
+// otherwise it is the workgroup's partial (m, l, O) and the last workgroup of
+// the kv head to finish (arrival ticket) merges all partials with the
+// reference's log-sum-exp formula (attn/flash.cu:222-255).
+
+
+template <int HPW>
+struct TfPAttnLds {
+    static constexpr int GMAX = 4 * HPW;
+    static constexpr int KROW = TF_P_HD + 8;
+    static constexpr int Q_FLOATS = GMAX * TF_P_HD;
+    static constexpr int P_FLOATS = GMAX * TF_P_TILE;
+    static constexpr int BYTES =
+        4 * (Q_FLOATS + P_FLOATS) + 2 * (TF_P_TILE * KROW + TF_P_TILE * TF_P_HD);
+    static constexpr int PER_THREAD = TF_P_TILE * TF_P_HD / 8 / 256;
+};
+
+struct TfPAttnGeo {
+    int n_ws, tpq, kh, ws, t_begin, t_end;
+    bool active;
+};
+
+__device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
+    TfPAttnGeo g;
+    const int seq = pos + 1;
+    const int n_tiles = (seq + TF_P_TILE - 1) / TF_P_TILE;
+    int per_kv = (int)gridDim.x / a.KV;
+    per_kv = per_kv < 1 ? 1 : (per_kv > TF_P_MAX_SPLIT ? TF_P_MAX_SPLIT : per_kv);
+    int n_ws = (n_tiles + TF_P_NQ - 1) / TF_P_NQ;
+    g.n_ws = n_ws < per_kv ? n_ws : per_kv;
+    g.tpq = (n_tiles + TF_P_NQ * g.n_ws - 1) / (TF_P_NQ * g.n_ws);
+    const int b = blockIdx.x;
+    g.active = b < a.KV * g.n_ws;
+    g.kh = g.active ? b / g.n_ws : 0;
+    g.ws = g.active ? b % g.n_ws : 0;
+    const int gq = g.ws * TF_P_NQ + (int)(tf_p_tid() >> 8);
+    const int tile0 = gq * g.tpq;
+    g.t_begin = tile0 * TF_P_TILE;
+    int te = (tile0 + g.tpq) * TF_P_TILE;
+    g.t_end = te < seq ? te : seq;
+    return g;
+}
+
+template <int HPW>
+struct TfPAttnRegs {
+    tf_u32x4 kr[TfPAttnLds<HPW>::PER_THREAD], vr[TfPAttnLds<HPW>::PER_THREAD];
+};
+
+// Tile t0 of this quarter -> registers.  Row `pos` is produced in this
+// launch; it is left out here and taken from the flagged new K/V row when
+// the tile is stored to LDS.
+template <int HPW>
+__device__ __forceinline__ void tf_p_attn_load(TfPL& L, int stride, int kh, int t0,
+                                               int t_end, int pos, TfPAttnRegs<HPW>& r) {
+    const int qt = tf_p_tid() & 255;
+    const uint16_t* kb = L.k_cache + (size_t)kh * TF_P_HD;
+    const uint16_t* vb = L.v_cache + (size_t)kh * TF_P_HD;
+#pragma unroll
+    for (int i = 0; i < TfPAttnLds<HPW>::PER_THREAD; i++) {
+        const int c = qt + 256 * i;
+        const int row = c / (TF_P_HD / 8), col = 8 * (c % (TF_P_HD / 8));
+        const int t = t0 + row;
+        // unconditional loads from a valid row (see tf_p_poll); rows past the
+        // split and the row `pos` are replaced when the tile is stored
+        const size_t off = (size_t)(t < t_end && t != pos ? t : 0) * stride + col;
+        r.kr[i] = tf_ld16(kb + off);
+        r.vr[i] = tf_ld16(vb + off);
+    }
+}
+
+// Static LDS for the new K/V row of this workgroup's kv head (f16 bits).
+__shared__ __align__(16) uint16_t tf_p_knew[TF_P_HD], tf_p_vnew[TF_P_HD];
+__shared__ int tf_p_last;
+
+template <int HPW>
+__device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo& g, int pos,
+                                              TfPAttnRegs<HPW>& r, uint8_t* lds,
+                                              const unsigned long long* fq,
+                                              const unsigned long long* fkv, unsigned tq,
+                                              unsigned tkv, unsigned long long* fo,
+                                              unsigned to, int tk) {
+    using LL = TfPAttnLds<HPW>;
+    constexpr int GMAX = LL::GMAX, HD = TF_P_HD, DPL = HD / 64;
+    const int tid = tf_p_tid(), qd = tid >> 8, qt = tid & 255, lane = tid & 63;
+    const int qw = (tid >> 6) & 3;
+    const int G = a.H / a.KV, stride = a.KV * HD;
+    uint8_t* base = lds + qd * LL::BYTES;
+    float* q_lds = reinterpret_cast<float*>(base);
+    float* p_lds = q_lds + LL::Q_FLOATS;
+    uint16_t* k_lds = reinterpret_cast<uint16_t*>(p_lds + LL::P_FLOATS);
+    uint16_t* v_lds = k_lds + TF_P_TILE * LL::KROW;
+    // q of this kv head's G query heads (each quarter its copy) and the new
+    // K/V row; rows of q past G are zero
+    for (int i = qt; i < GMAX * HD; i += 256)
+        if (i >= G * HD) q_lds[i] = 0.f;
+    if (!tf_p_poll<(8 * TF_P_HD + 255) / 256, 1>(
+            [&](int i, uint32_t b) { q_lds[i] = __uint_as_float(b); },
+            fq + (size_t)g.kh * G * HD, G * HD, tq, qt, 256, a))
+        return false;
+    if (!tf_p_poll<1, 1>(
+            [&](int i, uint32_t b) {
+                if (i < HD) tf_p_knew[i] = (uint16_t)b;
+                else tf_p_vnew[i - HD] = (uint16_t)b;
+            },
+            fkv + (size_t)g.kh * 2 * HD, 2 * HD, tkv, tid, TF_P_THREADS, a))
+        return false;
+    tf_p_stamp(a, tk, 1);
+
+    float m[HPW], l[HPW], o[HPW][DPL];
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+        m[hh] = TF_P_NEG_BIG;
+        l[hh] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; i++) o[hh][i] = 0.f;
+    }
+    const float scale = a.scale;
+    for (int it = 0; it < g.tpq; it++) {
+        const int t0 = g.t_begin + it * TF_P_TILE;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < LL::PER_THREAD; i++) {
+            const int c = qt + 256 * i;
+            const int row = c / (HD / 8), col = 8 * (c % (HD / 8));
+            tf_u32x4 kw = r.kr[i], vw = r.vr[i];
+            if (t0 + row == pos) {  // the row produced in this launch
+                kw = *reinterpret_cast<const tf_u32x4*>(tf_p_knew + col);
+                vw = *reinterpret_cast<const tf_u32x4*>(tf_p_vnew + col);
+            } else if (t0 + row >= g.t_end) {
+                kw = tf_u32x4{0, 0, 0, 0};
+                vw = tf_u32x4{0, 0, 0, 0};
+            }
+            *reinterpret_cast<tf_u32x4*>(k_lds + row * LL::KROW + col) = kw;
+            *reinterpret_cast<tf_u32x4*>(v_lds + row * HD + col) = vw;
+        }
+        if (it + 1 < g.tpq)
+            tf_p_attn_load<HPW>(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
+        __syncthreads();
+        if (t0 >= g.t_end) continue;  // uniform per quarter; barriers stay matched
+        const int t = t0 + lane;
+        const bool tv = t < g.t_end;
+        float sc[HPW];
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) sc[hh] = 0.f;
+        const uint16_t* krow = k_lds + lane * LL::KROW;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 8) {
+            const tf_u32x4 kw = *reinterpret_cast<const tf_u32x4*>(krow + d);
+            float kf[8];
+            kf[0] = tf_h2f(kw.x);
+            kf[1] = tf_h2f(kw.x >> 16);
+            kf[2] = tf_h2f(kw.y);
+            kf[3] = tf_h2f(kw.y >> 16);
+            kf[4] = tf_h2f(kw.z);
+            kf[5] = tf_h2f(kw.z >> 16);
+            kf[6] = tf_h2f(kw.w);
+            kf[7] = tf_h2f(kw.w >> 16);
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++) {
+                const float* qh = q_lds + (qw * HPW + hh) * HD + d;
+                const float4 q0 = *reinterpret_cast<const float4*>(qh);
+                const float4 q1 = *reinterpret_cast<const float4*>(qh + 4);
+                float acc = sc[hh];
+                acc += q0.x * kf[0];
+                acc += q0.y * kf[1];
+                acc += q0.z * kf[2];
+                acc += q0.w * kf[3];
+                acc += q1.x * kf[4];
+                acc += q1.y * kf[5];
+                acc += q1.z * kf[6];
+                acc += q1.w * kf[7];
+                sc[hh] = acc;
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) {
+            const float sv = tv ? sc[hh] * scale : TF_P_NEG_BIG;
+            const float mx = tf_wave_max(sv);
+            const float m_new = fmaxf(m[hh], mx);
+            const float alpha = __expf(m[hh] - m_new);
+            const float e = tv ? __expf(sv - m_new) : 0.f;
+            p_lds[(qw * HPW + hh) * TF_P_TILE + lane] = e;
+            l[hh] = l[hh] * alpha + tf_group_sum<64>(e);
+            m[hh] = m_new;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) o[hh][i] *= alpha;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int tlen = min(TF_P_TILE, g.t_end - t0);
+        const uint16_t* vcol = v_lds + lane * DPL;
+        for (int tt = 0; tt < tlen; tt += 4) {
+            float pw[HPW][4];
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++) {
+                const float4 pv =
+                    *reinterpret_cast<const float4*>(p_lds + (qw * HPW + hh) * TF_P_TILE + tt);
+                pw[hh][0] = pv.x;
+                pw[hh][1] = pv.y;
+                pw[hh][2] = pv.z;
+                pw[hh][3] = pv.w;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t vv = *reinterpret_cast<const uint32_t*>(vcol + (tt + u) * HD);
+                const float v0 = tf_h2f(vv), v1 = tf_h2f(vv >> 16);
+#pragma unroll
+                for (int hh = 0; hh < HPW; hh++) {
+                    o[hh][0] += pw[hh][u] * v0;
+                    o[hh][1] += pw[hh][u] * v1;
+                }
+            }
+        }
+    }
+    tf_p_stamp(a, tk, 2);
+    // ---- merge the quarters in LDS: mq[quarter][GMAX][2 + HD]
+    constexpr int PO = 2 + HD;
+    __syncthreads();
+    float* mq = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+        const int gg = qw * HPW + hh;
+        float* dst = mq + ((size_t)qd * GMAX + gg) * PO;
+        if (lane == 0) {
+            dst[0] = m[hh];
+            dst[1] = l[hh];
+        }
+        dst[2 + lane * DPL] = o[hh][0];
+        dst[2 + lane * DPL + 1] = o[hh][1];
+    }
+    __syncthreads();
+    // (head, dim) outputs idx = tid + THREADS k of this kv head's G * HD
+    constexpr int OPT = 8 * TF_P_HD / TF_P_THREADS;  // outputs per thread (G <= 8)
+    float Mv[OPT], Lv[OPT], Ov[OPT];
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int idx = tid + TF_P_THREADS * k2;
+        const int gh = idx / HD, dd = idx % HD;
+        float M = TF_P_NEG_BIG, Lw = 0.f, O = 0.f;
+        if (gh < G) {
+#pragma unroll
+            for (int k = 0; k < TF_P_NQ; k++) M = fmaxf(M, mq[((size_t)k * GMAX + gh) * PO]);
+#pragma unroll
+            for (int k = 0; k < TF_P_NQ; k++) {
+                const float* src = mq + ((size_t)k * GMAX + gh) * PO;
+                const float w = __expf(src[0] - M);
+                Lw += w * src[1];
+                O += w * src[2 + dd];
+            }
+        }
+        Mv[k2] = M;
+        Lv[k2] = Lw;
+        Ov[k2] = O;
+    }
+    if (g.n_ws == 1) {
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int idx = tid + TF_P_THREADS * k2;
+            if (idx / HD < G)
+                tf_p_putf(fo + (size_t)g.kh * G * HD + idx, Ov[k2] / fmaxf(Lv[k2], 1e-20f), to);
+        }
+        return true;
+    }
+    // ---- split partial, then the last workgroup of the kv head merges
+    const size_t pstride = (size_t)TF_P_MAX_SPLIT * PO;
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int idx = tid + TF_P_THREADS * k2;
+        const int gh = idx / HD, dd = idx % HD;
+        if (gh < G) {
+            float* dst = a.part + (size_t)(g.kh * G + gh) * pstride + (size_t)g.ws * PO;
+            if (dd == 0) {
+                tf_stc(dst, Mv[k2]);
+                tf_stc(dst + 1, Lv[k2]);
+            }
+            tf_stc(dst + 2 + dd, Ov[k2]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.att_cnt + g.kh, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        tf_p_last = prev == (unsigned)(g.n_ws - 1);
+    }
+    __syncthreads();
+    if (!tf_p_last) return true;
+    // re-arm the ticket before the output can release the next layer
+    if (tid == 0) tf_stu(a.att_cnt + g.kh, 0u);
+    __builtin_amdgcn_s_waitcnt(0);
+    float* wts = reinterpret_cast<float*>(lds);  // [GMAX][64]
+    float* Ls = wts + GMAX * 64;
+    {
+        const int gw = tid >> 6;  // one wave per head, lane = split
+        if (gw < G) {
+            const float* src = a.part + (size_t)(g.kh * G + gw) * pstride + (size_t)lane * PO;
+            const bool live = lane < g.n_ws;
+            const float ms = live ? tf_ldc(src) : TF_P_NEG_BIG;
+            const float ls = live ? tf_ldc(src + 1) : 0.f;
+            const float Mx = tf_wave_max(ms);
+            const float w = live ? __expf(ms - Mx) : 0.f;
+            const float Ltot = tf_group_sum<64>(w * ls);
+            wts[gw * 64 + lane] = w;
+            if (lane == 0) Ls[gw] = Ltot;
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += TF_P_THREADS) {
+        const int gh = idx / HD, dd = idx % HD;
+        const float* src = a.part + (size_t)(g.kh * G + gh) * pstride + 2 + dd;
+        float acc = 0.f;
+        for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                v[u] = s0 + u < g.n_ws ? tf_ldc(src + (size_t)(s0 + u) * PO) : 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (s0 + u < g.n_ws) acc += wts[gh * 64 + s0 + u] * v[u];
+        }
+        tf_p_putf(fo + (size_t)g.kh * G * HD + idx, acc / fmaxf(Ls[gh], 1e-20f), to);
+    }
+    return true;
+}
+
+// ------------------------------------------------------------ stages
+//
+// Each stage runs as its own (non-inlined) function: its prefetch, its
+// activation poll, its staging and its GEMV then share one register
+// allocation that nothing else in the kernel adds to.  Every stage first
+// issues the loads of its first weight tasks (they do not depend on the
+// previous stage), then waits at a workgroup barrier (waves that finished
+// the previous stage early must not overwrite the LDS image the others are
+// still reading; the barrier waits for LDS traffic only, not for the weight
+// loads in flight), then polls its input vector.  A false return means the
+// launch was aborted.
+
+__device__ __forceinline__ unsigned long long* tf_p_vec(TfPA& a, int kind, int li) {
+    const int par = li & 1;
+    switch (kind) {
+    case TF_PK_XA: return a.fx + (size_t)par * a.E;
+    case TF_PK_XB: return a.fx + (size_t)(2 + par) * a.E;
+    case TF_PK_Q: return a.fq + (size_t)par * a.H * a.HD;
+    case TF_PK_KV: return a.fkv + (size_t)par * 2 * a.KV * a.HD;
+    case TF_PK_O: return a.fo + (size_t)par * a.H * a.HD;
+    default: return a.fh + (size_t)par * a.F;
+    }
+}
+
+// Polls a flagged vector into the f32 slot of the LDS activation image.
+template <int K, int P = 1>
+__device__ __forceinline__ bool tf_p_poll_xf(TfPA& a, float* xf, const unsigned long long* src,
+                                             int n, unsigned tag) {
+    return tf_p_poll<K, P>([&](int i, uint32_t b) { xf[i] = __uint_as_float(b); }, src, n, tag,
+                        tf_p_tid(), TF_P_THREADS, a);
+}
+
+// Layer li's norm + QKV + RoPE + K/V append.
+template <int SPR, int IT>
+__device__ __noinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int pos, int token) {
+    uint8_t* lds = tf_p_lds;
+    TfPA& a = *pa;
+    TfPL& L = tf_p_layer(a, li);
+    const int nbE = a.E / 256, wid = tf_p_wid(), tid = tf_p_tid();
+    const TfAct xE = tf_act_view(lds, nbE);
+    float* xf = const_cast<float*>(xE.xf);
+    TfPQkvRegs<SPR, IT> rq;
+    tf_p_qkv_load<SPR, IT>(a, L, wid, rq);
+    float nw[8];
+    tf_p_norm_wload(L.attn_norm, a.E, nw);
+    float* raw = tf_p_raw(lds, nbE);
+    tf_p_stamp(a, 5 * li, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    if (li == 0) {
+        tf_p_rope_table(a.HD, pos, a.theta);
+        const int bb = a.embd_q6k ? 210 : 144;
+        const uint8_t* col = a.embd + (size_t)token * a.embd_cb;
+        for (int i = tid; i < a.E; i += TF_P_THREADS) {
+            const uint8_t* blk = col + (size_t)(i >> 8) * bb;
+            raw[i] = a.embd_q6k ? tf_q6k_value(blk, i & 255) : tf_q4k_value(blk, i & 255);
+        }
+        __syncthreads();
+    } else if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
+                   a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E, tf_p_tag(tb, li - 1, TF_PK_XB))) {
+        return false;
+    }
+    tf_p_stamp(a, 5 * li, 1);
+    tf_p_stage8<true, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+    tf_p_stamp(a, 5 * li, 2);
+    const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
+    const int nwv = gridDim.x * TF_P_WAVES;
+    unsigned long long* fq = tf_p_vec(a, TF_PK_Q, li);
+    unsigned long long* fkv = tf_p_vec(a, TF_PK_KV, li);
+    const unsigned tq = tf_p_tag(tb, li, TF_PK_Q), tkv = tf_p_tag(tb, li, TF_PK_KV);
+    for (int task = wid; task < g.n_tasks; task += nwv) {
+        if (task != wid) tf_p_qkv_load<SPR, IT>(a, L, task, rq);
+        tf_p_qkv_task<SPR, IT>(a, L, task, pos, xE, rq, fq, fkv, tq, tkv);
+    }
+    tf_p_stamp(a, 5 * li, 3);
+    return true;
+}
+
+template <int HPW>
+__device__ __noinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
+    uint8_t* lds = tf_p_lds;
+    TfPA& a = *pa;
+    TfPL& L = tf_p_layer(a, li);
+    const TfPAttnGeo g = tf_p_attn_geo(a, pos);
+    if (!g.active) return true;
+    TfPAttnRegs<HPW> ra;
+    tf_p_attn_load<HPW>(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
+    tf_p_stamp(a, 5 * li + 1, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    const bool ok = tf_p_attn_run<HPW>(
+        a, L, g, pos, ra, lds, tf_p_vec(a, TF_PK_Q, li), tf_p_vec(a, TF_PK_KV, li),
+        tf_p_tag(tb, li, TF_PK_Q), tf_p_tag(tb, li, TF_PK_KV), tf_p_vec(a, TF_PK_O, li),
+        tf_p_tag(tb, li, TF_PK_O), 5 * li + 1);
+    tf_p_stamp(a, 5 * li + 1, 3);
+    return ok;
+}
+
+// x_in[j] of layer li's residual.
+__device__ __forceinline__ float tf_p_res_in(TfPA& a, int li, unsigned tb, int token, int j) {
+    if (li == 0) {
+        const uint8_t* blk = a.embd + (size_t)token * a.embd_cb +
+                             (size_t)(j >> 8) * (a.embd_q6k ? 210 : 144);
+        return a.embd_q6k ? tf_q6k_value(blk, j & 255) : tf_q4k_value(blk, j & 255);
+    }
+    const unsigned long long v = tf_ldc64(tf_p_vec(a, TF_PK_XB, li - 1) + j);
+    if ((unsigned)(v >> 32) != tf_p_tag(tb, li - 1, TF_PK_XB)) tf_p_abort(a);  // cannot happen
+    return __uint_as_float((unsigned)v);
+}
+
+template <int SPR, int IT>
+__device__ __noinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int token) {
+    uint8_t* lds = tf_p_lds;
+    TfPA& a = *pa;
+    TfPL& L = tf_p_layer(a, li);
+    const int nbE = a.E / 256;
+    const TfAct xE = tf_act_view(lds, nbE);
+    float* xf = const_cast<float*>(xE.xf);
+    TfPRow<IT, false> ro[1];
+    tf_p_rows_prefetch<SPR, IT, false, 1>(L.wo, L.cb_o, nbE, a.E, ro);
+    tf_p_stamp(a, 5 * li + 2, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
+            a, xf, tf_p_vec(a, TF_PK_O, li), a.E, tf_p_tag(tb, li, TF_PK_O)))
+        return false;
+    tf_p_stamp(a, 5 * li + 2, 1);
+    tf_p_stage8<false, false>(lds, nbE, xf, 1.f, tf_p_now);
+    tf_p_stamp(a, 5 * li + 2, 2);
+    tf_p_rows_run<SPR, IT, false, 1, 0>(
+        L.wo, L.cb_o, nbE, a.E, xE, ro, [&](int j) { return tf_p_res_in(a, li, tb, token, j); },
+        tf_p_vec(a, TF_PK_XA, li), tf_p_tag(tb, li, TF_PK_XA), nullptr, nullptr);
+    tf_p_stamp(a, 5 * li + 2, 3);
+    return true;
+}
+
+template <int SPR, int IT>
+__device__ __noinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
+    uint8_t* lds = tf_p_lds;
+    TfPA& a = *pa;
+    TfPL& L = tf_p_layer(a, li);
+    const int nbE = a.E / 256;
+    const TfAct xE = tf_act_view(lds, nbE);
+    constexpr int D = SPR <= 8 ? 4 : 2;
+    TfPGuRegs<IT> rg[D];
+    tf_p_gu_prefetch<SPR, IT, D>(a, L, rg);
+    float nw[8];
+    tf_p_norm_wload(L.ffn_norm, a.E, nw);
+    float* raw = tf_p_raw(lds, nbE);
+    tf_p_stamp(a, 5 * li + 3, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
+            a, raw, tf_p_vec(a, TF_PK_XA, li), a.E, tf_p_tag(tb, li, TF_PK_XA)))
+        return false;
+    tf_p_stamp(a, 5 * li + 3, 1);
+    tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+    tf_p_stamp(a, 5 * li + 3, 2);
+    tf_p_gu_run<SPR, IT, D>(a, L, xE, rg, tf_p_vec(a, TF_PK_H, li), tf_p_tag(tb, li, TF_PK_H));
+    tf_p_stamp(a, 5 * li + 3, 3);
+    return true;
+}
+
+// Down projection: x_out = x_mid + W_down q8(h).
+template <int SPR, int IT, bool Q6>
+__device__ __forceinline__ bool tf_p_down_body(TfPA& a, TfPL& L, int li, unsigned tb) {
+    uint8_t* lds = tf_p_lds;
+    const int nbF = a.F / 256;
+    const TfAct xF = tf_act_view(lds, nbF);
+    float* hf = const_cast<float*>(xF.xf);
+    TfPRow<IT, Q6> rd[1];
+    tf_p_rows_prefetch<SPR, IT, Q6, 1>(L.down, L.cb_down, nbF, a.E, rd);
+    tf_p_stamp(a, 5 * li + 4, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    // h in one pass up to 11264 values (44 registers), else in two
+    constexpr int HK = IT <= 3 ? 22 : 19, HP = IT <= 3 ? 1 : 2;
+    if (!tf_p_poll_xf<HK, HP>(a, hf, tf_p_vec(a, TF_PK_H, li), a.F, tf_p_tag(tb, li, TF_PK_H)))
+        return false;
+    tf_p_stamp(a, 5 * li + 4, 1);
+    tf_p_stage8<false, false>(lds, nbF, hf, 1.f, tf_p_now);
+    tf_p_stamp(a, 5 * li + 4, 2);
+    const unsigned long long* xm = tf_p_vec(a, TF_PK_XA, li);
+    tf_p_rows_run<SPR, IT, Q6, 1, 0>(
+        L.down, L.cb_down, nbF, a.E, xF, rd,
+        [&](int j) { return __uint_as_float((unsigned)tf_ldc64(xm + j)); },
+        tf_p_vec(a, TF_PK_XB, li), tf_p_tag(tb, li, TF_PK_XB), nullptr, nullptr);
+    tf_p_stamp(a, 5 * li + 4, 3);
+    return true;
+}
+
+template <int SPR, int IT>
+__device__ __noinline__ bool tf_p_stage_down(TfPA* pa, int li, unsigned tb) {
+    TfPA& a = *pa;
+    TfPL& L = tf_p_layer(a, li);
+    if (L.down_q6k) return tf_p_down_body<SPR, IT, true>(a, L, li, tb);
+    return tf_p_down_body<SPR, IT, false>(a, L, li, tb);
+}
+
+// Final norm + lm_head + argmax keys; the last workgroup to finish takes the
+// argmax and advances the decode state.
+__shared__ unsigned long long tf_p_key[TF_P_WAVES];
+
+template <int SPR, int IT>
+__device__ __noinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_mode, int pos,
+                                             unsigned gen) {
+    uint8_t* lds = tf_p_lds;
+    TfPA& a = *pa;
+    const int nbE = a.E / 256, tid = tf_p_tid(), L = a.n_layer;
+    const TfAct xE = tf_act_view(lds, nbE);
+    constexpr int D = 4;
+    TfPRow<IT, true> rh[D];
+    tf_p_rows_prefetch<SPR, IT, true, D>(a.head, a.head_cb, nbE, a.n_vocab, rh);
+    float nw[8];
+    tf_p_norm_wload(a.out_norm, a.E, nw);
+    float* raw = tf_p_raw(lds, nbE);
+    tf_p_stamp(a, 5 * L, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
+    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
+            a, raw, tf_p_vec(a, TF_PK_XB, L - 1), a.E, tf_p_tag(tb, L - 1, TF_PK_XB)))
+        return false;
+    tf_p_stamp(a, 5 * L, 1);
+    tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+    tf_p_stamp(a, 5 * L, 2);
+    tf_p_rows_run<SPR, IT, true, D, 1>(a.head, a.head_cb, nbE, a.n_vocab, xE, rh,
+                                       [](int) { return 0.f; }, nullptr, 0u, a.logits, a.amax);
+    tf_p_stamp(a, 5 * L, 3);
+    // ticket: the keys of this workgroup are in before its ticket
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.bar + TF_BAR_DONE, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        tf_p_last = prev == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!tf_p_last) return true;
+    unsigned long long k = 0;
+    for (int i = tid; i < TF_ARGMAX_SLOTS; i += TF_P_THREADS) {
+        const unsigned long long v = tf_ldc64(a.amax + i);
+        k = v > k ? v : k;
+        tf_stc64(a.amax + i, 0ull);
+    }
+    k = tf_wave_max_u64(k);
+    if ((tid & 63) == 0) tf_p_key[tid >> 6] = k;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 0; w < TF_P_WAVES; w++) k = tf_p_key[w] > k ? tf_p_key[w] : k;
+        const int next = tf_argmax_key_index(k);
+        if (host_mode) {
+            tf_stu(reinterpret_cast<unsigned*>(a.argmax), (unsigned)next);
+        } else {
+            const int st = (int)tf_ldu(reinterpret_cast<unsigned*>(a.step));
+            tf_stu(reinterpret_cast<unsigned*>(a.log + st), (unsigned)next);
+            const int nf = tf_gld(a.nforced);
+            tf_stu(reinterpret_cast<unsigned*>(a.token),
+                   (unsigned)(st + 1 < nf ? tf_gld(a.forced + st + 1) : next));
+            tf_stu(reinterpret_cast<unsigned*>(a.pos), (unsigned)(pos + 1));
+            tf_stu(reinterpret_cast<unsigned*>(a.step), (unsigned)(st + 1));
+        }
+        tf_stu(a.bar + TF_BAR_DONE, 0u);
+        tf_stu(a.bar + TF_BAR_GEN, gen + 1u);
+    }
+    return true;
+}
+
+// ------------------------------------------------------------ the kernel
+
+template <int SPR_E, int IT_E, int SPR_F, int IT_F, int HPW>
+__global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
+    const TfPArgs* args, int host_mode, int token_host, int pos_host) {
+    {
+        const int tid = tf_p_tid();
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(args);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(&tf_p_args);
+        for (int i = tid; i < (int)(sizeof(TfPArgs) / 4); i += TF_P_THREADS) dst[i] = tf_gld(src + i);
+        const int nl = tf_gld(&args->n_layer);
+        const uint32_t* lsrc = reinterpret_cast<const uint32_t*>(tf_gld(&args->layers));
+        uint32_t* ldst = reinterpret_cast<uint32_t*>(tf_p_layers);
+        for (int i = tid; i < nl * (int)(sizeof(TfPLayer) / 4); i += TF_P_THREADS)
+            ldst[i] = tf_gld(lsrc + i);
+        if (tid == 0) tf_p_flag = 0;
+        __syncthreads();
+    }
+    TfPA& a = *(TfPA*)&tf_p_args;
+    const int pos = host_mode ? pos_host : (int)tf_ldu(reinterpret_cast<unsigned*>(a.pos));
+    const int token = host_mode ? token_host : (int)tf_ldu(reinterpret_cast<unsigned*>(a.token));
+    const unsigned gen = tf_ldu(a.bar + TF_BAR_GEN);
+    const unsigned tb = gen * (unsigned)(8 * a.n_layer + 8);
+    __syncthreads();
+    for (int li = 0; li < a.n_layer; li++) {
+        if (!tf_p_stage_qkv<SPR_E, IT_E>(&a, li, tb, pos, token)) return;
+        if (!tf_p_stage_attn<HPW>(&a, li, tb, pos)) return;
+        if (!tf_p_stage_wo<SPR_E, IT_E>(&a, li, tb, token)) return;
+        if (!tf_p_stage_gu<SPR_E, IT_E>(&a, li, tb)) return;
+        if (!tf_p_stage_down<SPR_F, IT_F>(&a, li, tb)) return;
+    }
+    tf_p_stage_head<SPR_E, IT_E>(&a, tb, host_mode, pos, gen);
+}
+
+// ------------------------------------------------------------ host side
+
+namespace {
+
+template <int HPW>
+int tf_p_lds(const TfPArgs& a) {
+    const int nbE = a.E / 256, nbF = a.F / 256;
+    int b = tf_act_lds_bytes(nbE, true) + 4 * a.E;
+    const int f = tf_act_lds_bytes(nbF, true);
+    if (f > b) b = f;
+    const int at = TF_P_NQ * TfPAttnLds<HPW>::BYTES;
+    return at > b ? at : b;
+}
+
+struct TfPLaunch {
+    const TfPArgs* dev;
+    int host_mode, token, pos;
+};
+
+template <int SE, int IE, int SF, int IF, int HPW>
+int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid_out,
+                  int* lds_out) {
+    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, HPW>;
+    const int lds = tf_p_lds<HPW>(a);
+    static int attr_done[64];
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !attr_done[dev]) {
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds) != hipSuccess)
+            return (int)hipErrorInvalidValue;
+        attr_done[dev] = 1;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, TF_P_THREADS,
+                                                     lds) != hipSuccess ||
+        per_cu < 1)
+        return (int)hipErrorInvalidConfiguration;
+    int grid = tf_device_cus();
+    if (grid > TF_P_MAX_WG) grid = TF_P_MAX_WG;
+    if (grid_out) *grid_out = grid;
+    if (lds_out) *lds_out = lds;
+    if (!l) return 0;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(TF_P_THREADS), lds, s, l->dev, l->host_mode,
+                       l->token, l->pos);
+    return (int)hipGetLastError();
+}
+
+// Instantiations: (SPR, ITERS) of the model width and of the FFN width, and
+// query heads per wave (G = n_head / n_kv <= 4 HPW).
+template <class F>
+int tf_p_dispatch(int E, int F_, int H, int KV, int HD, F&& f) {
+    if (HD != TF_P_HD || KV <= 0 || H % KV) return -1;
+    const int nbE = E / 256, nbF = F_ / 256, G = H / KV;
+    if (nbE <= 4 && nbF <= 4 && G <= 4) return f(std::integral_constant<int, 0>{});
+    if (nbE > 4 && nbE <= 8 && nbF > 32 && nbF <= 48 && G <= 8)
+        return f(std::integral_constant<int, 1>{});
+    if (nbE > 8 && nbE <= 16 && nbF > 64 && nbF <= 80 && G <= 8)
+        return f(std::integral_constant<int, 2>{});
+    return -1;
+}
+
+template <int V>
+int tf_p_call(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid, int* lds) {
+    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1, 1>(a, l, s, grid, lds);
+    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3, 2>(a, l, s, grid, lds);
+    else return tf_p_launch_t<16, 1, 16, 5, 2>(a, l, s, grid, lds);
+}
+
+}  // namespace
+
+bool tf_decode_persistent_supported(int n_layer, int E, int F, int H, int KV, int HD) {
+    if (n_layer < 1 || n_layer > TF_P_MAX_LAYERS || E % 256 || F % 256 || H * HD != E)
+        return false;
+    return tf_p_dispatch(E, F, H, KV, HD, [](auto) { return 0; }) == 0;
+}
+
+int tf_decode_persistent_grid(const TfPArgs& a, int* lds_bytes) {
+    int grid = 0;
+    const int rc = tf_p_dispatch(a.E, a.F, a.H, a.KV, a.HD, [&](auto v) {
+        return tf_p_call<decltype(v)::value>(a, nullptr, nullptr, &grid, lds_bytes);
+    });
+    return rc == 0 ? grid : 0;
+}
+
+int tf_decode_persistent_launch(const TfPArgs& a, const TfPArgs* dev, int host_mode, int token,
+                                int pos, hipStream_t stream) {
+    if (!dev) return (int)hipErrorInvalidValue;
+    const TfPLaunch l{dev, host_mode, token, pos};
+    const int rc = tf_p_dispatch(a.E, a.F, a.H, a.KV, a.HD, [&](auto v) {
+        return tf_p_call<decltype(v)::value>(a, &l, stream, nullptr, nullptr);
+    });
+    return rc < 0 ? (int)hipErrorInvalidValue : rc;
+}

@@ -22,11 +22,13 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <memory>
 #include <new>
 #include <vector>
 
 #include "argmax_key.hpp"
+#include "decode_persistent.hpp"
 #include "op_api.hpp"
 #include "taraference_hip.h"
 
@@ -101,8 +103,24 @@ struct tf_model {
     // 0: the reference operator sequence (step); 1: fused, each activation
     // normalized and quantized once by its own kernel; 2: fused, the
     // normalization / quantization / attention merge runs in the consuming
-    // GEMV's prologue; 3: as 2 but h is quantized by its own kernel.
+    // GEMV's prologue; 3: as 2 but h is quantized by its own kernel;
+    // 4: the whole step in one persistent launch (decode_persistent.hip).
+    // Default: 4 when persistent_ok(), else 3 (set in tf_model_create).
     int path = 3;
+    // persistent-step state (allocated on first use of path 4)
+    TfPLayer* d_players = nullptr;
+    unsigned* d_bar = nullptr;
+    unsigned* d_att_cnt = nullptr;
+    int* d_perr = nullptr;
+    float* p_part = nullptr;
+    unsigned long long* p_flags = nullptr;  // the flagged stage vectors
+    size_t p_flag_words = 0;
+    // diagnostic stage timeline of the persistent step: when the environment
+    // names a file in TF_P_TRACE, the last step of each run() is written there
+    unsigned long long* d_trace = nullptr;
+    size_t trace_words = 0;
+    TfPArgs pargs{};
+    TfPArgs* d_pargs = nullptr;
     unsigned* d_flash_cnt = nullptr;  // per-kv-head tickets of tf_flash_decode
     int *d_forced = nullptr, *d_nforced = nullptr, *d_log = nullptr;
     std::vector<void*> allocs;
@@ -327,8 +345,154 @@ struct tf_model {
             throw tf::HipError(1, "Q6_K matrix without its compact copy");
     }
 
+    // Whether path 4 can serve this model: Q4_K q/k/wo/gate/up, Q6_K or
+    // Q4_K v and down (Q6_K down and the lm_head with their compact copy), and
+    // a shape the persistent kernel is instantiated for.
+    bool persistent_ok() const {
+        const tf_model_config& c = cfg;
+        if (!tf_decode_persistent_supported(c.n_layer, c.n_embd, c.n_ff, c.n_head, c.n_kv,
+                                            c.head_dim))
+            return false;
+        if (output.wtype != tf::WType::Q6K || !output.compact_data) return false;
+        for (const Layer& L : layers) {
+            if (L.wq.wtype != tf::WType::Q4K || L.wk.wtype != tf::WType::Q4K ||
+                L.wo.wtype != tf::WType::Q4K || L.gate.wtype != tf::WType::Q4K ||
+                L.up.wtype != tf::WType::Q4K || L.wq.col_bytes != L.wk.col_bytes ||
+                L.gate.col_bytes != L.up.col_bytes)
+                return false;
+            if (L.down.wtype == tf::WType::Q6K && !L.down.compact_data) return false;
+        }
+        return true;
+    }
+
+    void ensure_persistent() {
+        if (d_players) return;
+        const tf_model_config& c = cfg;
+        std::vector<TfPLayer> h(layers.size());
+        for (size_t i = 0; i < layers.size(); i++) {
+            const Layer& L = layers[i];
+            TfPLayer& p = h[i];
+            p.attn_norm = L.attn_norm;
+            p.ffn_norm = L.ffn_norm;
+            p.wq = L.wq.data;
+            p.wk = L.wk.data;
+            p.wv = L.wv.data;
+            p.wo = L.wo.data;
+            p.gate = L.gate.data;
+            p.up = L.up.data;
+            p.v_q6k = L.wv.wtype == tf::WType::Q6K;
+            p.down_q6k = L.down.wtype == tf::WType::Q6K;
+            p.down = p.down_q6k ? L.down.compact_data : L.down.data;
+            p.bq = L.bq;
+            p.bk = L.bk;
+            p.bv = L.bv;
+            p.k_cache = kc[i];
+            p.v_cache = vc[i];
+            p.cb_qk = (int)L.wq.col_bytes;
+            p.cb_v = (int)L.wv.col_bytes;
+            p.cb_o = (int)L.wo.col_bytes;
+            p.cb_gu = (int)L.gate.col_bytes;
+            p.cb_down = (int)(p.down_q6k ? L.down.compact_col_bytes : L.down.col_bytes);
+        }
+        d_players = alloc<TfPLayer>(h.size());
+        tf::check((int)hipMemcpy(d_players, h.data(), h.size() * sizeof(TfPLayer),
+                                 hipMemcpyHostToDevice), "copy layer table");
+        d_bar = alloc<unsigned>(TF_BAR_WORDS);
+        d_att_cnt = alloc<unsigned>(c.n_kv);
+        d_perr = alloc<int>(1);
+        p_flag_words = (size_t)4 * c.n_embd + 2 * (size_t)c.n_head * c.head_dim +
+                       4 * (size_t)c.n_kv * c.head_dim + 2 * (size_t)c.n_head * c.head_dim +
+                       2 * (size_t)c.n_ff;
+        p_flags = alloc<unsigned long long>(p_flag_words);
+        p_part = alloc<float>((size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim));
+        if (std::getenv("TF_P_TRACE")) {
+            trace_words = (size_t)(5 * c.n_layer + 2) * TF_P_MAX_WG * 4;
+            d_trace = alloc<unsigned long long>(trace_words);
+        }
+        fill_pargs();
+        d_pargs = alloc<TfPArgs>(1);
+        tf::check((int)hipMemcpy(d_pargs, &pargs, sizeof(TfPArgs), hipMemcpyHostToDevice),
+                  "copy args");
+        reset_persistent(nullptr);
+    }
+
+    // Zero the barrier words, merge tickets and error flag (a fresh
+    // generation; also clears what an aborted launch left behind).
+    void reset_persistent(hipStream_t s) {
+        tf::check((int)hipMemsetAsync(d_bar, 0, TF_BAR_WORDS * sizeof(unsigned), s), "memset");
+        tf::check((int)hipMemsetAsync(d_att_cnt, 0, cfg.n_kv * sizeof(unsigned), s), "memset");
+        tf::check((int)hipMemsetAsync(d_perr, 0, sizeof(int), s), "memset");
+        tf::check((int)hipMemsetAsync(p_flags, 0, p_flag_words * sizeof(unsigned long long), s),
+                  "memset");
+        if (!s) tf::check((int)hipDeviceSynchronize(), "sync");
+    }
+
+    // After a synchronization: a barrier time-out inside the persistent
+    // kernel is reported as hipErrorLaunchTimeOut (and the state is reset).
+    void check_persistent(hipStream_t s) {
+        if (path != 4 || !d_perr) return;
+        int e = 0;
+        tf::check((int)hipMemcpy(&e, d_perr, sizeof(int), hipMemcpyDeviceToHost), "copy");
+        if (e) {
+            reset_persistent(s);
+            tf::check((int)hipStreamSynchronize(s), "sync");
+            throw tf::HipError((int)hipErrorLaunchTimeOut, "persistent step barrier time-out");
+        }
+    }
+
+    // The persistent kernel's argument table (host copy in pargs, device
+    // copy in d_pargs).
+    void fill_pargs() {
+        const tf_model_config& c = cfg;
+        TfPArgs& a = pargs;
+        a = TfPArgs{};
+        a.layers = d_players;
+        a.n_layer = c.n_layer;
+        a.E = c.n_embd;
+        a.F = c.n_ff;
+        a.H = c.n_head;
+        a.KV = c.n_kv;
+        a.HD = c.head_dim;
+        a.theta = c.rope_theta;
+        a.eps = c.rms_eps;
+        a.scale = fd.scale;
+        a.embd = token_embd.data;
+        a.embd_cb = (int)token_embd.col_bytes;
+        a.embd_q6k = embd_block_bytes == 210;
+        a.head = output.compact_data;
+        a.head_cb = (int)output.compact_col_bytes;
+        a.n_vocab = (int)output.n_cols;
+        a.out_norm = output_norm;
+        a.fx = p_flags;
+        a.fq = a.fx + 4 * (size_t)c.n_embd;
+        a.fkv = a.fq + 2 * (size_t)c.n_head * c.head_dim;
+        a.fo = a.fkv + 4 * (size_t)c.n_kv * c.head_dim;
+        a.fh = a.fo + 2 * (size_t)c.n_head * c.head_dim;
+        a.logits = logits;
+        a.part = p_part;
+        a.att_cnt = d_att_cnt;
+        a.amax = d_amax_key;
+        a.bar = d_bar;
+        a.err = d_perr;
+        a.trace = d_trace;
+        a.argmax = d_argmax;
+        a.pos = d_pos;
+        a.step = d_step;
+        a.token = d_token;
+        a.forced = d_forced;
+        a.nforced = d_nforced;
+        a.log = d_log;
+    }
+
+    void step_persistent(hipStream_t s, int token, int pos, bool device_state) {
+        ensure_persistent();
+        tf::check(tf_decode_persistent_launch(pargs, d_pargs, device_state ? 0 : 1, token, pos, s),
+                  "persistent step");
+    }
+
     void run_step(hipStream_t s, int token, int pos, bool device_state) {
         if (path == 0) step(s, token, pos, device_state);
+        else if (path == 4) step_persistent(s, token, pos, device_state);
         else step_fused(s, token, pos, device_state, path >= 2, path == 3);
     }
 
@@ -366,6 +530,10 @@ struct tf_model {
         tf::check((int)hipMemcpyAsync(d_step, &h[1], sizeof(int), hipMemcpyHostToDevice, s), "copy");
         tf::check((int)hipMemcpyAsync(d_token, &h[2], sizeof(int), hipMemcpyHostToDevice, s), "copy");
         tf::check((int)hipMemcpyAsync(d_nforced, &h[3], sizeof(int), hipMemcpyHostToDevice, s), "copy");
+        if (path == 4) {
+            ensure_persistent();
+            reset_persistent(s);
+        }
         if (use_graph) capture();
         for (int i = 0; i < total; i++) {
             if (use_graph) tf::check((int)hipGraphLaunch(graph_exec, s), "graph launch");
@@ -375,6 +543,31 @@ struct tf_model {
             tf::check((int)hipMemcpyAsync(tokens, d_log + n_forced - 1, sizeof(int) * n_gen,
                                           hipMemcpyDeviceToHost, s), "copy tokens");
         tf::check((int)hipStreamSynchronize(s), "sync");
+        check_persistent(s);
+        if (path == 4 && d_trace) dump_trace();
+    }
+
+    void dump_trace() {
+        std::vector<unsigned long long> h(trace_words);
+        tf::check((int)hipMemcpy(h.data(), d_trace, trace_words * sizeof(unsigned long long),
+                                 hipMemcpyDeviceToHost), "copy trace");
+        TfPArgs a{};
+        a.E = cfg.n_embd;
+        a.F = cfg.n_ff;
+        a.H = cfg.n_head;
+        a.KV = cfg.n_kv;
+        a.HD = cfg.head_dim;
+        const int grid = tf_decode_persistent_grid(a, nullptr);
+        FILE* f = std::fopen(std::getenv("TF_P_TRACE"), "w");
+        if (!f) return;
+        std::fprintf(f, "%d %d\n", 5 * cfg.n_layer + 2, grid);
+        for (int k = 0; k < 5 * cfg.n_layer + 2; k++) {
+            for (int b = 0; b < grid; b++)
+                for (int w = 0; w < 4; w++)
+                    std::fprintf(f, "%llu ", h[((size_t)k * grid + b) * 4 + w]);
+            std::fprintf(f, "\n");
+        }
+        std::fclose(f);
     }
 };
 
@@ -442,6 +635,9 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->d_nforced = m->alloc<int>(1);
         m->d_forced = m->alloc<int>(c.max_seq);
         m->d_log = m->alloc<int>(c.max_seq);
+        // the persistent step where the kernel serves this model, else the
+        // fused multi-launch step
+        m->path = m->persistent_ok() ? 4 : 3;
         *out = m.release();
         return 0;
     } catch (const tf::HipError& e) {
@@ -464,6 +660,7 @@ extern "C" int tf_model_forward(tf_model* m, int token, int pos, int* next_token
             tf::check((int)hipMemcpyAsync(next_token, m->d_argmax, sizeof(int),
                                           hipMemcpyDeviceToHost, s), "copy");
             tf::check((int)hipStreamSynchronize(s), "sync");
+            m->check_persistent(s);
         }
         return 0;
     } catch (const tf::HipError& e) {
@@ -486,7 +683,8 @@ extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, i
 }
 
 extern "C" int tf_model_set_path(tf_model* m, int path) {
-    if (!m || path < 0 || path > 3) return (int)hipErrorInvalidValue;
+    if (!m || path < 0 || path > 4) return (int)hipErrorInvalidValue;
+    if (path == 4 && !m->persistent_ok()) return (int)hipErrorNotSupported;
     if (m->path != path) {
         m->path = path;
         if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);

@@ -34,12 +34,12 @@ __device__ __forceinline__ void tf_q6k_load_c(const uint8_t* blk, int p, TfQ6kPa
     q.b = tf_ld16_a4(blk + 64 * n + 32 + 16 * h);
     q.hq = tf_ld16_a4(blk + 128 + 32 * n + 16 * h);
     q.sc = tf_ld8_a4(blk + 192 + 8 * n);
-    q.d = *reinterpret_cast<const uint32_t*>(blk + 208);
+    q.d = tf_gld(reinterpret_cast<const uint32_t*>(blk + 208));
 }
 
 // 210-byte raw blocks: only 2-byte alignment is guaranteed.
 __device__ __forceinline__ tf_u32x4 tf_ld16_a2(const uint8_t* p) {
-    const uint16_t* s = reinterpret_cast<const uint16_t*>(p);
+    const TF_GAS uint16_t* s = (const TF_GAS uint16_t*)p;
     tf_u32x4 v;
     v.x = s[0] | ((uint32_t)s[1] << 16);
     v.y = s[2] | ((uint32_t)s[3] << 16);
@@ -52,9 +52,9 @@ __device__ __forceinline__ void tf_q6k_load_r(const uint8_t* blk, int p, TfQ6kPa
     q.a = tf_ld16_a2(blk + 64 * n + 16 * h);
     q.b = tf_ld16_a2(blk + 64 * n + 32 + 16 * h);
     q.hq = tf_ld16_a2(blk + 128 + 32 * n + 16 * h);
-    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * n);
+    const TF_GAS uint16_t* s2 = (const TF_GAS uint16_t*)(blk + 192 + 8 * n);
     q.sc = tf_u32x2{s2[0] | ((uint32_t)s2[1] << 16), s2[2] | ((uint32_t)s2[3] << 16)};
-    q.d = reinterpret_cast<const uint16_t*>(blk + 208)[0];
+    q.d = ((const TF_GAS uint16_t*)(blk + 208))[0];
 }
 
 // Unsigned 6-bit values (0..63) of dword i of value group k, 4 per dword.

@@ -125,14 +125,31 @@ typedef uint32_t tf_u32x2 __attribute__((ext_vector_type(2)));
 struct __attribute__((packed, aligned(4))) tf_a4x4 { tf_u32x4 v; };
 struct __attribute__((packed, aligned(4))) tf_a4x2 { tf_u32x2 v; };
 
+// Global memory (address space 1).  The weight and cache loads below name
+// it explicitly: a pointer the compiler cannot trace to a kernel argument
+// (one read from a table in memory) would otherwise become a flat access,
+// which also counts against the LDS wait counter and so makes every LDS
+// wait drain the weight loads in flight.
+#define TF_GAS __attribute__((address_space(1)))
+
 __device__ __forceinline__ tf_u32x4 tf_ld16(const void* p) {
-    return reinterpret_cast<const tf_u32x4*>(p)[0];
+    return *(const TF_GAS tf_u32x4*)p;
 }
 __device__ __forceinline__ tf_u32x4 tf_ld16_a4(const void* p) {
-    return reinterpret_cast<const tf_a4x4*>(p)->v;
+    return ((const TF_GAS tf_a4x4*)p)->v;
 }
 __device__ __forceinline__ tf_u32x2 tf_ld8_a4(const void* p) {
-    return reinterpret_cast<const tf_a4x2*>(p)->v;
+    return ((const TF_GAS tf_a4x2*)p)->v;
+}
+// One value of type T (a scalar) from global memory.
+template <class T>
+__device__ __forceinline__ T tf_gld(const T* p) {
+    return *(const TF_GAS T*)p;
+}
+// Two consecutive floats from global memory (8-byte aligned).
+__device__ __forceinline__ float2 tf_gld2(const float* p) {
+    const unsigned long long v = *(const TF_GAS unsigned long long*)p;
+    return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
 }
 
 // ---------------------------------------------------------------- Q8 math

@@ -140,7 +140,7 @@ class DecodeModel:
     def set_path(self, path: int) -> None:
         """0 = reference kernel sequence, 1 = fused (quantize once),
         2 = fused with GEMV prologues, 3 = as 2 with a separate h quantize
-        (default)."""
+        (default), 4 = the whole step in one persistent launch."""
         rc = self.lib.tf_model_set_path(self.h, int(path))
         if rc != 0:
             raise capi.HipError(f"tf_model_set_path returned {rc}")

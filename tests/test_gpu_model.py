@@ -44,7 +44,7 @@ def build(cfg, seed, max_seq):
     return DecodeModel(c, layers, emb), RefModel(cfg, layers, emb, max_seq)
 
 
-@pytest.mark.parametrize("path", [0, 1, 2, 3])
+@pytest.mark.parametrize("path", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("ci", [0, 1, 2, 3])
 def test_decode_steps_match_reference(gpu, ci, path):
     cfg = TINY[ci]
@@ -76,7 +76,7 @@ def test_decode_steps_match_reference(gpu, ci, path):
     gm.close()
 
 
-@pytest.mark.parametrize("path", [0, 1, 2, 3])
+@pytest.mark.parametrize("path", [0, 1, 2, 3, 4])
 def test_graph_replay_equals_eager(gpu, path):
     cfg = TINY[1]
     gm, _ = build(cfg, 7, 64)
