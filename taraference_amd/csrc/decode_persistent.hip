@@ -62,10 +62,10 @@ __shared__ TfPLayer tf_p_layers[TF_P_MAX_LAYERS];
 // function addresses it as LDS.
 extern __shared__ __align__(16) uint8_t tf_p_lds[];
 __shared__ int tf_p_ok, tf_p_flag;  // tf_p_flag: sticky per-launch abort
+__shared__ int tf_p_last;
 
 #define TF_P_THREADS 512
 #define TF_P_WAVES (TF_P_THREADS / 64)
-#define TF_P_NQ (TF_P_THREADS / 256)  // 256-thread attention quarters
 #define TF_SPIN_LIMIT (1 << 20)
 #define TF_P_TILE 64
 #define TF_P_HD 128
@@ -139,7 +139,9 @@ __device__ __forceinline__ int tf_p_wid() {
 // Tags grow with the launch generation; the runtime zeroes the buffers
 // (tag 0, never expected) whenever it resets the generation.
 
-enum TfPKind { TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5 };
+enum TfPKind {
+    TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5, TF_PK_PART = 6
+};
 
 __device__ __forceinline__ unsigned tf_p_tag(unsigned tb, int li, int kind) {
     return tb + 8u * (unsigned)li + (unsigned)kind + 1u;
@@ -195,7 +197,7 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src
                 bad = 1;
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(4);
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const int i = i0 + k * R;
@@ -346,14 +348,28 @@ __device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* s
 // turn; then red[t] = p(t) + p(t + 128) (t < 128), v = red[t] + red[t + 64]
 // (t < 64), then the shift-down tree over 32, 16, ..., 1 -- the same
 // additions tf_norm_quant performs through LDS.
+// The four partials of a lane advance together, four terms at a time with
+// their LDS reads issued first; a padded term adds fmaf(0, 0, p) = p
+// exactly (p >= +0), so the value is that of the plain per-partial loop.
 __device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps) {
     const int lane = tf_p_tid() & 63;
-    float p[4];
+    const int nj = n / 256;
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < nj; j0 += 4) {
+        float v[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        float acc = 0.f;
-        for (int i = lane + 64 * c; i < n; i += 256) acc = fmaf(x[i], x[i], acc);
-        p[c] = acc;
+        for (int jj = 0; jj < 4; jj++) {
+            const int j = j0 + jj < nj ? j0 + jj : nj - 1;
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[jj][c] = x[lane + 64 * c + 256 * j];
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float t = j0 + jj < nj ? v[jj][c] : 0.f;
+                p[c] = fmaf(t, t, p[c]);
+            }
     }
     float v = (p[0] + p[2]) + (p[1] + p[3]);
     v += __shfl_down(v, 32, 64);
@@ -669,106 +685,199 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 
 // --------------------------------------------------- gate/up + SiLU
 //
-// Task map as tf_q4k_pair_rows_kernel (gemv_q4k.hip): with SPR <= 8 the even
-// units of a wave take gate rows and the odd units the up rows of the same
-// outputs; with SPR = 16 a lane loads both rows of one output.
+// h = silu(gate x) * up x, published already in Q8 (the activation the down
+// projection reads; kernels/gemv.cu:16-65 quantization of the f32 h, so the
+// bytes are those tf_quantize_q8 would make of the same h).  A workgroup
+// owns whole 32-value groups (g = blockIdx.x, + gridDim.x, ...); wave w
+// computes outputs 32 g + 4 w .. + 3 in 4 / JPW passes (with SPR <= 8 the
+// even units of a pass take gate rows and the odd units the up rows of the
+// same outputs, as tf_q4k_pair_rows_kernel; with SPR = 16 a lane loads both
+// rows of one output), the group's h is gathered in LDS and wave 0
+// quantizes it.  Published group g: words 9 g .. 9 g + 7 hold the 32 Q8
+// bytes (little-endian, 4 per word), word 9 g + 8 the scale d8.
+
+#define TF_P_MAX_GROUPS_PER_WG 4
+__shared__ float tf_p_hbuf[TF_P_MAX_GROUPS_PER_WG][32];
 
 template <int IT>
 struct TfPGuRegs {
     TfQ4kRow<IT> a, b;
 };
 
+template <int SPR>
+struct TfPGuMap {
+    static constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;  // outputs per pass
+    static constexpr int PASSES = 4 / JPW;                  // passes per group
+};
+
+// Task t of this wave: owned group k = t / PASSES, pass t % PASSES.
+template <int SPR>
+__device__ __forceinline__ int tf_p_gu_j(int k, int pass, int unit) {
+    const int g = blockIdx.x + k * gridDim.x;
+    const int wave = tf_p_tid() >> 6;
+    if constexpr (SPR <= 8)
+        return 32 * g + 4 * wave + TfPGuMap<SPR>::JPW * pass + (unit >> 1);
+    else
+        return 32 * g + 4 * wave + pass;
+}
+
 template <int SPR, int IT>
-__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int task,
+__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int t, int n_tasks,
                                              TfPGuRegs<IT>& r) {
+    if (t >= n_tasks) return;
     const TfPLane ln = tf_p_lane<SPR>();
-    const int nb = a.E / 256, F = a.F;
+    const int nb = a.E / 256;
+    constexpr int PS = TfPGuMap<SPR>::PASSES;
+    const int j = tf_p_gu_j<SPR>(t / PS, t % PS, ln.unit);
     if constexpr (SPR <= 8) {
-        constexpr int JPW = 16 / SPR / 2;
-        if (task >= (F + JPW - 1) / JPW) return;
-        const int j = task * JPW + (ln.unit >> 1);
-        const bool valid = j < F;
         const uint8_t* w = (ln.unit & 1) ? L.up : L.gate;
-        tf_q4k_row_load<SPR, IT>(w + (size_t)(valid ? j : 0) * L.cb_gu, valid, 0, nb, ln.sir, ln.t,
-                                 r.a);
+        tf_q4k_row_load<SPR, IT>(w + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
     } else {
-        if (task >= F) return;
-        tf_q4k_row_load<SPR, IT>(L.gate + (size_t)task * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
-        tf_q4k_row_load<SPR, IT>(L.up + (size_t)task * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.b);
+        tf_q4k_row_load<SPR, IT>(L.gate + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
+        tf_q4k_row_load<SPR, IT>(L.up + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.b);
     }
+}
+
+// Tasks of this wave: PASSES per owned group.
+__device__ __forceinline__ int tf_p_gu_owned(TfPA& a) {
+    const int ng = a.F / 32, b = blockIdx.x;
+    return b < ng ? (ng - 1 - b) / (int)gridDim.x + 1 : 0;
 }
 
 template <int SPR, int IT, int D>
 __device__ __forceinline__ void tf_p_gu_prefetch(TfPA& a, TfPL& L, TfPGuRegs<IT> (&r)[D]) {
-    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
+    const int n_tasks = tf_p_gu_owned(a) * TfPGuMap<SPR>::PASSES;
 #pragma unroll
-    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, wid + d * nwv, r[d]);
+    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, d, n_tasks, r[d]);
 }
 
-// The wave's gate/up tasks through a ring of D register sets (as
-// tf_p_rows_run).
+// Publishes the Q8 of one 32-value group held as 8 values per lane of a
+// quad (tf_q8_oct layout): words 9 g + 2 j, + 1 and (lane j = 0) the scale.
+__device__ __forceinline__ void tf_p_put_oct(unsigned long long* dst, int g, int j,
+                                             const TfQ8Oct& r, unsigned tag) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        lo |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
+        hi |= (uint32_t)(r.q[4 + i] & 0xff) << (8 * i);
+    }
+    tf_p_put(dst + 9 * g + 2 * j, lo, tag);
+    tf_p_put(dst + 9 * g + 2 * j + 1, hi, tag);
+    if (j == 0) tf_p_put(dst + 9 * g + 8, __float_as_uint(r.d), tag);
+}
+
 template <int SPR, int IT, int D>
 __device__ __forceinline__ void tf_p_gu_run(TfPA& a, TfPL& L, const TfAct& x,
                                             TfPGuRegs<IT> (&r)[D], unsigned long long* fh,
                                             unsigned tag) {
     const TfPLane ln = tf_p_lane<SPR>();
-    const int nb = a.E / 256, F = a.F;
-    const int wid = tf_p_wid(), nwv = gridDim.x * TF_P_WAVES;
-    constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;
-    const int n_tasks = (F + JPW - 1) / JPW;
-    for (int base = wid; base < n_tasks; base += D * nwv) {
+    const int nb = a.E / 256;
+    constexpr int PS = TfPGuMap<SPR>::PASSES, JPW = TfPGuMap<SPR>::JPW;
+    const int owned = tf_p_gu_owned(a);
+    const int n_tasks = owned * PS;
+    const int wave = tf_p_tid() >> 6;
+    for (int base = 0; base < n_tasks; base += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            const int task = base + d * nwv;
-            if (task >= n_tasks) break;  // wave-uniform
+            const int t = base + d;
+            if (t >= n_tasks) break;  // wave-uniform
+            const int k = t / PS, pass = t % PS;
             if constexpr (SPR <= 8) {
-                const int j = task * JPW + (ln.unit >> 1);
-                const bool valid = j < F;
-                float acc = tf_q4k_row_partial<SPR, IT>(r[d].a, valid, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, task + D * nwv, r[d]);
+                float acc = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
+                tf_p_gu_load<SPR, IT>(a, L, t + D, n_tasks, r[d]);
                 acc = tf_group_sum<4 * SPR>(acc);
                 const float other = __shfl(acc, (ln.lane + 4 * SPR) & 63, 64);
-                if (valid && (ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0)
-                    tf_p_putf(fh + j, (acc / (1.f + __expf(-acc))) * other, tag);
+                if ((ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0)
+                    tf_p_hbuf[k][4 * wave + JPW * pass + (ln.unit >> 1)] =
+                        (acc / (1.f + __expf(-acc))) * other;
             } else {
                 float g = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
                 float u = tf_q4k_row_partial<SPR, IT>(r[d].b, true, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, task + D * nwv, r[d]);
+                tf_p_gu_load<SPR, IT>(a, L, t + D, n_tasks, r[d]);
                 g = tf_group_sum<64>(g);
                 u = tf_group_sum<64>(u);
-                if (ln.lane == 0) tf_p_putf(fh + task, (g / (1.f + __expf(-g))) * u, tag);
+                if (ln.lane == 0) tf_p_hbuf[k][4 * wave + pass] = (g / (1.f + __expf(-g))) * u;
             }
         }
     }
+    __syncthreads();
+    if (wave == 0) {  // quad k quantizes owned group k
+        const int k = ln.lane >> 2, j = ln.lane & 3;
+        const int kc = k < owned ? k : 0;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[kc][8 * j + i];
+        const TfQ8Oct q = tf_q8_oct<false>(v);
+        if (k < owned) tf_p_put_oct(fh, blockIdx.x + k * gridDim.x, j, q, tag);
+    }
+}
+
+// Polls a Q8 vector published as 9-word groups (tf_p_put_oct layout) into the
+// LDS image of nb super-blocks, then forms the per-16 sums (s16) and
+// d8 * sum32 (ds) exactly as tf_stage_act does for a Q8 source.
+template <int K>
+__device__ __forceinline__ bool tf_p_poll_q8img(TfPA& a, uint8_t* lds, int nb,
+                                                const unsigned long long* src, unsigned tag) {
+    uint32_t* q8w = reinterpret_cast<uint32_t*>(lds);
+    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
+    float* dss = d8s + nb * 8;
+    int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
+    const int ng = nb * 8;
+    if (!tf_p_poll<K, 1>(
+            [&](int i, uint32_t b) {
+                const int g = i / 9, w = i - 9 * g;
+                if (w < 8) q8w[8 * g + w] = b;
+                else d8s[g] = __uint_as_float(b);
+            },
+            src, 9 * ng, tag, tf_p_tid(), TF_P_THREADS, a))
+        return false;
+    for (int g = tf_p_tid(); g < ng; g += TF_P_THREADS) {
+        const tf_u32x4 u0 = *reinterpret_cast<const tf_u32x4*>(q8w + 8 * g);
+        const tf_u32x4 u1 = *reinterpret_cast<const tf_u32x4*>(q8w + 8 * g + 4);
+        const int one = 0x01010101;
+        int sa = tf_dot4(one, (int)u0.x, 0);
+        sa = tf_dot4(one, (int)u0.y, sa);
+        sa = tf_dot4(one, (int)u0.z, sa);
+        sa = tf_dot4(one, (int)u0.w, sa);
+        int sb = tf_dot4(one, (int)u1.x, 0);
+        sb = tf_dot4(one, (int)u1.y, sb);
+        sb = tf_dot4(one, (int)u1.z, sb);
+        sb = tf_dot4(one, (int)u1.w, sb);
+        s16[2 * g] = sa;
+        s16[2 * g + 1] = sb;
+        dss[g] = d8s[g] * (float)(sa + sb);
+    }
+    __syncthreads();
+    return true;
 }
 
 // ------------------------------------------------------------ attention
 //
-// A workgroup serves one (kv head, split) pair; its four 256-thread
-// quarters walk four consecutive runs of 64-token tiles of that split with
-// the tile code of tf_flash_partial_kernel (flash.hip): K/V tiles staged in
-// LDS, next tile in registers, lane = token for the scores, lane = dims for
-// PV, HPW query heads per wave.  The quarters run in lockstep (same tile
-// count) so workgroup barriers stay uniform.  The four quarter results are
-// merged in LDS; with one split per kv head that is the attention output,
-// otherwise it is the workgroup's partial (m, l, O) and the last workgroup of
-// the kv head to finish (arrival ticket) merges all partials with the
-// reference's log-sum-exp formula (attn/flash.cu:222-255).
+// Split-KV flash decode (attn/flash.cu:16-255 semantics: per split the
+// running max m, normalizer l and unnormalized output O; splits merged with
+// the log-sum-exp formula).  A workgroup serves one (kv head, split) pair,
+// the split being a run of 64-token tiles; wave g owns query head g of the
+// kv head (G = n_head / n_kv <= 8).  Per tile: the workgroup stages K and V
+// in LDS (the next tile is already in registers); lane = token for the
+// scores (four independent 32-term chains over the head dimension); online
+// softmax per wave; lane = two output dims for PV (four independent chains
+// over the tokens).  With one split per kv head the wave writes its head's
+// output; otherwise it publishes (m, l, O) as tagged words and the first
+// workgroup of the kv head polls every split's partial and merges them.
 
+#define TF_P_KROW (TF_P_HD + 8)  // halves per padded K row in LDS
 
-template <int HPW>
-struct TfPAttnLds {
-    static constexpr int GMAX = 4 * HPW;
-    static constexpr int KROW = TF_P_HD + 8;
-    static constexpr int Q_FLOATS = GMAX * TF_P_HD;
-    static constexpr int P_FLOATS = GMAX * TF_P_TILE;
-    static constexpr int BYTES =
-        4 * (Q_FLOATS + P_FLOATS) + 2 * (TF_P_TILE * KROW + TF_P_TILE * TF_P_HD);
-    static constexpr int PER_THREAD = TF_P_TILE * TF_P_HD / 8 / 256;
+struct TfPAttnLayout {
+    static constexpr int K_BYTES = TF_P_TILE * TF_P_KROW * 2;
+    static constexpr int V_BYTES = TF_P_TILE * TF_P_HD * 2;
+    static constexpr int Q_BYTES = 8 * TF_P_HD * 4;
+    static constexpr int P_BYTES = 8 * TF_P_TILE * 4;
+    static constexpr int BYTES = K_BYTES + V_BYTES + Q_BYTES + P_BYTES;
+    static constexpr int CHUNKS = TF_P_TILE * TF_P_HD / 8 / TF_P_THREADS;  // 16 B per thread
 };
 
 struct TfPAttnGeo {
-    int n_ws, tpq, kh, ws, t_begin, t_end;
+    int n_ws, tpw, kh, ws, t_begin, t_end;
     bool active;
 };
 
@@ -778,42 +887,37 @@ __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     const int n_tiles = (seq + TF_P_TILE - 1) / TF_P_TILE;
     int per_kv = (int)gridDim.x / a.KV;
     per_kv = per_kv < 1 ? 1 : (per_kv > TF_P_MAX_SPLIT ? TF_P_MAX_SPLIT : per_kv);
-    int n_ws = (n_tiles + TF_P_NQ - 1) / TF_P_NQ;
-    g.n_ws = n_ws < per_kv ? n_ws : per_kv;
-    g.tpq = (n_tiles + TF_P_NQ * g.n_ws - 1) / (TF_P_NQ * g.n_ws);
+    const int n0 = n_tiles < per_kv ? n_tiles : per_kv;
+    g.tpw = (n_tiles + n0 - 1) / n0;
+    g.n_ws = (n_tiles + g.tpw - 1) / g.tpw;  // every split holds at least one tile
     const int b = blockIdx.x;
     g.active = b < a.KV * g.n_ws;
     g.kh = g.active ? b / g.n_ws : 0;
     g.ws = g.active ? b % g.n_ws : 0;
-    const int gq = g.ws * TF_P_NQ + (int)(tf_p_tid() >> 8);
-    const int tile0 = gq * g.tpq;
-    g.t_begin = tile0 * TF_P_TILE;
-    int te = (tile0 + g.tpq) * TF_P_TILE;
+    g.t_begin = g.ws * g.tpw * TF_P_TILE;
+    const int te = (g.ws + 1) * g.tpw * TF_P_TILE;
     g.t_end = te < seq ? te : seq;
     return g;
 }
 
-template <int HPW>
 struct TfPAttnRegs {
-    tf_u32x4 kr[TfPAttnLds<HPW>::PER_THREAD], vr[TfPAttnLds<HPW>::PER_THREAD];
+    tf_u32x4 kr[TfPAttnLayout::CHUNKS], vr[TfPAttnLayout::CHUNKS];
 };
 
-// Tile t0 of this quarter -> registers.  Row `pos` is produced in this
-// launch; it is left out here and taken from the flagged new K/V row when
-// the tile is stored to LDS.
-template <int HPW>
-__device__ __forceinline__ void tf_p_attn_load(TfPL& L, int stride, int kh, int t0,
-                                               int t_end, int pos, TfPAttnRegs<HPW>& r) {
-    const int qt = tf_p_tid() & 255;
+// Tile t0 -> registers (chunk c = tid + THREADS i: row c / 16, 8 halves at
+// 8 (c % 16)).  Unconditional loads from a valid row (see tf_p_poll); rows
+// past the split and the row `pos`, produced in this launch, are replaced
+// when the tile is stored.
+__device__ __forceinline__ void tf_p_attn_load(TfPL& L, int stride, int kh, int t0, int t_end,
+                                               int pos, TfPAttnRegs& r) {
+    const int tid = tf_p_tid();
     const uint16_t* kb = L.k_cache + (size_t)kh * TF_P_HD;
     const uint16_t* vb = L.v_cache + (size_t)kh * TF_P_HD;
 #pragma unroll
-    for (int i = 0; i < TfPAttnLds<HPW>::PER_THREAD; i++) {
-        const int c = qt + 256 * i;
+    for (int i = 0; i < TfPAttnLayout::CHUNKS; i++) {
+        const int c = tid + TF_P_THREADS * i;
         const int row = c / (TF_P_HD / 8), col = 8 * (c % (TF_P_HD / 8));
         const int t = t0 + row;
-        // unconditional loads from a valid row (see tf_p_poll); rows past the
-        // split and the row `pos` are replaced when the tile is stored
         const size_t off = (size_t)(t < t_end && t != pos ? t : 0) * stride + col;
         r.kr[i] = tf_ld16(kb + off);
         r.vr[i] = tf_ld16(vb + off);
@@ -822,32 +926,42 @@ __device__ __forceinline__ void tf_p_attn_load(TfPL& L, int stride, int kh, int 
 
 // Static LDS for the new K/V row of this workgroup's kv head (f16 bits).
 __shared__ __align__(16) uint16_t tf_p_knew[TF_P_HD], tf_p_vnew[TF_P_HD];
-__shared__ int tf_p_last;
 
-template <int HPW>
+// Publishes the Q8 of one 32-value group held as two values per lane of a
+// 16-lane row (tf_q8_pair layout, the quantization of tf_quantize_q8) in the
+// tf_p_put_oct word layout: group G_ at words 9 G_ ... ; m = lane & 15.
+__device__ __forceinline__ void tf_p_put_pair16(unsigned long long* dst, int G_, int m, float v0,
+                                                float v1, unsigned tag) {
+    const TfQ8Pair r = tf_q8_pair<false>(v0, v1);
+    const uint32_t h16 = (uint32_t)(r.q0 & 0xff) | ((uint32_t)(r.q1 & 0xff) << 8);
+    const uint32_t other = (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)h16);  // lane m ^ 1
+    if ((m & 1) == 0) tf_p_put(dst + 9 * G_ + (m >> 1), h16 | (other << 16), tag);
+    if (m == 0) tf_p_put(dst + 9 * G_ + 8, __float_as_uint(r.d), tag);
+}
+
+// Partial of (kv head kh, head g, split s): 2 + HD tagged words.
+__device__ __forceinline__ unsigned long long* tf_p_part(TfPA& a, int kh, int g, int s) {
+    const int G = a.H / a.KV;
+    return a.fpart + ((size_t)(kh * G + g) * TF_P_MAX_SPLIT + s) * (2 + TF_P_HD);
+}
+
 __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo& g, int pos,
-                                              TfPAttnRegs<HPW>& r, uint8_t* lds,
+                                              TfPAttnRegs& r, uint8_t* lds,
                                               const unsigned long long* fq,
                                               const unsigned long long* fkv, unsigned tq,
                                               unsigned tkv, unsigned long long* fo,
-                                              unsigned to, int tk) {
-    using LL = TfPAttnLds<HPW>;
-    constexpr int GMAX = LL::GMAX, HD = TF_P_HD, DPL = HD / 64;
-    const int tid = tf_p_tid(), qd = tid >> 8, qt = tid & 255, lane = tid & 63;
-    const int qw = (tid >> 6) & 3;
+                                              unsigned to, unsigned tp) {
+    using LA = TfPAttnLayout;
+    constexpr int HD = TF_P_HD;
+    const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KV, stride = a.KV * HD;
-    uint8_t* base = lds + qd * LL::BYTES;
-    float* q_lds = reinterpret_cast<float*>(base);
-    float* p_lds = q_lds + LL::Q_FLOATS;
-    uint16_t* k_lds = reinterpret_cast<uint16_t*>(p_lds + LL::P_FLOATS);
-    uint16_t* v_lds = k_lds + TF_P_TILE * LL::KROW;
-    // q of this kv head's G query heads (each quarter its copy) and the new
-    // K/V row; rows of q past G are zero
-    for (int i = qt; i < GMAX * HD; i += 256)
-        if (i >= G * HD) q_lds[i] = 0.f;
-    if (!tf_p_poll<(8 * TF_P_HD + 255) / 256, 1>(
-            [&](int i, uint32_t b) { q_lds[i] = __uint_as_float(b); },
-            fq + (size_t)g.kh * G * HD, G * HD, tq, qt, 256, a))
+    uint16_t* k_lds = reinterpret_cast<uint16_t*>(lds);
+    uint16_t* v_lds = reinterpret_cast<uint16_t*>(lds + LA::K_BYTES);
+    float* q_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES);
+    float* p_lds = q_lds + 8 * HD;
+    // q of the kv head's G query heads and the new K/V row
+    if (!tf_p_poll<2, 1>([&](int i, uint32_t b) { q_lds[i] = __uint_as_float(b); },
+                         fq + (size_t)g.kh * G * HD, G * HD, tq, tid, TF_P_THREADS, a))
         return false;
     if (!tf_p_poll<1, 1>(
             [&](int i, uint32_t b) {
@@ -856,23 +970,16 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
             },
             fkv + (size_t)g.kh * 2 * HD, 2 * HD, tkv, tid, TF_P_THREADS, a))
         return false;
-    tf_p_stamp(a, tk, 1);
 
-    float m[HPW], l[HPW], o[HPW][DPL];
-#pragma unroll
-    for (int hh = 0; hh < HPW; hh++) {
-        m[hh] = TF_P_NEG_BIG;
-        l[hh] = 0.f;
-#pragma unroll
-        for (int i = 0; i < DPL; i++) o[hh][i] = 0.f;
-    }
+    const bool own = wave < G;  // wave-uniform: this wave owns head `wave`
+    float m = TF_P_NEG_BIG, l = 0.f, o0 = 0.f, o1 = 0.f;
     const float scale = a.scale;
-    for (int it = 0; it < g.tpq; it++) {
+    for (int it = 0; it < g.tpw; it++) {
         const int t0 = g.t_begin + it * TF_P_TILE;
-        __syncthreads();
+        __syncthreads();  // the previous tile is consumed
 #pragma unroll
-        for (int i = 0; i < LL::PER_THREAD; i++) {
-            const int c = qt + 256 * i;
+        for (int i = 0; i < LA::CHUNKS; i++) {
+            const int c = tid + TF_P_THREADS * i;
             const int row = c / (HD / 8), col = 8 * (c % (HD / 8));
             tf_u32x4 kw = r.kr[i], vw = r.vr[i];
             if (t0 + row == pos) {  // the row produced in this launch
@@ -882,197 +989,141 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
                 kw = tf_u32x4{0, 0, 0, 0};
                 vw = tf_u32x4{0, 0, 0, 0};
             }
-            *reinterpret_cast<tf_u32x4*>(k_lds + row * LL::KROW + col) = kw;
+            *reinterpret_cast<tf_u32x4*>(k_lds + row * TF_P_KROW + col) = kw;
             *reinterpret_cast<tf_u32x4*>(v_lds + row * HD + col) = vw;
         }
-        if (it + 1 < g.tpq)
-            tf_p_attn_load<HPW>(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
+        if (it + 1 < g.tpw) tf_p_attn_load(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
         __syncthreads();
-        if (t0 >= g.t_end) continue;  // uniform per quarter; barriers stay matched
+        if (!own || t0 >= g.t_end) continue;
+        // ---- scores: lane = token, four chains of 32 terms
         const int t = t0 + lane;
         const bool tv = t < g.t_end;
-        float sc[HPW];
+        const uint16_t* krow = k_lds + lane * TF_P_KROW;
+        const float* qh = q_lds + wave * HD;
+        float sa[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int hh = 0; hh < HPW; hh++) sc[hh] = 0.f;
-        const uint16_t* krow = k_lds + lane * LL::KROW;
-#pragma unroll 4
-        for (int d = 0; d < HD; d += 8) {
-            const tf_u32x4 kw = *reinterpret_cast<const tf_u32x4*>(krow + d);
-            float kf[8];
-            kf[0] = tf_h2f(kw.x);
-            kf[1] = tf_h2f(kw.x >> 16);
-            kf[2] = tf_h2f(kw.y);
-            kf[3] = tf_h2f(kw.y >> 16);
-            kf[4] = tf_h2f(kw.z);
-            kf[5] = tf_h2f(kw.z >> 16);
-            kf[6] = tf_h2f(kw.w);
-            kf[7] = tf_h2f(kw.w >> 16);
-#pragma unroll
-            for (int hh = 0; hh < HPW; hh++) {
-                const float* qh = q_lds + (qw * HPW + hh) * HD + d;
-                const float4 q0 = *reinterpret_cast<const float4*>(qh);
-                const float4 q1 = *reinterpret_cast<const float4*>(qh + 4);
-                float acc = sc[hh];
-                acc += q0.x * kf[0];
-                acc += q0.y * kf[1];
-                acc += q0.z * kf[2];
-                acc += q0.w * kf[3];
-                acc += q1.x * kf[4];
-                acc += q1.y * kf[5];
-                acc += q1.z * kf[6];
-                acc += q1.w * kf[7];
-                sc[hh] = acc;
-            }
+        for (int dd = 0; dd < HD / 8; dd++) {
+            const tf_u32x4 kw = *reinterpret_cast<const tf_u32x4*>(krow + 8 * dd);
+            const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * dd);
+            const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * dd + 4);
+            float acc = sa[dd & 3];
+            acc += qa.x * tf_h2f(kw.x);
+            acc += qa.y * tf_h2f(kw.x >> 16);
+            acc += qa.z * tf_h2f(kw.y);
+            acc += qa.w * tf_h2f(kw.y >> 16);
+            acc += qb.x * tf_h2f(kw.z);
+            acc += qb.y * tf_h2f(kw.z >> 16);
+            acc += qb.z * tf_h2f(kw.w);
+            acc += qb.w * tf_h2f(kw.w >> 16);
+            sa[dd & 3] = acc;
         }
-#pragma unroll
-        for (int hh = 0; hh < HPW; hh++) {
-            const float sv = tv ? sc[hh] * scale : TF_P_NEG_BIG;
-            const float mx = tf_wave_max(sv);
-            const float m_new = fmaxf(m[hh], mx);
-            const float alpha = __expf(m[hh] - m_new);
-            const float e = tv ? __expf(sv - m_new) : 0.f;
-            p_lds[(qw * HPW + hh) * TF_P_TILE + lane] = e;
-            l[hh] = l[hh] * alpha + tf_group_sum<64>(e);
-            m[hh] = m_new;
-#pragma unroll
-            for (int i = 0; i < DPL; i++) o[hh][i] *= alpha;
-        }
+        const float sv = tv ? ((sa[0] + sa[1]) + (sa[2] + sa[3])) * scale : TF_P_NEG_BIG;
+        // ---- online softmax (wave = head)
+        const float m_new = fmaxf(m, tf_wave_max(sv));
+        const float alpha = __expf(m - m_new);
+        const float e = tv ? __expf(sv - m_new) : 0.f;
+        p_lds[wave * TF_P_TILE + lane] = e;
+        l = l * alpha + tf_group_sum<64>(e);
+        m = m_new;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // ---- PV: lane = dims 2 lane, 2 lane + 1; four chains over the tokens
         const int tlen = min(TF_P_TILE, g.t_end - t0);
-        const uint16_t* vcol = v_lds + lane * DPL;
+        const uint32_t* vcol = reinterpret_cast<const uint32_t*>(v_lds) + lane;
+        const float* pw = p_lds + wave * TF_P_TILE;
+        float c0[4] = {0.f, 0.f, 0.f, 0.f}, c1[4] = {0.f, 0.f, 0.f, 0.f};
         for (int tt = 0; tt < tlen; tt += 4) {
-            float pw[HPW][4];
-#pragma unroll
-            for (int hh = 0; hh < HPW; hh++) {
-                const float4 pv =
-                    *reinterpret_cast<const float4*>(p_lds + (qw * HPW + hh) * TF_P_TILE + tt);
-                pw[hh][0] = pv.x;
-                pw[hh][1] = pv.y;
-                pw[hh][2] = pv.z;
-                pw[hh][3] = pv.w;
-            }
+            const float4 pv = *reinterpret_cast<const float4*>(pw + tt);
+            const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const uint32_t vv = *reinterpret_cast<const uint32_t*>(vcol + (tt + u) * HD);
-                const float v0 = tf_h2f(vv), v1 = tf_h2f(vv >> 16);
-#pragma unroll
-                for (int hh = 0; hh < HPW; hh++) {
-                    o[hh][0] += pw[hh][u] * v0;
-                    o[hh][1] += pw[hh][u] * v1;
-                }
+                const uint32_t vv = vcol[(tt + u) * (HD / 2)];
+                c0[u] = fmaf(pp[u], tf_h2f(vv), c0[u]);
+                c1[u] = fmaf(pp[u], tf_h2f(vv >> 16), c1[u]);
             }
         }
+        o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
+        o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
     }
-    tf_p_stamp(a, tk, 2);
-    // ---- merge the quarters in LDS: mq[quarter][GMAX][2 + HD]
-    constexpr int PO = 2 + HD;
-    __syncthreads();
-    float* mq = reinterpret_cast<float*>(lds);
-#pragma unroll
-    for (int hh = 0; hh < HPW; hh++) {
-        const int gg = qw * HPW + hh;
-        float* dst = mq + ((size_t)qd * GMAX + gg) * PO;
-        if (lane == 0) {
-            dst[0] = m[hh];
-            dst[1] = l[hh];
-        }
-        dst[2 + lane * DPL] = o[hh][0];
-        dst[2 + lane * DPL + 1] = o[hh][1];
-    }
-    __syncthreads();
-    // (head, dim) outputs idx = tid + THREADS k of this kv head's G * HD
-    constexpr int OPT = 8 * TF_P_HD / TF_P_THREADS;  // outputs per thread (G <= 8)
-    float Mv[OPT], Lv[OPT], Ov[OPT];
-#pragma unroll
-    for (int k2 = 0; k2 < OPT; k2++) {
-        const int idx = tid + TF_P_THREADS * k2;
-        const int gh = idx / HD, dd = idx % HD;
-        float M = TF_P_NEG_BIG, Lw = 0.f, O = 0.f;
-        if (gh < G) {
-#pragma unroll
-            for (int k = 0; k < TF_P_NQ; k++) M = fmaxf(M, mq[((size_t)k * GMAX + gh) * PO]);
-#pragma unroll
-            for (int k = 0; k < TF_P_NQ; k++) {
-                const float* src = mq + ((size_t)k * GMAX + gh) * PO;
-                const float w = __expf(src[0] - M);
-                Lw += w * src[1];
-                O += w * src[2 + dd];
-            }
-        }
-        Mv[k2] = M;
-        Lv[k2] = Lw;
-        Ov[k2] = O;
-    }
+    // output group of this lane's dims: (head, 32-dim group) in Q8
+    const int og = ((g.kh * G + wave) * HD + 2 * lane) / 32;
     if (g.n_ws == 1) {
-#pragma unroll
-        for (int k2 = 0; k2 < OPT; k2++) {
-            const int idx = tid + TF_P_THREADS * k2;
-            if (idx / HD < G)
-                tf_p_putf(fo + (size_t)g.kh * G * HD + idx, Ov[k2] / fmaxf(Lv[k2], 1e-20f), to);
+        if (own) {
+            const float den = fmaxf(l, 1e-20f);
+            tf_p_put_pair16(fo, og, lane & 15, o0 / den, o1 / den, to);
         }
         return true;
     }
-    // ---- split partial, then the last workgroup of the kv head merges
-    const size_t pstride = (size_t)TF_P_MAX_SPLIT * PO;
+    // ---- publish this split's partial; the split-0 workgroup merges
+    if (own) {
+        unsigned long long* pp = tf_p_part(a, g.kh, wave, g.ws);
+        if (lane == 0) {
+            tf_p_putf(pp, m, tp);
+            tf_p_putf(pp + 1, l, tp);
+        }
+        tf_p_putf(pp + 2 + 2 * lane, o0, tp);
+        tf_p_putf(pp + 3 + 2 * lane, o1, tp);
+    }
+    if (g.ws != 0 || !own) return true;
+    // wave `wave` merges head `wave`: lane = dims 2 lane, 2 lane + 1; splits
+    // in chunks of 8, every word of a chunk polled together
+    float M = TF_P_NEG_BIG, Lt = 0.f, A0 = 0.f, A1 = 0.f;
+    for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
+        unsigned long long wm[8], wl[8], w0[8], w1[8];
 #pragma unroll
-    for (int k2 = 0; k2 < OPT; k2++) {
-        const int idx = tid + TF_P_THREADS * k2;
-        const int gh = idx / HD, dd = idx % HD;
-        if (gh < G) {
-            float* dst = a.part + (size_t)(g.kh * G + gh) * pstride + (size_t)g.ws * PO;
-            if (dd == 0) {
-                tf_stc(dst, Mv[k2]);
-                tf_stc(dst + 1, Lv[k2]);
+        for (int u = 0; u < 8; u++) {
+            const int sp = s0 + u < g.n_ws ? s0 + u : s0;
+            const unsigned long long* pp = tf_p_part(a, g.kh, wave, sp);
+            wm[u] = tf_ldc64(pp);
+            wl[u] = tf_ldc64(pp + 1);
+            w0[u] = tf_ldc64(pp + 2 + 2 * lane);
+            w1[u] = tf_ldc64(pp + 3 + 2 * lane);
+        }
+        for (int spins = 0;;) {
+            bool miss = false;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                miss |= (unsigned)(wm[u] >> 32) != tp || (unsigned)(wl[u] >> 32) != tp ||
+                        (unsigned)(w0[u] >> 32) != tp || (unsigned)(w1[u] >> 32) != tp;
+            if (!__builtin_amdgcn_ballot_w64(miss)) break;
+            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                tf_p_abort(a);
+                return true;  // the launch is aborted; outputs are not used
             }
-            tf_stc(dst + 2 + dd, Ov[k2]);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.att_cnt + g.kh, 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        tf_p_last = prev == (unsigned)(g.n_ws - 1);
-    }
-    __syncthreads();
-    if (!tf_p_last) return true;
-    // re-arm the ticket before the output can release the next layer
-    if (tid == 0) tf_stu(a.att_cnt + g.kh, 0u);
-    __builtin_amdgcn_s_waitcnt(0);
-    float* wts = reinterpret_cast<float*>(lds);  // [GMAX][64]
-    float* Ls = wts + GMAX * 64;
-    {
-        const int gw = tid >> 6;  // one wave per head, lane = split
-        if (gw < G) {
-            const float* src = a.part + (size_t)(g.kh * G + gw) * pstride + (size_t)lane * PO;
-            const bool live = lane < g.n_ws;
-            const float ms = live ? tf_ldc(src) : TF_P_NEG_BIG;
-            const float ls = live ? tf_ldc(src + 1) : 0.f;
-            const float Mx = tf_wave_max(ms);
-            const float w = live ? __expf(ms - Mx) : 0.f;
-            const float Ltot = tf_group_sum<64>(w * ls);
-            wts[gw * 64 + lane] = w;
-            if (lane == 0) Ls[gw] = Ltot;
-        }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * HD; idx += TF_P_THREADS) {
-        const int gh = idx / HD, dd = idx % HD;
-        const float* src = a.part + (size_t)(g.kh * G + gh) * pstride + 2 + dd;
-        float acc = 0.f;
-        for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
-            float v[8];
+            __builtin_amdgcn_s_sleep(4);
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                v[u] = s0 + u < g.n_ws ? tf_ldc(src + (size_t)(s0 + u) * PO) : 0.f;
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (s0 + u < g.n_ws) acc += wts[gh * 64 + s0 + u] * v[u];
+            for (int u = 0; u < 8; u++) {
+                const int sp = s0 + u < g.n_ws ? s0 + u : s0;
+                const unsigned long long* pp = tf_p_part(a, g.kh, wave, sp);
+                wm[u] = tf_ldc64(pp);
+                wl[u] = tf_ldc64(pp + 1);
+                w0[u] = tf_ldc64(pp + 2 + 2 * lane);
+                w1[u] = tf_ldc64(pp + 3 + 2 * lane);
+            }
         }
-        tf_p_putf(fo + (size_t)g.kh * G * HD + idx, acc / fmaxf(Ls[gh], 1e-20f), to);
+        // merge the chunk: M' = max(M, m_s); running sums rescaled to M'
+        float Mc = M;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < g.n_ws) Mc = fmaxf(Mc, __uint_as_float((unsigned)wm[u]));
+        const float r0 = __expf(M - Mc);
+        Lt *= r0;
+        A0 *= r0;
+        A1 *= r0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (s0 + u < g.n_ws) {
+                const float w = __expf(__uint_as_float((unsigned)wm[u]) - Mc);
+                Lt = fmaf(w, __uint_as_float((unsigned)wl[u]), Lt);
+                A0 = fmaf(w, __uint_as_float((unsigned)w0[u]), A0);
+                A1 = fmaf(w, __uint_as_float((unsigned)w1[u]), A1);
+            }
+        }
+        M = Mc;
     }
+    const float den = fmaxf(Lt, 1e-20f);
+    tf_p_put_pair16(fo, og, lane & 15, A0 / den, A1 / den, to);
     return true;
 }
 
@@ -1153,21 +1204,20 @@ __device__ __noinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int p
     return true;
 }
 
-template <int HPW>
 __device__ __noinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     const TfPAttnGeo g = tf_p_attn_geo(a, pos);
     if (!g.active) return true;
-    TfPAttnRegs<HPW> ra;
-    tf_p_attn_load<HPW>(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
+    TfPAttnRegs ra;
+    tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    const bool ok = tf_p_attn_run<HPW>(
+    const bool ok = tf_p_attn_run(
         a, L, g, pos, ra, lds, tf_p_vec(a, TF_PK_Q, li), tf_p_vec(a, TF_PK_KV, li),
         tf_p_tag(tb, li, TF_PK_Q), tf_p_tag(tb, li, TF_PK_KV), tf_p_vec(a, TF_PK_O, li),
-        tf_p_tag(tb, li, TF_PK_O), 5 * li + 1);
+        tf_p_tag(tb, li, TF_PK_O), tf_p_tag(tb, li, TF_PK_PART));
     tf_p_stamp(a, 5 * li + 1, 3);
     return ok;
 }
@@ -1191,16 +1241,14 @@ __device__ __noinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int to
     TfPL& L = tf_p_layer(a, li);
     const int nbE = a.E / 256;
     const TfAct xE = tf_act_view(lds, nbE);
-    float* xf = const_cast<float*>(xE.xf);
     TfPRow<IT, false> ro[1];
     tf_p_rows_prefetch<SPR, IT, false, 1>(L.wo, L.cb_o, nbE, a.E, ro);
     tf_p_stamp(a, 5 * li + 2, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
-            a, xf, tf_p_vec(a, TF_PK_O, li), a.E, tf_p_tag(tb, li, TF_PK_O)))
+    if (!tf_p_poll_q8img<(9 * 4096 / 32 + TF_P_THREADS - 1) / TF_P_THREADS>(
+            a, lds, nbE, tf_p_vec(a, TF_PK_O, li), tf_p_tag(tb, li, TF_PK_O)))
         return false;
     tf_p_stamp(a, 5 * li + 2, 1);
-    tf_p_stage8<false, false>(lds, nbE, xf, 1.f, tf_p_now);
     tf_p_stamp(a, 5 * li + 2, 2);
     tf_p_rows_run<SPR, IT, false, 1, 0>(
         L.wo, L.cb_o, nbE, a.E, xE, ro, [&](int j) { return tf_p_res_in(a, li, tb, token, j); },
@@ -1216,7 +1264,9 @@ __device__ __noinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     TfPL& L = tf_p_layer(a, li);
     const int nbE = a.E / 256;
     const TfAct xE = tf_act_view(lds, nbE);
-    constexpr int D = SPR <= 8 ? 4 : 2;
+    // the whole workload of a workgroup that owns two groups is in flight
+    // before the input poll (SPR <= 8: 8 tasks of one row per lane)
+    constexpr int D = SPR <= 8 ? 8 : 3;
     TfPGuRegs<IT> rg[D];
     tf_p_gu_prefetch<SPR, IT, D>(a, L, rg);
     float nw[8];
@@ -1241,18 +1291,16 @@ __device__ __forceinline__ bool tf_p_down_body(TfPA& a, TfPL& L, int li, unsigne
     uint8_t* lds = tf_p_lds;
     const int nbF = a.F / 256;
     const TfAct xF = tf_act_view(lds, nbF);
-    float* hf = const_cast<float*>(xF.xf);
     TfPRow<IT, Q6> rd[1];
     tf_p_rows_prefetch<SPR, IT, Q6, 1>(L.down, L.cb_down, nbF, a.E, rd);
     tf_p_stamp(a, 5 * li + 4, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    // h in one pass up to 11264 values (44 registers), else in two
-    constexpr int HK = IT <= 3 ? 22 : 19, HP = IT <= 3 ? 1 : 2;
-    if (!tf_p_poll_xf<HK, HP>(a, hf, tf_p_vec(a, TF_PK_H, li), a.F, tf_p_tag(tb, li, TF_PK_H)))
+    // Q8 h: 9 words per 32 values, one pass (up to 19456 values: nbF <= 76)
+    if (!tf_p_poll_q8img<(9 * 19456 / 32 + TF_P_THREADS - 1) / TF_P_THREADS>(
+            a, lds, nbF, tf_p_vec(a, TF_PK_H, li), tf_p_tag(tb, li, TF_PK_H)))
         return false;
     tf_p_stamp(a, 5 * li + 4, 1);
-    tf_p_stage8<false, false>(lds, nbF, hf, 1.f, tf_p_now);
-    tf_p_stamp(a, 5 * li + 4, 2);
+    tf_p_stamp(a, 5 * li + 4, 2);  // (no staging: h arrives in Q8)
     const unsigned long long* xm = tf_p_vec(a, TF_PK_XA, li);
     tf_p_rows_run<SPR, IT, Q6, 1, 0>(
         L.down, L.cb_down, nbF, a.E, xF, rd,
@@ -1339,7 +1387,7 @@ __device__ __noinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_mod
 
 // ------------------------------------------------------------ the kernel
 
-template <int SPR_E, int IT_E, int SPR_F, int IT_F, int HPW>
+template <int SPR_E, int IT_E, int SPR_F, int IT_F>
 __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     const TfPArgs* args, int host_mode, int token_host, int pos_host) {
     {
@@ -1363,7 +1411,7 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     __syncthreads();
     for (int li = 0; li < a.n_layer; li++) {
         if (!tf_p_stage_qkv<SPR_E, IT_E>(&a, li, tb, pos, token)) return;
-        if (!tf_p_stage_attn<HPW>(&a, li, tb, pos)) return;
+        if (!tf_p_stage_attn(&a, li, tb, pos)) return;
         if (!tf_p_stage_wo<SPR_E, IT_E>(&a, li, tb, token)) return;
         if (!tf_p_stage_gu<SPR_E, IT_E>(&a, li, tb)) return;
         if (!tf_p_stage_down<SPR_F, IT_F>(&a, li, tb)) return;
@@ -1375,13 +1423,12 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
 
 namespace {
 
-template <int HPW>
 int tf_p_lds(const TfPArgs& a) {
     const int nbE = a.E / 256, nbF = a.F / 256;
     int b = tf_act_lds_bytes(nbE, true) + 4 * a.E;
     const int f = tf_act_lds_bytes(nbF, true);
     if (f > b) b = f;
-    const int at = TF_P_NQ * TfPAttnLds<HPW>::BYTES;
+    const int at = TfPAttnLayout::BYTES;
     return at > b ? at : b;
 }
 
@@ -1390,11 +1437,11 @@ struct TfPLaunch {
     int host_mode, token, pos;
 };
 
-template <int SE, int IE, int SF, int IF, int HPW>
+template <int SE, int IE, int SF, int IF>
 int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid_out,
                   int* lds_out) {
-    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, HPW>;
-    const int lds = tf_p_lds<HPW>(a);
+    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF>;
+    const int lds = tf_p_lds(a);
     static int attr_done[64];
     int dev = 0;
     (void)hipGetDevice(&dev);
@@ -1419,25 +1466,24 @@ int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid
     return (int)hipGetLastError();
 }
 
-// Instantiations: (SPR, ITERS) of the model width and of the FFN width, and
-// query heads per wave (G = n_head / n_kv <= 4 HPW).
+// Instantiations: (SPR, ITERS) of the model width and of the FFN width.
+// One wave per query head of a kv head (G <= 8); the FFN width also bounds
+// the unrolled poll of h (22 words per thread in one pass, or 19 in two).
 template <class F>
 int tf_p_dispatch(int E, int F_, int H, int KV, int HD, F&& f) {
-    if (HD != TF_P_HD || KV <= 0 || H % KV) return -1;
-    const int nbE = E / 256, nbF = F_ / 256, G = H / KV;
-    if (nbE <= 4 && nbF <= 4 && G <= 4) return f(std::integral_constant<int, 0>{});
-    if (nbE > 4 && nbE <= 8 && nbF > 32 && nbF <= 48 && G <= 8)
-        return f(std::integral_constant<int, 1>{});
-    if (nbE > 8 && nbE <= 16 && nbF > 64 && nbF <= 80 && G <= 8)
-        return f(std::integral_constant<int, 2>{});
+    if (HD != TF_P_HD || KV <= 0 || H % KV || H / KV > TF_P_WAVES) return -1;
+    const int nbE = E / 256, nbF = F_ / 256;
+    if (nbE <= 4 && nbF <= 4) return f(std::integral_constant<int, 0>{});
+    if (nbE > 4 && nbE <= 8 && nbF > 32 && nbF <= 44) return f(std::integral_constant<int, 1>{});
+    if (nbE > 8 && nbE <= 16 && nbF > 64 && nbF <= 76) return f(std::integral_constant<int, 2>{});
     return -1;
 }
 
 template <int V>
 int tf_p_call(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid, int* lds) {
-    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1, 1>(a, l, s, grid, lds);
-    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3, 2>(a, l, s, grid, lds);
-    else return tf_p_launch_t<16, 1, 16, 5, 2>(a, l, s, grid, lds);
+    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1>(a, l, s, grid, lds);
+    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3>(a, l, s, grid, lds);
+    else return tf_p_launch_t<16, 1, 16, 5>(a, l, s, grid, lds);
 }
 
 }  // namespace

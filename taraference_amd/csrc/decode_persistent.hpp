@@ -53,8 +53,8 @@ struct TfPArgs {
     // fh [2][F] silu(gate) * up.
     unsigned long long *fx, *fq, *fkv, *fo, *fh;
     float* logits;  // [n_vocab]
-    float* part;    // split-KV partials [KV][G][TF_P_MAX_SPLIT][2 + HD]
-    unsigned* att_cnt;         // [KV] arrival tickets of the attention merge
+    // split-KV partials (m, l, O[HD]) as tagged words [KV][G][TF_P_MAX_SPLIT][2 + HD]
+    unsigned long long* fpart;
     unsigned long long* amax;  // TF_ARGMAX_SLOTS argmax keys
     unsigned* bar;             // TF_BAR_WORDS barrier words
     int* err;                  // nonzero after a barrier time-out

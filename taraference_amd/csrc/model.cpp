@@ -110,9 +110,9 @@ struct tf_model {
     // persistent-step state (allocated on first use of path 4)
     TfPLayer* d_players = nullptr;
     unsigned* d_bar = nullptr;
-    unsigned* d_att_cnt = nullptr;
     int* d_perr = nullptr;
-    float* p_part = nullptr;
+    unsigned long long* p_part = nullptr;
+    size_t p_part_words = 0;
     unsigned long long* p_flags = nullptr;  // the flagged stage vectors
     size_t p_flag_words = 0;
     // diagnostic stage timeline of the persistent step: when the environment
@@ -398,13 +398,13 @@ struct tf_model {
         tf::check((int)hipMemcpy(d_players, h.data(), h.size() * sizeof(TfPLayer),
                                  hipMemcpyHostToDevice), "copy layer table");
         d_bar = alloc<unsigned>(TF_BAR_WORDS);
-        d_att_cnt = alloc<unsigned>(c.n_kv);
         d_perr = alloc<int>(1);
         p_flag_words = (size_t)4 * c.n_embd + 2 * (size_t)c.n_head * c.head_dim +
                        4 * (size_t)c.n_kv * c.head_dim + 2 * (size_t)c.n_head * c.head_dim +
                        2 * (size_t)c.n_ff;
         p_flags = alloc<unsigned long long>(p_flag_words);
-        p_part = alloc<float>((size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim));
+        p_part_words = (size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim);
+        p_part = alloc<unsigned long long>(p_part_words);
         if (std::getenv("TF_P_TRACE")) {
             trace_words = (size_t)(5 * c.n_layer + 2) * TF_P_MAX_WG * 4;
             d_trace = alloc<unsigned long long>(trace_words);
@@ -420,7 +420,8 @@ struct tf_model {
     // generation; also clears what an aborted launch left behind).
     void reset_persistent(hipStream_t s) {
         tf::check((int)hipMemsetAsync(d_bar, 0, TF_BAR_WORDS * sizeof(unsigned), s), "memset");
-        tf::check((int)hipMemsetAsync(d_att_cnt, 0, cfg.n_kv * sizeof(unsigned), s), "memset");
+        tf::check((int)hipMemsetAsync(p_part, 0, p_part_words * sizeof(unsigned long long), s),
+                  "memset");
         tf::check((int)hipMemsetAsync(d_perr, 0, sizeof(int), s), "memset");
         tf::check((int)hipMemsetAsync(p_flags, 0, p_flag_words * sizeof(unsigned long long), s),
                   "memset");
@@ -469,8 +470,7 @@ struct tf_model {
         a.fo = a.fkv + 4 * (size_t)c.n_kv * c.head_dim;
         a.fh = a.fo + 2 * (size_t)c.n_head * c.head_dim;
         a.logits = logits;
-        a.part = p_part;
-        a.att_cnt = d_att_cnt;
+        a.fpart = p_part;
         a.amax = d_amax_key;
         a.bar = d_bar;
         a.err = d_perr;
