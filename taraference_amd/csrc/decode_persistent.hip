@@ -1204,12 +1204,35 @@ __device__ __noinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int p
     return true;
 }
 
+// Cache warm-up by the workgroups that have no attention work: they read one
+// dword of every 128-byte line of this layer's wo, gate, up and down weights
+// (the values are discarded), so the memory-side cache holds those lines
+// when the next stages stream them.
+__device__ __forceinline__ void tf_p_warm(TfPA& a, TfPL& L, int idle_rank, int n_idle) {
+    const uint8_t* ptrs[4] = {L.wo, L.gate, L.up, L.down};
+    const size_t bytes[4] = {(size_t)a.E * L.cb_o, (size_t)a.F * L.cb_gu, (size_t)a.F * L.cb_gu,
+                             (size_t)a.E * L.cb_down};
+    const size_t stride = (size_t)n_idle * TF_P_THREADS;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const size_t lines = bytes[m] / 128;
+        for (size_t ln = (size_t)idle_rank * TF_P_THREADS + tf_p_tid(); ln < lines; ln += stride)
+            acc ^= tf_gld(reinterpret_cast<const uint32_t*>(ptrs[m] + ln * 128));
+    }
+    asm volatile("" ::"v"(acc));
+}
+
 __device__ __noinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     const TfPAttnGeo g = tf_p_attn_geo(a, pos);
-    if (!g.active) return true;
+    if (!g.active) {
+        const int n_att = a.KV * g.n_ws;
+        tf_p_warm(a, L, (int)blockIdx.x - n_att, (int)gridDim.x - n_att);
+        return true;
+    }
     TfPAttnRegs ra;
     tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
