@@ -236,6 +236,7 @@ def main():
     tok_s = steps / dt
     log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
     wbytes = synth.weight_bytes(cfg)
+    path = m.path()
     m.close()
     del m
     torch.cuda.empty_cache()
@@ -250,6 +251,20 @@ def main():
             "kernel": ROOFLINE_KERNEL,
             "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
             "us_per_launch_single": round(r["per_us"], 3)}
+    # the decode step itself: one launch per token on the default path (the
+    # persistent kernel); algorithmic bytes per launch = the weights once
+    # plus the K/V cache the attention reads (mean context of the timed
+    # steps), over the measured time per step
+    ctx_mean = args.warmup + steps / 2.0
+    kv_bytes = int(2 * cfg["n_layer"] * ctx_mean * cfg["n_kv"] * cfg["head_dim"] * 2)
+    step_bytes = wbytes + kv_bytes
+    step_gbs = step_bytes / (dt / steps) / 1e9
+    decode_roof = {"bound": "hbm", "kernel": (f"decode step, path {path}" +
+                                              (" (tf_decode_persistent_kernel, one launch per "
+                                               "token)" if path == 4 else "")),
+                   "bytes_per_launch": step_bytes, "us_per_launch": round(dt / steps * 1e6, 2),
+                   "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                   "frac": round(step_gbs / HBM_PEAK_GBS, 4)}
     table = {} if args.no_kernels else kernel_table(args.kernel_iters)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
 
@@ -272,6 +287,7 @@ def main():
                    "effective_weight_GBs": round(wbytes * tok_s / 1e9, 1),
                    "parallelism": "single GPU"},
         "roofline": roof,
+        "roofline_decode_step": decode_roof,
         "cpu_baseline": cpu,
         "kernels": table,
         "greedy_tokens_head": [int(t) for t in toks[:8]],

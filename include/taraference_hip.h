@@ -397,6 +397,9 @@ int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
  *      instantiation for (the default where it applies).
  * Changing the path drops the captured graph. */
 int tf_model_set_path(tf_model *m, int path);
+/* The decode path in use (the default chosen at creation, or the last
+ * tf_model_set_path); -1 for a null handle. */
+int tf_model_get_path(const tf_model *m);
 /* Device pointer of the last logits (n_vocab floats) and of the f16 K/V
  * cache of layer li. */
 const float *tf_model_logits(const tf_model *m);

@@ -682,6 +682,8 @@ extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, i
     }
 }
 
+extern "C" int tf_model_get_path(const tf_model* m) { return m ? m->path : -1; }
+
 extern "C" int tf_model_set_path(tf_model* m, int path) {
     if (!m || path < 0 || path > 4) return (int)hipErrorInvalidValue;
     if (path == 4 && !m->persistent_ok()) return (int)hipErrorNotSupported;

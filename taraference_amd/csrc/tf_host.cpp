@@ -122,6 +122,7 @@ static const char* const k_symbols[] = {
     "tf_model_forward",
     "tf_model_generate",
     "tf_model_set_path",
+    "tf_model_get_path",
     "tf_model_logits",
     "tf_model_k_cache",
     "tf_model_v_cache",

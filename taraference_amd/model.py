@@ -51,6 +51,8 @@ def _bind(lib):
     lib.tf_model_generate.restype = C.c_int
     lib.tf_model_set_path.argtypes = [C.c_void_p, C.c_int]
     lib.tf_model_set_path.restype = C.c_int
+    lib.tf_model_get_path.argtypes = [C.c_void_p]
+    lib.tf_model_get_path.restype = C.c_int
     lib.tf_model_logits.argtypes = [C.c_void_p]
     lib.tf_model_logits.restype = C.c_void_p
     for n in ("tf_model_k_cache", "tf_model_v_cache"):
@@ -144,6 +146,11 @@ class DecodeModel:
         rc = self.lib.tf_model_set_path(self.h, int(path))
         if rc != 0:
             raise capi.HipError(f"tf_model_set_path returned {rc}")
+
+    def path(self) -> int:
+        """The decode path in use (4 = persistent step, the default where it
+        applies)."""
+        return int(self.lib.tf_model_get_path(self.h))
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.cfg["n_vocab"], np.float32)
