@@ -140,7 +140,8 @@ __device__ __forceinline__ int tf_p_wid() {
 // (tag 0, never expected) whenever it resets the generation.
 
 enum TfPKind {
-    TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5, TF_PK_PART = 6
+    TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5, TF_PK_PART = 6,
+    TF_PK_HX = 7
 };
 
 __device__ __forceinline__ unsigned tf_p_tag(unsigned tb, int li, int kind) {
@@ -687,17 +688,25 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 //
 // h = silu(gate x) * up x, published already in Q8 (the activation the down
 // projection reads; kernels/gemv.cu:16-65 quantization of the f32 h, so the
-// bytes are those tf_quantize_q8 would make of the same h).  A workgroup
-// owns whole 32-value groups (g = blockIdx.x, + gridDim.x, ...); wave w
-// computes outputs 32 g + 4 w .. + 3 in 4 / JPW passes (with SPR <= 8 the
-// even units of a pass take gate rows and the odd units the up rows of the
-// same outputs, as tf_q4k_pair_rows_kernel; with SPR = 16 a lane loads both
-// rows of one output), the group's h is gathered in LDS and wave 0
-// quantizes it.  Published group g: words 9 g .. 9 g + 7 hold the 32 Q8
-// bytes (little-endian, 4 per word), word 9 g + 8 the scale d8.
+// bytes are those tf_quantize_q8 would make of the same h).  Work is dealt
+// in half-groups of 16 outputs: workgroup b takes half-groups
+// [F/16 b / grid, F/16 (b + 1) / grid), so no workgroup has more than one
+// half-group above the fair share; wave w computes outputs 16 h + 2 w, + 1 of
+// half-group h in 2 / JPW passes (with SPR <= 8 the even units of a pass take
+// gate rows and the odd units the up rows of the same outputs, as
+// tf_q4k_pair_rows_kernel; with SPR = 16 a lane loads both rows of one
+// output).  A workgroup quantizes each group whose first half it holds: h is
+// gathered in LDS and wave 0 quantizes it.  A group split between two
+// workgroups has its second half computed first by the later workgroup,
+// which publishes those 16 values as tagged f32 words (the exchange area,
+// fh + F / 2 + 16 g); the earlier workgroup computes its first half last and
+// reads them.  Published group g: words 9 g .. 9 g + 7 hold the 32 Q8 bytes
+// (little-endian, 4 per word), word 9 g + 8 the scale d8.
 
-#define TF_P_MAX_GROUPS_PER_WG 4
-__shared__ float tf_p_hbuf[TF_P_MAX_GROUPS_PER_WG][32];
+// Half-groups per workgroup the LDS gather holds (one more slot takes a
+// split group's second half).
+#define TF_P_MAX_HALVES_PER_WG 7
+__shared__ float tf_p_hbuf[TF_P_MAX_HALVES_PER_WG + 1][16];
 
 template <int IT>
 struct TfPGuRegs {
@@ -707,28 +716,39 @@ struct TfPGuRegs {
 template <int SPR>
 struct TfPGuMap {
     static constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;  // outputs per pass
-    static constexpr int PASSES = 4 / JPW;                  // passes per group
+    static constexpr int PH = 2 / JPW;                      // passes per half-group
+    static_assert(JPW >= 1 && JPW <= 2, "gate/up lane map needs SPR >= 4");
 };
 
-// Task t of this wave: owned group k = t / PASSES, pass t % PASSES.
-template <int SPR>
-__device__ __forceinline__ int tf_p_gu_j(int k, int pass, int unit) {
-    const int g = blockIdx.x + k * gridDim.x;
-    const int wave = tf_p_tid() >> 6;
-    if constexpr (SPR <= 8)
-        return 32 * g + 4 * wave + TfPGuMap<SPR>::JPW * pass + (unit >> 1);
-    else
-        return 32 * g + 4 * wave + pass;
+// Half-groups [s, e) of this workgroup.
+struct TfPGuSpan {
+    int s, e;
+};
+
+__device__ __forceinline__ TfPGuSpan tf_p_gu_span(TfPA& a) {
+    const int nh = a.F / 16, b = blockIdx.x, G = gridDim.x;
+    return {(int)((long long)nh * b / G), (int)((long long)nh * (b + 1) / G)};
 }
 
+// Output row of pass p of half-group h for this wave's lane unit.
+template <int SPR>
+__device__ __forceinline__ int tf_p_gu_j(int h, int p, int unit) {
+    const int wave = tf_p_tid() >> 6;
+    if constexpr (SPR <= 8)
+        return 16 * h + 2 * wave + TfPGuMap<SPR>::JPW * p + (unit >> 1);
+    else
+        return 16 * h + 2 * wave + p;
+}
+
+// Task t of this wave: half-group s + t / PH, pass t % PH.
 template <int SPR, int IT>
-__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int t, int n_tasks,
+__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, const TfPGuSpan& sp, int t,
                                              TfPGuRegs<IT>& r) {
-    if (t >= n_tasks) return;
+    constexpr int PH = TfPGuMap<SPR>::PH;
+    if (t >= (sp.e - sp.s) * PH) return;
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    constexpr int PS = TfPGuMap<SPR>::PASSES;
-    const int j = tf_p_gu_j<SPR>(t / PS, t % PS, ln.unit);
+    const int j = tf_p_gu_j<SPR>(sp.s + t / PH, t % PH, ln.unit);
     if constexpr (SPR <= 8) {
         const uint8_t* w = (ln.unit & 1) ? L.up : L.gate;
         tf_q4k_row_load<SPR, IT>(w + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
@@ -738,17 +758,11 @@ __device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int t, int n_task
     }
 }
 
-// Tasks of this wave: PASSES per owned group.
-__device__ __forceinline__ int tf_p_gu_owned(TfPA& a) {
-    const int ng = a.F / 32, b = blockIdx.x;
-    return b < ng ? (ng - 1 - b) / (int)gridDim.x + 1 : 0;
-}
-
 template <int SPR, int IT, int D>
 __device__ __forceinline__ void tf_p_gu_prefetch(TfPA& a, TfPL& L, TfPGuRegs<IT> (&r)[D]) {
-    const int n_tasks = tf_p_gu_owned(a) * TfPGuMap<SPR>::PASSES;
+    const TfPGuSpan sp = tf_p_gu_span(a);
 #pragma unroll
-    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, d, n_tasks, r[d]);
+    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, sp, d, r[d]);
 }
 
 // Publishes the Q8 of one 32-value group held as 8 values per lane of a
@@ -766,50 +780,83 @@ __device__ __forceinline__ void tf_p_put_oct(unsigned long long* dst, int g, int
     if (j == 0) tf_p_put(dst + 9 * g + 8, __float_as_uint(r.d), tag);
 }
 
+// h = silu(gate) * up of this workgroup's half-groups, then the Q8 of the
+// groups whose first half it holds.  False: the launch was aborted.
 template <int SPR, int IT, int D>
-__device__ __forceinline__ void tf_p_gu_run(TfPA& a, TfPL& L, const TfAct& x,
+__device__ __forceinline__ bool tf_p_gu_run(TfPA& a, TfPL& L, const TfAct& x,
                                             TfPGuRegs<IT> (&r)[D], unsigned long long* fh,
-                                            unsigned tag) {
+                                            unsigned tag, unsigned tag_x) {
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    constexpr int PS = TfPGuMap<SPR>::PASSES, JPW = TfPGuMap<SPR>::JPW;
-    const int owned = tf_p_gu_owned(a);
-    const int n_tasks = owned * PS;
+    constexpr int PH = TfPGuMap<SPR>::PH, JPW = TfPGuMap<SPR>::JPW;
+    const TfPGuSpan sp = tf_p_gu_span(a);
+    const int n_tasks = (sp.e - sp.s) * PH;
     const int wave = tf_p_tid() >> 6;
+    unsigned long long* fx = fh + a.F / 2;  // the exchange area, 16 words per group
+    const bool sends = (sp.s & 1) && sp.e > sp.s;  // half-group s is a second half
     for (int base = 0; base < n_tasks; base += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const int t = base + d;
             if (t >= n_tasks) break;  // wave-uniform
-            const int k = t / PS, pass = t % PS;
+            const int lh = t / PH, pass = t % PH;
+            float hv;
+            int i;
+            bool writer;
             if constexpr (SPR <= 8) {
                 float acc = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, t + D, n_tasks, r[d]);
+                tf_p_gu_load<SPR, IT>(a, L, sp, t + D, r[d]);
                 acc = tf_group_sum<4 * SPR>(acc);
                 const float other = __shfl(acc, (ln.lane + 4 * SPR) & 63, 64);
-                if ((ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0)
-                    tf_p_hbuf[k][4 * wave + JPW * pass + (ln.unit >> 1)] =
-                        (acc / (1.f + __expf(-acc))) * other;
+                hv = (acc / (1.f + __expf(-acc))) * other;
+                i = 2 * wave + JPW * pass + (ln.unit >> 1);
+                writer = (ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0;
             } else {
                 float g = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
                 float u = tf_q4k_row_partial<SPR, IT>(r[d].b, true, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, t + D, n_tasks, r[d]);
+                tf_p_gu_load<SPR, IT>(a, L, sp, t + D, r[d]);
                 g = tf_group_sum<64>(g);
                 u = tf_group_sum<64>(u);
-                if (ln.lane == 0) tf_p_hbuf[k][4 * wave + pass] = (g / (1.f + __expf(-g))) * u;
+                hv = (g / (1.f + __expf(-g))) * u;
+                i = 2 * wave + pass;
+                writer = ln.lane == 0;
+            }
+            if (writer) {
+                tf_p_hbuf[lh][i] = hv;
+                if (sends && lh == 0) tf_p_putf(fx + 16 * (sp.s >> 1) + i, hv, tag_x);
             }
         }
     }
+    // a group whose second half the next workgroup holds: read that half
+    const int last = sp.e - 1;
+    if (wave == 0 && sp.e > sp.s && (last & 1) == 0) {
+        const unsigned long long* src = fx + 16 * (last >> 1) + (ln.lane & 15);
+        unsigned long long w = tf_ldc64(src);
+        for (int spins = 0;;) {
+            if (!__builtin_amdgcn_ballot_w64((unsigned)(w >> 32) != tag_x)) break;
+            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                tf_p_abort(a);
+                tf_p_flag = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            w = tf_ldc64(src);
+        }
+        if (ln.lane < 16) tf_p_hbuf[sp.e - sp.s][ln.lane] = __uint_as_float((unsigned)w);
+    }
     __syncthreads();
-    if (wave == 0) {  // quad k quantizes owned group k
+    if (tf_p_flag) return false;
+    if (wave == 0) {  // quad k quantizes group g0 + k (values 8 j .. 8 j + 7)
+        const int g0 = (sp.s + 1) >> 1, ng = ((sp.e + 1) >> 1) - g0;
         const int k = ln.lane >> 2, j = ln.lane & 3;
-        const int kc = k < owned ? k : 0;
+        const int lh = k < ng ? 2 * (g0 + k) - sp.s + (j >> 1) : 0;
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[kc][8 * j + i];
+        for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[lh][8 * (j & 1) + i];
         const TfQ8Oct q = tf_q8_oct<false>(v);
-        if (k < owned) tf_p_put_oct(fh, blockIdx.x + k * gridDim.x, j, q, tag);
+        if (k < ng) tf_p_put_oct(fh, g0 + k, j, q, tag);
     }
+    return true;
 }
 
 // Polls a Q8 vector published as 9-word groups (tf_p_put_oct layout) into the
@@ -1066,61 +1113,68 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         tf_p_putf(pp + 3 + 2 * lane, o1, tp);
     }
     if (g.ws != 0 || !own) return true;
-    // wave `wave` merges head `wave`: lane = dims 2 lane, 2 lane + 1; splits
-    // in chunks of 8, every word of a chunk polled together
-    float M = TF_P_NEG_BIG, Lt = 0.f, A0 = 0.f, A1 = 0.f;
-    for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
-        unsigned long long wm[8], wl[8], w0[8], w1[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int sp = s0 + u < g.n_ws ? s0 + u : s0;
-            const unsigned long long* pp = tf_p_part(a, g.kh, wave, sp);
-            wm[u] = tf_ldc64(pp);
-            wl[u] = tf_ldc64(pp + 1);
-            w0[u] = tf_ldc64(pp + 2 + 2 * lane);
-            w1[u] = tf_ldc64(pp + 3 + 2 * lane);
-        }
+    // wave `wave` merges head `wave`: lane s holds split s's (m, l); lane =
+    // dims 2 lane, 2 lane + 1 for O; the O words of 8 splits are polled
+    // together.  M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O =
+    // sum_s w_s O_s (attn/flash.cu:222-255), the O sum in split order.
+    const unsigned long long* pbase = tf_p_part(a, g.kh, wave, 0);
+    constexpr size_t PS = 2 + HD;
+    float A0 = 0.f, A1 = 0.f, Lt = 0.f;
+    {
+        const int sl = lane < g.n_ws ? lane : 0;
+        unsigned long long wm = tf_ldc64(pbase + sl * PS), wl = tf_ldc64(pbase + sl * PS + 1);
         for (int spins = 0;;) {
-            bool miss = false;
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                miss |= (unsigned)(wm[u] >> 32) != tp || (unsigned)(wl[u] >> 32) != tp ||
-                        (unsigned)(w0[u] >> 32) != tp || (unsigned)(w1[u] >> 32) != tp;
+            const bool miss =
+                lane < g.n_ws && ((unsigned)(wm >> 32) != tp || (unsigned)(wl >> 32) != tp);
             if (!__builtin_amdgcn_ballot_w64(miss)) break;
             if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
                 tf_p_abort(a);
                 return true;  // the launch is aborted; outputs are not used
             }
             __builtin_amdgcn_s_sleep(4);
+            wm = tf_ldc64(pbase + sl * PS);
+            wl = tf_ldc64(pbase + sl * PS + 1);
+        }
+        const float ms = lane < g.n_ws ? __uint_as_float((unsigned)wm) : TF_P_NEG_BIG;
+        const float Mx = tf_wave_max(ms);
+        const float ws_ = lane < g.n_ws ? __expf(ms - Mx) : 0.f;
+        Lt = tf_group_sum<64>(ws_ * __uint_as_float((unsigned)wl));
+        for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
+            unsigned long long w0[8], w1[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int sp = s0 + u < g.n_ws ? s0 + u : s0;
-                const unsigned long long* pp = tf_p_part(a, g.kh, wave, sp);
-                wm[u] = tf_ldc64(pp);
-                wl[u] = tf_ldc64(pp + 1);
-                w0[u] = tf_ldc64(pp + 2 + 2 * lane);
-                w1[u] = tf_ldc64(pp + 3 + 2 * lane);
+                w0[u] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
+                w1[u] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
+            }
+            for (int spins = 0;;) {
+                bool miss = false;
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    miss |= s0 + u < g.n_ws &&
+                            ((unsigned)(w0[u] >> 32) != tp || (unsigned)(w1[u] >> 32) != tp);
+                if (!__builtin_amdgcn_ballot_w64(miss)) break;
+                if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                    tf_p_abort(a);
+                    return true;
+                }
+                __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int sp = s0 + u < g.n_ws ? s0 + u : s0;
+                    w0[u] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
+                    w1[u] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (s0 + u < g.n_ws) {  // wave-uniform
+                    const float w = tf_readlane(ws_, s0 + u);
+                    A0 = fmaf(w, __uint_as_float((unsigned)w0[u]), A0);
+                    A1 = fmaf(w, __uint_as_float((unsigned)w1[u]), A1);
+                }
             }
         }
-        // merge the chunk: M' = max(M, m_s); running sums rescaled to M'
-        float Mc = M;
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (s0 + u < g.n_ws) Mc = fmaxf(Mc, __uint_as_float((unsigned)wm[u]));
-        const float r0 = __expf(M - Mc);
-        Lt *= r0;
-        A0 *= r0;
-        A1 *= r0;
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            if (s0 + u < g.n_ws) {
-                const float w = __expf(__uint_as_float((unsigned)wm[u]) - Mc);
-                Lt = fmaf(w, __uint_as_float((unsigned)wl[u]), Lt);
-                A0 = fmaf(w, __uint_as_float((unsigned)w0[u]), A0);
-                A1 = fmaf(w, __uint_as_float((unsigned)w1[u]), A1);
-            }
-        }
-        M = Mc;
     }
     const float den = fmaxf(Lt, 1e-20f);
     tf_p_put_pair16(fo, og, lane & 15, A0 / den, A1 / den, to);
@@ -1287,9 +1341,9 @@ __device__ __noinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     TfPL& L = tf_p_layer(a, li);
     const int nbE = a.E / 256;
     const TfAct xE = tf_act_view(lds, nbE);
-    // the whole workload of a workgroup that owns two groups is in flight
-    // before the input poll (SPR <= 8: 8 tasks of one row per lane)
-    constexpr int D = SPR <= 8 ? 8 : 3;
+    // the whole workload of a workgroup with three half-groups is in flight
+    // before the input poll (SPR <= 8: 6 tasks of one row per lane)
+    constexpr int D = SPR <= 8 ? 6 : 3;
     TfPGuRegs<IT> rg[D];
     tf_p_gu_prefetch<SPR, IT, D>(a, L, rg);
     float nw[8];
@@ -1303,9 +1357,10 @@ __device__ __noinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     tf_p_stamp(a, 5 * li + 3, 1);
     tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
     tf_p_stamp(a, 5 * li + 3, 2);
-    tf_p_gu_run<SPR, IT, D>(a, L, xE, rg, tf_p_vec(a, TF_PK_H, li), tf_p_tag(tb, li, TF_PK_H));
+    const bool ok = tf_p_gu_run<SPR, IT, D>(a, L, xE, rg, tf_p_vec(a, TF_PK_H, li),
+                                            tf_p_tag(tb, li, TF_PK_H), tf_p_tag(tb, li, TF_PK_HX));
     tf_p_stamp(a, 5 * li + 3, 3);
-    return true;
+    return ok;
 }
 
 // Down projection: x_out = x_mid + W_down q8(h).
@@ -1481,6 +1536,8 @@ int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid
         return (int)hipErrorInvalidConfiguration;
     int grid = tf_device_cus();
     if (grid > TF_P_MAX_WG) grid = TF_P_MAX_WG;
+    // the LDS gather of h holds TF_P_MAX_HALVES_PER_WG half-groups
+    if ((a.F / 16 + grid - 1) / grid > TF_P_MAX_HALVES_PER_WG) return (int)hipErrorInvalidValue;
     if (grid_out) *grid_out = grid;
     if (lds_out) *lds_out = lds;
     if (!l) return 0;
