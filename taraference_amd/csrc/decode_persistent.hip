@@ -162,9 +162,19 @@ __device__ __forceinline__ void tf_p_abort(TfPA& a) {
 
 // Stage timeline (diagnostics): stage k of this workgroup started (0), had
 // its activation staged (2) and finished (3).
+// The stamps collect in LDS (a global store here would hold up the wave's
+// next memory wait) and are copied out at the end of the launch.
+__shared__ unsigned long long tf_p_tstamp[(5 * TF_P_MAX_LAYERS + 1) * 4];
+
 __device__ __forceinline__ void tf_p_stamp(TfPA& a, int k, int which) {
-    if (a.trace && tf_p_tid() == 0)
-        a.trace[((size_t)k * gridDim.x + blockIdx.x) * 4 + which] = __builtin_amdgcn_s_memrealtime();
+    if (a.trace && tf_p_tid() == 0) tf_p_tstamp[k * 4 + which] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void tf_p_trace_flush(TfPA& a) {
+    if (!a.trace) return;
+    __syncthreads();
+    for (int i = tf_p_tid(); i < (5 * a.n_layer + 1) * 4; i += TF_P_THREADS)
+        a.trace[((size_t)(i >> 2) * gridDim.x + blockIdx.x) * 4 + (i & 3)] = tf_p_tstamp[i];
 }
 
 // dst(i, bits) for i < n once word i of src carries `tag`; threads r, r + R,
@@ -173,10 +183,11 @@ __device__ __forceinline__ void tf_p_stamp(TfPA& a, int k, int which) {
 // passes are unrolled and every load is issued unconditionally (past-the-end
 // words reload word 0): a load under a branch, or a loop back edge, makes
 // the compiler drain all loads in flight (the weight prefetch included)
-// before issuing the next one.  Must be called by every thread of the
+// before issuing the next one.  WG: must be called by every thread of the
 // workgroup; returns false (everywhere) if the wait timed out or the launch
-// was aborted.
-template <int K, int P, class Dst>
+// was aborted.  !WG: called by the R threads alone, no barrier; a time-out
+// or abort sets tf_p_flag, which the caller reads after its next barrier.
+template <int K, int P, class Dst, bool WG = true>
 __device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src, int n,
                                           unsigned tag, int rank, int R, TfPA& a) {
     int bad = n > K * R * P;
@@ -215,6 +226,7 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src
         tf_p_abort(a);
         tf_p_flag = 1;
     }
+    if constexpr (!WG) return !bad;
     __syncthreads();
     const bool ok = tf_p_flag == 0;
     __syncthreads();
@@ -299,7 +311,7 @@ template <bool F32, bool NORM>
 __device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* src, float scale,
                                             const float (&w)[8]) {
     int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
+    float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
     float* dss = d8s + nb * 8;
     int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
     float* xf = reinterpret_cast<float*>(s16 + nb * 16);
@@ -325,7 +337,7 @@ __device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* s
                 lo |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
                 hi |= (uint32_t)(r.q[4 + i] & 0xff) << (8 * i);
             }
-            *reinterpret_cast<uint2*>(q8s + e) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(q8s + tf_q8_pad(e)) = make_uint2(lo, hi);
             if ((j & 1) == 0) {
                 s16[2 * g + (j >> 1)] = r.s_half;
                 if (F32) xs16[2 * g + (j >> 1)] = r.f_half;
@@ -703,10 +715,13 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 // reads them.  Published group g: words 9 g .. 9 g + 7 hold the 32 Q8 bytes
 // (little-endian, 4 per word), word 9 g + 8 the scale d8.
 
-// Half-groups per workgroup the LDS gather holds (one more slot takes a
-// split group's second half).
-#define TF_P_MAX_HALVES_PER_WG 7
-__shared__ float tf_p_hbuf[TF_P_MAX_HALVES_PER_WG + 1][16];
+// Wave 0 of a workgroup polls the stage's input; the other waves (the
+// compute waves) own the GEMV tasks.  A wave's memory counter completes in
+// issue order, so a poll issued behind a weight prefetch would also wait for
+// all of that prefetch; with the roles split the input is staged as soon as
+// it arrives, and each compute wave then consumes its tasks one by one as
+// their weights land.
+#define TF_P_CW (TF_P_WAVES - 1)
 
 template <int IT>
 struct TfPGuRegs {
@@ -715,10 +730,17 @@ struct TfPGuRegs {
 
 template <int SPR>
 struct TfPGuMap {
-    static constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;  // outputs per pass
-    static constexpr int PH = 2 / JPW;                      // passes per half-group
+    static constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;  // outputs per task
+    static constexpr int HMAX = SPR <= 8 ? 3 : 5;            // half-groups per workgroup
+    // tasks per compute wave, and register sets in flight
+    static constexpr int K = (16 * HMAX + TF_P_CW * JPW - 1) / (TF_P_CW * JPW);
+    static constexpr int D = SPR <= 8 ? K : 4;
     static_assert(JPW >= 1 && JPW <= 2, "gate/up lane map needs SPR >= 4");
 };
+
+// LDS gather of h: the outputs of the workgroup's half-groups, then (one more
+// half-group) the second half of a split group.
+__shared__ float tf_p_hbuf[6 * 16];
 
 // Half-groups [s, e) of this workgroup.
 struct TfPGuSpan {
@@ -730,39 +752,30 @@ __device__ __forceinline__ TfPGuSpan tf_p_gu_span(TfPA& a) {
     return {(int)((long long)nh * b / G), (int)((long long)nh * (b + 1) / G)};
 }
 
-// Output row of pass p of half-group h for this wave's lane unit.
+// Output (index into the workgroup's outputs, 16 s + o is the row) of task q
+// of compute wave cw, for this lane's unit.
 template <int SPR>
-__device__ __forceinline__ int tf_p_gu_j(int h, int p, int unit) {
-    const int wave = tf_p_tid() >> 6;
-    if constexpr (SPR <= 8)
-        return 16 * h + 2 * wave + TfPGuMap<SPR>::JPW * p + (unit >> 1);
-    else
-        return 16 * h + 2 * wave + p;
+__device__ __forceinline__ int tf_p_gu_out(int cw, int q, int unit) {
+    const int u = cw + TF_P_CW * q;
+    if constexpr (SPR <= 8) return u * TfPGuMap<SPR>::JPW + (unit >> 1);
+    else return u;
 }
 
-// Task t of this wave: half-group s + t / PH, pass t % PH.
+// Weights of task q (unconditional; an output past the span loads row j0).
 template <int SPR, int IT>
-__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, const TfPGuSpan& sp, int t,
+__device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int n_out, int j0, int q,
                                              TfPGuRegs<IT>& r) {
-    constexpr int PH = TfPGuMap<SPR>::PH;
-    if (t >= (sp.e - sp.s) * PH) return;
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    const int j = tf_p_gu_j<SPR>(sp.s + t / PH, t % PH, ln.unit);
+    const int o = tf_p_gu_out<SPR>((tf_p_tid() >> 6) - 1, q, ln.unit);
+    const int j = j0 + (o < n_out ? o : 0);
     if constexpr (SPR <= 8) {
         const uint8_t* w = (ln.unit & 1) ? L.up : L.gate;
-        tf_q4k_row_load<SPR, IT>(w + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
+        tf_q4k_row_load_u<SPR, IT>(w + (size_t)j * L.cb_gu, nb, ln.sir, ln.t, r.a);
     } else {
-        tf_q4k_row_load<SPR, IT>(L.gate + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.a);
-        tf_q4k_row_load<SPR, IT>(L.up + (size_t)j * L.cb_gu, true, 0, nb, ln.sir, ln.t, r.b);
+        tf_q4k_row_load_u<SPR, IT>(L.gate + (size_t)j * L.cb_gu, nb, ln.sir, ln.t, r.a);
+        tf_q4k_row_load_u<SPR, IT>(L.up + (size_t)j * L.cb_gu, nb, ln.sir, ln.t, r.b);
     }
-}
-
-template <int SPR, int IT, int D>
-__device__ __forceinline__ void tf_p_gu_prefetch(TfPA& a, TfPL& L, TfPGuRegs<IT> (&r)[D]) {
-    const TfPGuSpan sp = tf_p_gu_span(a);
-#pragma unroll
-    for (int d = 0; d < D; d++) tf_p_gu_load<SPR, IT>(a, L, sp, d, r[d]);
 }
 
 // Publishes the Q8 of one 32-value group held as 8 values per lane of a
@@ -780,83 +793,83 @@ __device__ __forceinline__ void tf_p_put_oct(unsigned long long* dst, int g, int
     if (j == 0) tf_p_put(dst + 9 * g + 8, __float_as_uint(r.d), tag);
 }
 
-// h = silu(gate) * up of this workgroup's half-groups, then the Q8 of the
-// groups whose first half it holds.  False: the launch was aborted.
-template <int SPR, int IT, int D>
-__device__ __forceinline__ bool tf_p_gu_run(TfPA& a, TfPL& L, const TfAct& x,
-                                            TfPGuRegs<IT> (&r)[D], unsigned long long* fh,
-                                            unsigned tag, unsigned tag_x) {
+// Compute-wave part of gate/up: h = silu(gate) * up of this wave's outputs
+// into tf_p_hbuf (and, for the first half-group when it is the second half
+// of a group, into the exchange area).  r holds tasks 0 .. D - 1 on entry.
+template <int SPR, int IT>
+__device__ __forceinline__ void tf_p_gu_compute(TfPA& a, TfPL& L, const TfAct& x,
+                                                TfPGuRegs<IT> (&r)[TfPGuMap<SPR>::D],
+                                                const TfPGuSpan& sp, unsigned long long* fx,
+                                                unsigned tag_x) {
+    using M = TfPGuMap<SPR>;
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    constexpr int PH = TfPGuMap<SPR>::PH, JPW = TfPGuMap<SPR>::JPW;
-    const TfPGuSpan sp = tf_p_gu_span(a);
-    const int n_tasks = (sp.e - sp.s) * PH;
-    const int wave = tf_p_tid() >> 6;
-    unsigned long long* fx = fh + a.F / 2;  // the exchange area, 16 words per group
-    const bool sends = (sp.s & 1) && sp.e > sp.s;  // half-group s is a second half
-    for (int base = 0; base < n_tasks; base += D) {
+    const int cw = (tf_p_tid() >> 6) - 1;
+    const int n_out = 16 * (sp.e - sp.s);
+    const int j0 = 16 * sp.s < a.F ? 16 * sp.s : 0;
+    const bool sends = (sp.s & 1) && n_out > 0;  // half-group s is a second half
 #pragma unroll
-        for (int d = 0; d < D; d++) {
-            const int t = base + d;
-            if (t >= n_tasks) break;  // wave-uniform
-            const int lh = t / PH, pass = t % PH;
-            float hv;
-            int i;
-            bool writer;
-            if constexpr (SPR <= 8) {
-                float acc = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, sp, t + D, r[d]);
-                acc = tf_group_sum<4 * SPR>(acc);
-                const float other = __shfl(acc, (ln.lane + 4 * SPR) & 63, 64);
-                hv = (acc / (1.f + __expf(-acc))) * other;
-                i = 2 * wave + JPW * pass + (ln.unit >> 1);
-                writer = (ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0;
-            } else {
-                float g = tf_q4k_row_partial<SPR, IT>(r[d].a, true, 0, nb, ln.sir, ln.t, x);
-                float u = tf_q4k_row_partial<SPR, IT>(r[d].b, true, 0, nb, ln.sir, ln.t, x);
-                tf_p_gu_load<SPR, IT>(a, L, sp, t + D, r[d]);
-                g = tf_group_sum<64>(g);
-                u = tf_group_sum<64>(u);
-                hv = (g / (1.f + __expf(-g))) * u;
-                i = 2 * wave + pass;
-                writer = ln.lane == 0;
-            }
-            if (writer) {
-                tf_p_hbuf[lh][i] = hv;
-                if (sends && lh == 0) tf_p_putf(fx + 16 * (sp.s >> 1) + i, hv, tag_x);
-            }
+    for (int q = 0; q < M::K; q++) {
+        TfPGuRegs<IT>& rq = r[q % M::D];
+        const int o = tf_p_gu_out<SPR>(cw, q, ln.unit);
+        float hv;
+        bool writer;
+        if constexpr (SPR <= 8) {
+            float acc = tf_q4k_row_partial<SPR, IT>(rq.a, true, 0, nb, ln.sir, ln.t, x);
+            if (q + M::D < M::K) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, q + M::D, rq);
+            acc = tf_group_sum<4 * SPR>(acc);
+            const float other = __shfl(acc, (ln.lane + 4 * SPR) & 63, 64);
+            hv = (acc / (1.f + __expf(-acc))) * other;
+            writer = (ln.unit & 1) == 0 && (ln.lane & (4 * SPR - 1)) == 0;
+        } else {
+            float g = tf_q4k_row_partial<SPR, IT>(rq.a, true, 0, nb, ln.sir, ln.t, x);
+            float u = tf_q4k_row_partial<SPR, IT>(rq.b, true, 0, nb, ln.sir, ln.t, x);
+            if (q + M::D < M::K) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, q + M::D, rq);
+            g = tf_group_sum<64>(g);
+            u = tf_group_sum<64>(u);
+            hv = (g / (1.f + __expf(-g))) * u;
+            writer = ln.lane == 0;
+        }
+        if (writer && o < n_out) {
+            tf_p_hbuf[o] = hv;
+            if (sends && o < 16) tf_p_putf(fx + 16 * (sp.s >> 1) + o, hv, tag_x);
         }
     }
-    // a group whose second half the next workgroup holds: read that half
-    const int last = sp.e - 1;
-    if (wave == 0 && sp.e > sp.s && (last & 1) == 0) {
-        const unsigned long long* src = fx + 16 * (last >> 1) + (ln.lane & 15);
-        unsigned long long w = tf_ldc64(src);
-        for (int spins = 0;;) {
-            if (!__builtin_amdgcn_ballot_w64((unsigned)(w >> 32) != tag_x)) break;
-            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
-                tf_p_abort(a);
-                tf_p_flag = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-            w = tf_ldc64(src);
+}
+
+// Wave 0 of gate/up, after the compute: reads the second half of a group
+// whose first half ends this workgroup's span, then (after the workgroup
+// barrier) quantizes the groups whose first half it holds.  False: aborted.
+__device__ __forceinline__ void tf_p_gu_exchange(TfPA& a, const TfPGuSpan& sp,
+                                                 const unsigned long long* fx, unsigned tag_x) {
+    const int lane = tf_p_tid() & 63, last = sp.e - 1;
+    if (sp.e <= sp.s || (last & 1)) return;
+    const unsigned long long* src = fx + 16 * (last >> 1) + (lane & 15);
+    unsigned long long w = tf_ldc64(src);
+    for (int spins = 0;;) {
+        if (!__builtin_amdgcn_ballot_w64((unsigned)(w >> 32) != tag_x)) break;
+        if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+            tf_p_abort(a);
+            tf_p_flag = 1;
+            break;
         }
-        if (ln.lane < 16) tf_p_hbuf[sp.e - sp.s][ln.lane] = __uint_as_float((unsigned)w);
+        __builtin_amdgcn_s_sleep(2);
+        w = tf_ldc64(src);
     }
-    __syncthreads();
-    if (tf_p_flag) return false;
-    if (wave == 0) {  // quad k quantizes group g0 + k (values 8 j .. 8 j + 7)
-        const int g0 = (sp.s + 1) >> 1, ng = ((sp.e + 1) >> 1) - g0;
-        const int k = ln.lane >> 2, j = ln.lane & 3;
-        const int lh = k < ng ? 2 * (g0 + k) - sp.s + (j >> 1) : 0;
-        float v[8];
+    if (lane < 16) tf_p_hbuf[16 * (sp.e - sp.s) + lane] = __uint_as_float((unsigned)w);
+}
+
+__device__ __forceinline__ void tf_p_gu_quantize(const TfPGuSpan& sp, unsigned long long* fh,
+                                                 unsigned tag) {
+    const int lane = tf_p_tid() & 63;
+    const int g0 = (sp.s + 1) >> 1, ng = ((sp.e + 1) >> 1) - g0;
+    const int k = lane >> 2, j = lane & 3;  // quad k: group g0 + k, values 8 j .. 8 j + 7
+    const int o = k < ng ? 16 * (2 * (g0 + k) - sp.s) + 8 * j : 0;
+    float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[lh][8 * (j & 1) + i];
-        const TfQ8Oct q = tf_q8_oct<false>(v);
-        if (k < ng) tf_p_put_oct(fh, g0 + k, j, q, tag);
-    }
-    return true;
+    for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[o + i];
+    const TfQ8Oct q = tf_q8_oct<false>(v);
+    if (k < ng) tf_p_put_oct(fh, g0 + k, j, q, tag);
 }
 
 // Polls a Q8 vector published as 9-word groups (tf_p_put_oct layout) into the
@@ -866,21 +879,22 @@ template <int K>
 __device__ __forceinline__ bool tf_p_poll_q8img(TfPA& a, uint8_t* lds, int nb,
                                                 const unsigned long long* src, unsigned tag) {
     uint32_t* q8w = reinterpret_cast<uint32_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
+    float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
     float* dss = d8s + nb * 8;
     int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
     const int ng = nb * 8;
     if (!tf_p_poll<K, 1>(
             [&](int i, uint32_t b) {
                 const int g = i / 9, w = i - 9 * g;
-                if (w < 8) q8w[8 * g + w] = b;
+                if (w < 8) q8w[(tf_q8_pad(32 * g) >> 2) + w] = b;
                 else d8s[g] = __uint_as_float(b);
             },
             src, 9 * ng, tag, tf_p_tid(), TF_P_THREADS, a))
         return false;
     for (int g = tf_p_tid(); g < ng; g += TF_P_THREADS) {
-        const tf_u32x4 u0 = *reinterpret_cast<const tf_u32x4*>(q8w + 8 * g);
-        const tf_u32x4 u1 = *reinterpret_cast<const tf_u32x4*>(q8w + 8 * g + 4);
+        const uint32_t* gw = q8w + (tf_q8_pad(32 * g) >> 2);
+        const tf_u32x4 u0 = *reinterpret_cast<const tf_u32x4*>(gw);
+        const tf_u32x4 u1 = *reinterpret_cast<const tf_u32x4*>(gw + 4);
         const int one = 0x01010101;
         int sa = tf_dot4(one, (int)u0.x, 0);
         sa = tf_dot4(one, (int)u0.y, sa);
@@ -1215,7 +1229,7 @@ __device__ __forceinline__ bool tf_p_poll_xf(TfPA& a, float* xf, const unsigned 
 
 // Layer li's norm + QKV + RoPE + K/V append.
 template <int SPR, int IT>
-__device__ __noinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int pos, int token) {
+__device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int pos, int token) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
@@ -1277,7 +1291,7 @@ __device__ __forceinline__ void tf_p_warm(TfPA& a, TfPL& L, int idle_rank, int n
     asm volatile("" ::"v"(acc));
 }
 
-__device__ __noinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
+__device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
@@ -1312,7 +1326,7 @@ __device__ __forceinline__ float tf_p_res_in(TfPA& a, int li, unsigned tb, int t
 }
 
 template <int SPR, int IT>
-__device__ __noinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int token) {
+__device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int token) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
@@ -1335,32 +1349,55 @@ __device__ __noinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int to
 }
 
 template <int SPR, int IT>
-__device__ __noinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
+__device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
+    using M = TfPGuMap<SPR>;
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     const int nbE = a.E / 256;
     const TfAct xE = tf_act_view(lds, nbE);
-    // the whole workload of a workgroup with three half-groups is in flight
-    // before the input poll (SPR <= 8: 6 tasks of one row per lane)
-    constexpr int D = SPR <= 8 ? 6 : 3;
-    TfPGuRegs<IT> rg[D];
-    tf_p_gu_prefetch<SPR, IT, D>(a, L, rg);
+    const int wave = tf_p_tid() >> 6;
+    const TfPGuSpan sp = tf_p_gu_span(a);
+    unsigned long long* fh = tf_p_vec(a, TF_PK_H, li);
+    unsigned long long* fx = fh + a.F / 2;  // the exchange area, 16 words per group
+    const unsigned tag_x = tf_p_tag(tb, li, TF_PK_HX);
+    float* raw = tf_p_raw(lds, nbE);
+    // the norm weights first: waiting for them does not wait for the weights
     float nw[8];
     tf_p_norm_wload(L.ffn_norm, a.E, nw);
-    float* raw = tf_p_raw(lds, nbE);
-    tf_p_stamp(a, 5 * li + 3, 0);
-    __syncthreads();  // the previous stage's LDS readers are done
-    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
-            a, raw, tf_p_vec(a, TF_PK_XA, li), a.E, tf_p_tag(tb, li, TF_PK_XA)))
-        return false;
-    tf_p_stamp(a, 5 * li + 3, 1);
-    tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
-    tf_p_stamp(a, 5 * li + 3, 2);
-    const bool ok = tf_p_gu_run<SPR, IT, D>(a, L, xE, rg, tf_p_vec(a, TF_PK_H, li),
-                                            tf_p_tag(tb, li, TF_PK_H), tf_p_tag(tb, li, TF_PK_HX));
-    tf_p_stamp(a, 5 * li + 3, 3);
-    return ok;
+    if (wave == 0) {
+        tf_p_stamp(a, 5 * li + 3, 0);
+        __syncthreads();  // the previous stage's LDS readers are done
+        auto put = [&](int i, uint32_t b) { raw[i] = __uint_as_float(b); };
+        // E <= 256 SPR: 4 SPR words per lane, in passes of up to 32
+        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
+        tf_p_poll<PK, PP, decltype(put), false>(
+            put, tf_p_vec(a, TF_PK_XA, li), a.E, tf_p_tag(tb, li, TF_PK_XA), tf_p_tid() & 63, 64, a);
+        tf_p_stamp(a, 5 * li + 3, 1);
+        __syncthreads();  // raw row in LDS
+        if (tf_p_flag) return false;
+        tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+        tf_p_stamp(a, 5 * li + 3, 2);
+        tf_p_gu_exchange(a, sp, fx, tag_x);
+        __syncthreads();  // h of every compute wave in LDS
+        if (tf_p_flag) return false;
+        tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H));
+        tf_p_stamp(a, 5 * li + 3, 3);
+    } else {
+        const int n_out = 16 * (sp.e - sp.s);
+        const int j0 = 16 * sp.s < a.F ? 16 * sp.s : 0;
+        TfPGuRegs<IT> rg[M::D];
+#pragma unroll
+        for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
+        __syncthreads();  // the previous stage's LDS readers are done
+        __syncthreads();  // raw row in LDS
+        if (tf_p_flag) return false;
+        tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+        tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
+        __syncthreads();  // h of every compute wave in LDS
+        if (tf_p_flag) return false;
+    }
+    return true;
 }
 
 // Down projection: x_out = x_mid + W_down q8(h).
@@ -1389,7 +1426,7 @@ __device__ __forceinline__ bool tf_p_down_body(TfPA& a, TfPL& L, int li, unsigne
 }
 
 template <int SPR, int IT>
-__device__ __noinline__ bool tf_p_stage_down(TfPA* pa, int li, unsigned tb) {
+__device__ __forceinline__ bool tf_p_stage_down(TfPA* pa, int li, unsigned tb) {
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     if (L.down_q6k) return tf_p_down_body<SPR, IT, true>(a, L, li, tb);
@@ -1401,7 +1438,7 @@ __device__ __noinline__ bool tf_p_stage_down(TfPA* pa, int li, unsigned tb) {
 __shared__ unsigned long long tf_p_key[TF_P_WAVES];
 
 template <int SPR, int IT>
-__device__ __noinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_mode, int pos,
+__device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_mode, int pos,
                                              unsigned gen) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
@@ -1479,6 +1516,8 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
         for (int i = tid; i < nl * (int)(sizeof(TfPLayer) / 4); i += TF_P_THREADS)
             ldst[i] = tf_gld(lsrc + i);
         if (tid == 0) tf_p_flag = 0;
+        if (tf_gld(&args->trace))
+            for (int i = tid; i < (5 * nl + 1) * 4; i += TF_P_THREADS) tf_p_tstamp[i] = 0;
         __syncthreads();
     }
     TfPA& a = *(TfPA*)&tf_p_args;
@@ -1495,6 +1534,7 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
         if (!tf_p_stage_down<SPR_F, IT_F>(&a, li, tb)) return;
     }
     tf_p_stage_head<SPR_E, IT_E>(&a, tb, host_mode, pos, gen);
+    tf_p_trace_flush(a);
 }
 
 // ------------------------------------------------------------ host side
@@ -1536,8 +1576,8 @@ int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid
         return (int)hipErrorInvalidConfiguration;
     int grid = tf_device_cus();
     if (grid > TF_P_MAX_WG) grid = TF_P_MAX_WG;
-    // the LDS gather of h holds TF_P_MAX_HALVES_PER_WG half-groups
-    if ((a.F / 16 + grid - 1) / grid > TF_P_MAX_HALVES_PER_WG) return (int)hipErrorInvalidValue;
+    // the gate/up task tables hold TfPGuMap<SE>::HMAX half-groups per workgroup
+    if ((a.F / 16 + grid - 1) / grid > TfPGuMap<SE>::HMAX) return (int)hipErrorInvalidValue;
     if (grid_out) *grid_out = grid;
     if (lds_out) *lds_out = lds;
     if (!l) return 0;

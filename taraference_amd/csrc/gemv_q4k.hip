@@ -241,14 +241,14 @@ __global__ __launch_bounds__(256) void tf_q4k_block_dots_kernel(
     int32_t* __restrict__ dots, int32_t* __restrict__ sums, int nb, int n_cols,
     int col_bytes) {
     extern __shared__ __align__(16) uint8_t lds[];
-    int32_t* lsums = reinterpret_cast<int32_t*>(lds + nb * 256);
+    int32_t* lsums = reinterpret_cast<int32_t*>(lds + TF_Q8_LDS_BYTES(nb));
     // Same copy-and-sum as tf_stage_act(TF_SRC_Q8); only the integer sums are kept.
     {
         int8_t* q8s = reinterpret_cast<int8_t*>(lds);
         for (int g = threadIdx.x; g < nb * 8; g += blockDim.x) {
             tf_u32x4 a = tf_ld16(xq + g * 32), b = tf_ld16(xq + g * 32 + 16);
-            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[0] = a;
-            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[1] = b;
+            reinterpret_cast<tf_u32x4*>(q8s + tf_q8_pad(g * 32))[0] = a;
+            reinterpret_cast<tf_u32x4*>(q8s + tf_q8_pad(g * 32))[1] = b;
             const int one = 0x01010101;
             int s = tf_dot4(one, (int)a.x, 0);
             s = tf_dot4(one, (int)a.y, s);
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void tf_q4k_block_dots_kernel(
     TfQ4kPart p;
     tf_q4k_load(w + (size_t)j * col_bytes + (size_t)sb * 144, t, p);
     int dlo, dhi;
-    tf_q4k_idots(p, q8s + sb * 256 + 64 * t, dlo, dhi);
+    tf_q4k_idots(p, q8s + tf_q8_pad(sb * 256 + 64 * t), dlo, dhi);
     const size_t o = ((size_t)j * nb + sb) * 8 + 2 * t;
     dots[o] = dlo;
     dots[o + 1] = dhi;
@@ -513,7 +513,7 @@ extern "C" int tf_q4k_block_dots(const uint8_t* w, const int8_t* xq, int32_t* do
     TF_CHECK_ARG(nb > 0 && n_cols > 0 && tf_q4k_weights_ok(w, nb, col_bytes));
     TF_CHECK_ARG(xq && ((uintptr_t)xq & 15) == 0 && dots && sums);
     const long long total = (long long)n_cols * nb * 4;
-    const int lds = nb * 256 + nb * 8 * 4;
+    const int lds = TF_Q8_LDS_BYTES(nb) + nb * 8 * 4;
     hipLaunchKernelGGL(tf_q4k_block_dots_kernel, dim3((unsigned)((total + 255) / 256)),
                        dim3(256), lds, tf_stream(stream), w, xq, dots, sums, nb, n_cols,
                        col_bytes);

@@ -166,10 +166,10 @@ __global__ __launch_bounds__(256) void tf_q6k_block_dots_kernel(
     extern __shared__ __align__(16) uint8_t lds[];
     // stage only the bytes and 16-value sums (d8 is not part of the integer stage)
     int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    int32_t* s16 = reinterpret_cast<int32_t*>(lds + nb * 256);
+    int32_t* s16 = reinterpret_cast<int32_t*>(lds + TF_Q8_LDS_BYTES(nb));
     for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
         const tf_u32x4 a = tf_ld16(xq + i * 16);
-        reinterpret_cast<tf_u32x4*>(q8s)[i] = a;
+        *reinterpret_cast<tf_u32x4*>(q8s + tf_q8_pad(16 * i)) = a;
         const int one = 0x01010101;
         int s = tf_dot4(one, (int)a.x, 0);
         s = tf_dot4(one, (int)a.y, s);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void tf_q6k_block_dots_kernel(
     if (BLOCK_BYTES == 212) tf_q6k_load_c(base, p, q);
     else tf_q6k_load_r(base, p, q);
     int idot[4];
-    tf_q6k_idots(q, p, q8s + sb * 256, s16 + sb * 16, idot);
+    tf_q6k_idots(q, p, q8s + sb * 320, s16 + sb * 16, idot);
     const int n = p >> 1, h = p & 1;
     for (int k = 0; k < 4; k++) dots[((size_t)j * nb + sb) * 16 + 8 * n + 2 * k + h] = idot[k];
 }
@@ -346,7 +346,7 @@ extern "C" int tf_q6k_block_dots(const uint8_t* w, int block_bytes, const int8_t
     if (block_bytes == 212) TF_CHECK_ARG(tf_q6c_weights_ok(w, nb, col_bytes));
     else TF_CHECK_ARG(((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
     const long long total = (long long)n_cols * nb * 4;
-    const int lds = nb * 256 + nb * 64;
+    const int lds = TF_Q8_LDS_BYTES(nb) + nb * 64;
     const dim3 grid((unsigned)((total + 255) / 256));
     if (block_bytes == 212)
         hipLaunchKernelGGL(tf_q6k_block_dots_kernel<212>, grid, dim3(256), lds,

@@ -52,7 +52,8 @@ __device__ __forceinline__ void tf_q4k_scales(const tf_u32x4& h, int t, int& sc0
 }
 
 // Exact integer stage: dlo = sum q4*q8 over sub-block 2t, dhi over 2t+1.
-// q8g points at the 64 LDS bytes of groups 2t, 2t+1 of this super-block.
+// q8g points at the 64 LDS bytes of groups 2t, 2t+1 of this super-block
+// (contiguous in the padded image too: the run is 64-byte aligned).
 __device__ __forceinline__ void tf_q4k_idots(const TfQ4kPart& p, const int8_t* q8g,
                                              int& dlo, int& dhi) {
     const tf_u32x4* qv = reinterpret_cast<const tf_u32x4*>(q8g);
@@ -82,7 +83,7 @@ __device__ __forceinline__ void tf_q4k_idots(const TfQ4kPart& p, const int8_t* q
 __device__ __forceinline__ float tf_q4k_part_dot(const TfQ4kPart& p, int t, int sb,
                                                  const TfQ8Lds& x) {
     int dlo, dhi;
-    tf_q4k_idots(p, x.q8 + sb * 256 + 64 * t, dlo, dhi);
+    tf_q4k_idots(p, x.q8 + tf_q8_pad(sb * 256 + 64 * t), dlo, dhi);
     int sc0, sc1, m0, m1;
     tf_q4k_scales(p.h, t, sc0, sc1, m0, m1);
     const float d = tf_h2f(p.h.x);
@@ -112,6 +113,19 @@ __device__ __forceinline__ void tf_q4k_row_load(const uint8_t* __restrict__ col,
     for (int i = 0; i < ITERS; i++) {
         const int sb = sb0 + sir + i * SPR;
         if (valid && sb < sb1) tf_q4k_load(col + (size_t)sb * 144, t, r.p[i]);
+    }
+}
+
+// The same loads issued unconditionally (a super-block past the row reloads
+// super-block 0; tf_q4k_row_partial skips it): no branch around the loads,
+// so the compiler can wait for exactly the loads a computation needs.
+template <int SPR, int ITERS>
+__device__ __forceinline__ void tf_q4k_row_load_u(const uint8_t* __restrict__ col, int nb,
+                                                  int sir, int t, TfQ4kRow<ITERS>& r) {
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sir + i * SPR;
+        tf_q4k_load(col + (size_t)(sb < nb ? sb : 0) * 144, t, r.p[i]);
     }
 }
 

@@ -78,7 +78,8 @@ __device__ __forceinline__ int tf_q6k_scale(const TfQ6kPart& q, int p, int k) {
 }
 
 // Exact integer stage: idot[k] = sum (q6 - 32) * q8 over scale group
-// 8n + 2k + h.  q8sb points at the 256 LDS Q8 bytes of the super-block and
+// 8n + 2k + h.  q8sb points at the super-block's Q8 bytes in the padded LDS
+// image (value byte o at q8sb + tf_q8_pad(o)) and
 // s16 at its 16 per-16-value q8 sums.
 __device__ __forceinline__ void tf_q6k_idots(const TfQ6kPart& q, int p, const int8_t* q8sb,
                                              const int32_t* s16, int idot[4]) {
@@ -86,7 +87,7 @@ __device__ __forceinline__ void tf_q6k_idots(const TfQ6kPart& q, int p, const in
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const tf_u32x4 u =
-            *reinterpret_cast<const tf_u32x4*>(q8sb + 128 * n + 32 * k + 16 * h);
+            *reinterpret_cast<const tf_u32x4*>(q8sb + tf_q8_pad(128 * n + 32 * k + 16 * h));
         int s = tf_dot4((int)tf_q6k_word(q, k, 0), (int)u.x, 0);
         s = tf_dot4((int)tf_q6k_word(q, k, 1), (int)u.y, s);
         s = tf_dot4((int)tf_q6k_word(q, k, 2), (int)u.z, s);
@@ -103,7 +104,7 @@ using TfQ6Lds = TfAct;
 __device__ __forceinline__ float tf_q6k_part_dot(const TfQ6kPart& q, int p, int sb,
                                                  const TfQ6Lds& x) {
     int idot[4];
-    tf_q6k_idots(q, p, x.q8 + sb * 256, x.s16 + sb * 16, idot);
+    tf_q6k_idots(q, p, x.q8 + sb * 320, x.s16 + sb * 16, idot);
     const int n = p >> 1;
     const float d = tf_h2f(q.d);
     const float4 d8 = *reinterpret_cast<const float4*>(x.d8 + sb * 8 + 4 * n);

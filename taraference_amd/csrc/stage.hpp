@@ -10,13 +10,19 @@
 // separate kernels would.
 //
 // LDS image for nb super-blocks (G = 8*nb groups of 32 values):
-//   q8[256*nb] int8 | d8[G] f32 | ds[G] f32 = d8*sum32(q8) |
+//   q8[320*nb] int8 | d8[G] f32 | ds[G] f32 = d8*sum32(q8) |
 //   s16[2G] i32 = per-16 sums of q8 | (optional) xf[256*nb] f32 normalized
 //   activation | xs16[2G] f32 = per-16 sums of xf
 // The Q4_K x Q8 path reads q8/d8/ds, the Q6_K x Q8 path q8/d8/s16 and the
 // Q6_K x f32 path xf/xs16.
+// The q8 bytes are padded: value byte o sits at tf_q8_pad(o), 16 bytes of gap
+// after every 64, so the GEMV lanes that each read a 64-byte run (lane stride
+// 64 B) fall on distinct LDS banks instead of four to a bank.
 #pragma once
 #include "tf_common.hpp"
+
+__host__ __device__ constexpr int tf_q8_pad(int o) { return o + ((o >> 6) << 4); }
+#define TF_Q8_LDS_BYTES(nb) ((nb) * 320)
 
 enum TfSrc { TF_SRC_Q8 = 0, TF_SRC_F32 = 1, TF_SRC_NORM = 2, TF_SRC_FLASH = 3 };
 
@@ -33,13 +39,14 @@ struct TfAct {
 };
 
 __host__ __device__ constexpr int tf_act_lds_bytes(int nb, bool with_f32) {
-    return nb * 256 + nb * 8 * 4 * 2 + nb * 16 * 4 + (with_f32 ? nb * 256 * 4 + nb * 16 * 4 : 0);
+    return TF_Q8_LDS_BYTES(nb) + nb * 8 * 4 * 2 + nb * 16 * 4 +
+           (with_f32 ? nb * 256 * 4 + nb * 16 * 4 : 0);
 }
 
 __device__ __forceinline__ TfAct tf_act_view(uint8_t* lds, int nb) {
     TfAct a;
     a.q8 = reinterpret_cast<const int8_t*>(lds);
-    a.d8 = reinterpret_cast<const float*>(lds + nb * 256);
+    a.d8 = reinterpret_cast<const float*>(lds + TF_Q8_LDS_BYTES(nb));
     a.ds = a.d8 + nb * 8;
     a.s16 = reinterpret_cast<const int32_t*>(a.ds + nb * 8);
     a.xf = reinterpret_cast<const float*>(a.s16 + nb * 16);
@@ -107,7 +114,7 @@ inline bool tf_src_ok(const TfActSrc& src) {
 template <bool WITH_F32, int SK>
 __device__ __forceinline__ void tf_stage_act(const TfActSrc& src, int nb, uint8_t* lds) {
     int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + nb * 256);
+    float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
     float* dss = d8s + nb * 8;
     int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
     float* xf = reinterpret_cast<float*>(s16 + nb * 16);
@@ -129,8 +136,8 @@ __device__ __forceinline__ void tf_stage_act(const TfActSrc& src, int nb, uint8_
                 a = tf_u32x4{w[0], w[1], w[2], w[3]};
                 b = tf_u32x4{w[4], w[5], w[6], w[7]};
             }
-            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[0] = a;
-            reinterpret_cast<tf_u32x4*>(q8s + g * 32)[1] = b;
+            reinterpret_cast<tf_u32x4*>(q8s + tf_q8_pad(g * 32))[0] = a;
+            reinterpret_cast<tf_u32x4*>(q8s + tf_q8_pad(g * 32))[1] = b;
             const int one = 0x01010101;
             int sa = tf_dot4(one, (int)a.x, 0);
             sa = tf_dot4(one, (int)a.y, sa);
@@ -186,7 +193,7 @@ __device__ __forceinline__ void tf_stage_act(const TfActSrc& src, int nb, uint8_
                 const bool ok = e0[k] >= 0;
                 const int e = ok ? e0[k] : 0;
                 const int g = e >> 5, half = m >> 3;
-                uint16_t* pq = ok ? reinterpret_cast<uint16_t*>(q8s + e)
+                uint16_t* pq = ok ? reinterpret_cast<uint16_t*>(q8s + tf_q8_pad(e))
                                   : reinterpret_cast<uint16_t*>(tf_dummy);
                 *pq = (uint16_t)((r[k].q0 & 0xff) | ((r[k].q1 & 0xff) << 8));
                 int* ps = (ok && (m & 7) == 0) ? s16 + 2 * g + half : tf_dummy + 1;
