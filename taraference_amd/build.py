@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import shlex
 import subprocess
 import sys
 from pathlib import Path
@@ -27,6 +28,8 @@ CFLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
+# extra compiler flags (e.g. -D tuning overrides for an experiment build)
+CFLAGS += shlex.split(os.environ.get("TF_HIPCC_EXTRA", ""))
 
 
 def sources() -> list[Path]:

@@ -187,9 +187,28 @@ __device__ __forceinline__ void tf_p_trace_flush(TfPA& a) {
 // workgroup; returns false (everywhere) if the wait timed out or the launch
 // was aborted.  !WG: called by the R threads alone, no barrier; a time-out
 // or abort sets tf_p_flag, which the caller reads after its next barrier.
-template <int K, int P, class Dst, bool WG = true>
-__device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src, int n,
-                                          unsigned tag, int rank, int R, TfPA& a) {
+// Two flagged vectors polled as one: words [0, n0) of a (tag ta), then b (tag tb).
+struct TfPSplitSrc {
+    const unsigned long long *a, *b;
+    int n0;
+    unsigned ta, tb;
+};
+__device__ __forceinline__ unsigned long long tf_p_src_ld(const unsigned long long* p, int i) {
+    return tf_ldc64(p + i);
+}
+__device__ __forceinline__ unsigned tf_p_src_tag(const unsigned long long*, unsigned tag, int) {
+    return tag;
+}
+__device__ __forceinline__ unsigned long long tf_p_src_ld(const TfPSplitSrc& s, int i) {
+    return tf_ldc64(i < s.n0 ? s.a + i : s.b + (i - s.n0));
+}
+__device__ __forceinline__ unsigned tf_p_src_tag(const TfPSplitSrc& s, unsigned, int i) {
+    return i < s.n0 ? s.ta : s.tb;
+}
+
+template <int K, int P, class Dst, bool WG = true, class Src = const unsigned long long*>
+__device__ __forceinline__ bool tf_p_poll(Dst dst, Src src, int n, unsigned tag, int rank, int R,
+                                          TfPA& a) {
     int bad = n > K * R * P;
 #pragma unroll
     for (int p = 0; p < P; p++) {
@@ -198,12 +217,13 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const int i = i0 + k * R;
-            v[k] = tf_ldc64(src + (i < n ? i : 0));
+            v[k] = tf_p_src_ld(src, i < n ? i : 0);
         }
         for (int spins = 0; !bad;) {
             bool miss = false;
 #pragma unroll
-            for (int k = 0; k < K; k++) miss |= (unsigned)(v[k] >> 32) != tag && i0 + k * R < n;
+            for (int k = 0; k < K; k++)
+                miss |= (unsigned)(v[k] >> 32) != tf_p_src_tag(src, tag, i0 + k * R) && i0 + k * R < n;
             if (!miss) break;
             if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
                 bad = 1;
@@ -213,7 +233,7 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, const unsigned long long* src
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const int i = i0 + k * R;
-                v[k] = tf_ldc64(src + (i < n ? i : 0));
+                v[k] = tf_p_src_ld(src, i < n ? i : 0);
             }
         }
 #pragma unroll
@@ -722,6 +742,9 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 // it arrives, and each compute wave then consumes its tasks one by one as
 // their weights land.
 #define TF_P_CW (TF_P_WAVES - 1)
+#ifndef TF_P_GU_D
+#define TF_P_GU_D 3
+#endif
 
 template <int IT>
 struct TfPGuRegs {
@@ -734,7 +757,7 @@ struct TfPGuMap {
     static constexpr int HMAX = SPR <= 8 ? 3 : 5;            // half-groups per workgroup
     // tasks per compute wave, and register sets in flight
     static constexpr int K = (16 * HMAX + TF_P_CW * JPW - 1) / (TF_P_CW * JPW);
-    static constexpr int D = SPR <= 8 ? K : 4;
+    static constexpr int D = SPR <= 8 ? TF_P_GU_D : 4;
     static_assert(JPW >= 1 && JPW <= 2, "gate/up lane map needs SPR >= 4");
 };
 
@@ -1020,17 +1043,21 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     uint16_t* v_lds = reinterpret_cast<uint16_t*>(lds + LA::K_BYTES);
     float* q_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES);
     float* p_lds = q_lds + 8 * HD;
-    // q of the kv head's G query heads and the new K/V row
-    if (!tf_p_poll<2, 1>([&](int i, uint32_t b) { q_lds[i] = __uint_as_float(b); },
-                         fq + (size_t)g.kh * G * HD, G * HD, tq, tid, TF_P_THREADS, a))
-        return false;
-    if (!tf_p_poll<1, 1>(
-            [&](int i, uint32_t b) {
-                if (i < HD) tf_p_knew[i] = (uint16_t)b;
-                else tf_p_vnew[i - HD] = (uint16_t)b;
-            },
-            fkv + (size_t)g.kh * 2 * HD, 2 * HD, tkv, tid, TF_P_THREADS, a))
-        return false;
+    // q of the kv head's G query heads (words 0 .. G HD) and the new K/V row
+    // (words G HD .. G HD + 2 HD): both vectors in one poll
+    {
+        const unsigned long long* qsrc = fq + (size_t)g.kh * G * HD;
+        const unsigned long long* kvsrc = fkv + (size_t)g.kh * 2 * HD;
+        const int nq = G * HD;
+        if (!tf_p_poll<3, 1>(
+                [&](int i, uint32_t b) {
+                    if (i < nq) q_lds[i] = __uint_as_float(b);
+                    else if (i < nq + HD) tf_p_knew[i - nq] = (uint16_t)b;
+                    else tf_p_vnew[i - nq - HD] = (uint16_t)b;
+                },
+                TfPSplitSrc{qsrc, kvsrc, nq, tq, tkv}, nq + 2 * HD, 0u, tid, TF_P_THREADS, a))
+            return false;
+    }
 
     const bool own = wave < G;  // wave-uniform: this wave owns head `wave`
     float m = TF_P_NEG_BIG, l = 0.f, o0 = 0.f, o1 = 0.f;
@@ -1116,7 +1143,8 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         return true;
     }
-    // ---- publish this split's partial; the split-0 workgroup merges
+    // ---- publish this split's partial; head w is merged by wave w of split
+    // workgroup w mod n_ws (the merges spread over the splits)
     if (own) {
         unsigned long long* pp = tf_p_part(a, g.kh, wave, g.ws);
         if (lane == 0) {
@@ -1126,67 +1154,58 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         tf_p_putf(pp + 2 + 2 * lane, o0, tp);
         tf_p_putf(pp + 3 + 2 * lane, o1, tp);
     }
-    if (g.ws != 0 || !own) return true;
-    // wave `wave` merges head `wave`: lane s holds split s's (m, l); lane =
-    // dims 2 lane, 2 lane + 1 for O; the O words of 8 splits are polled
-    // together.  M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O =
-    // sum_s w_s O_s (attn/flash.cu:222-255), the O sum in split order.
+    if (!own || wave % g.n_ws != g.ws) return true;
+    // lane s holds split s's (m, l); lane = dims 2 lane, 2 lane + 1 for O.
+    // M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O = sum_s w_s O_s
+    // (attn/flash.cu:222-255), the O sum in split order.  The (m, l) words
+    // and the O words of the first 16 splits are polled together.
     const unsigned long long* pbase = tf_p_part(a, g.kh, wave, 0);
     constexpr size_t PS = 2 + HD;
-    float A0 = 0.f, A1 = 0.f, Lt = 0.f;
-    {
+    constexpr int CH = 16;  // splits per O poll
+    float A0 = 0.f, A1 = 0.f, Lt = 0.f, ws_ = 0.f;
+    for (int s0 = 0; s0 < g.n_ws; s0 += CH) {
         const int sl = lane < g.n_ws ? lane : 0;
-        unsigned long long wm = tf_ldc64(pbase + sl * PS), wl = tf_ldc64(pbase + sl * PS + 1);
+        unsigned long long wm = 0, wl = 0, w0[CH], w1[CH];
+        auto load = [&]() {
+            if (s0 == 0) {  // wave-uniform
+                wm = tf_ldc64(pbase + sl * PS);
+                wl = tf_ldc64(pbase + sl * PS + 1);
+            }
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int sp = s0 + u < g.n_ws ? s0 + u : s0;
+                w0[u] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
+                w1[u] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
+            }
+        };
+        load();
         for (int spins = 0;;) {
-            const bool miss =
-                lane < g.n_ws && ((unsigned)(wm >> 32) != tp || (unsigned)(wl >> 32) != tp);
+            bool miss = s0 == 0 && lane < g.n_ws &&
+                        ((unsigned)(wm >> 32) != tp || (unsigned)(wl >> 32) != tp);
+#pragma unroll
+            for (int u = 0; u < CH; u++)
+                miss |= s0 + u < g.n_ws &&
+                        ((unsigned)(w0[u] >> 32) != tp || (unsigned)(w1[u] >> 32) != tp);
             if (!__builtin_amdgcn_ballot_w64(miss)) break;
             if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
                 tf_p_abort(a);
                 return true;  // the launch is aborted; outputs are not used
             }
-            __builtin_amdgcn_s_sleep(4);
-            wm = tf_ldc64(pbase + sl * PS);
-            wl = tf_ldc64(pbase + sl * PS + 1);
+            __builtin_amdgcn_s_sleep(2);
+            load();
         }
-        const float ms = lane < g.n_ws ? __uint_as_float((unsigned)wm) : TF_P_NEG_BIG;
-        const float Mx = tf_wave_max(ms);
-        const float ws_ = lane < g.n_ws ? __expf(ms - Mx) : 0.f;
-        Lt = tf_group_sum<64>(ws_ * __uint_as_float((unsigned)wl));
-        for (int s0 = 0; s0 < g.n_ws; s0 += 8) {
-            unsigned long long w0[8], w1[8];
+        if (s0 == 0) {
+            const float ms = lane < g.n_ws ? __uint_as_float((unsigned)wm) : TF_P_NEG_BIG;
+            const float Mx = tf_wave_max(ms);
+            ws_ = lane < g.n_ws ? __expf(ms - Mx) : 0.f;
+            Lt = tf_group_sum<64>(ws_ * __uint_as_float((unsigned)wl));
+        }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int sp = s0 + u < g.n_ws ? s0 + u : s0;
-                w0[u] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
-                w1[u] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
-            }
-            for (int spins = 0;;) {
-                bool miss = false;
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-                    miss |= s0 + u < g.n_ws &&
-                            ((unsigned)(w0[u] >> 32) != tp || (unsigned)(w1[u] >> 32) != tp);
-                if (!__builtin_amdgcn_ballot_w64(miss)) break;
-                if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
-                    tf_p_abort(a);
-                    return true;
-                }
-                __builtin_amdgcn_s_sleep(4);
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int sp = s0 + u < g.n_ws ? s0 + u : s0;
-                    w0[u] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
-                    w1[u] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (s0 + u < g.n_ws) {  // wave-uniform
-                    const float w = tf_readlane(ws_, s0 + u);
-                    A0 = fmaf(w, __uint_as_float((unsigned)w0[u]), A0);
-                    A1 = fmaf(w, __uint_as_float((unsigned)w1[u]), A1);
-                }
+        for (int u = 0; u < CH; u++) {
+            if (s0 + u < g.n_ws) {  // wave-uniform
+                const float w = tf_readlane(ws_, s0 + u);
+                A0 = fmaf(w, __uint_as_float((unsigned)w0[u]), A0);
+                A1 = fmaf(w, __uint_as_float((unsigned)w1[u]), A1);
             }
         }
     }
