@@ -1034,7 +1034,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
                                               const unsigned long long* fq,
                                               const unsigned long long* fkv, unsigned tq,
                                               unsigned tkv, unsigned long long* fo,
-                                              unsigned to, unsigned tp) {
+                                              unsigned to, unsigned tp, int sk) {
     using LA = TfPAttnLayout;
     constexpr int HD = TF_P_HD;
     const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
@@ -1058,6 +1058,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
                 TfPSplitSrc{qsrc, kvsrc, nq, tq, tkv}, nq + 2 * HD, 0u, tid, TF_P_THREADS, a))
             return false;
     }
+    tf_p_stamp(a, sk, 1);
 
     const bool own = wave < G;  // wave-uniform: this wave owns head `wave`
     float m = TF_P_NEG_BIG, l = 0.f, o0 = 0.f, o1 = 0.f;
@@ -1134,6 +1135,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
         o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
     }
+    tf_p_stamp(a, sk, 2);
     // output group of this lane's dims: (head, 32-dim group) in Q8
     const int og = ((g.kh * G + wave) * HD + 2 * lane) / 32;
     if (g.n_ws == 1) {
@@ -1291,35 +1293,12 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     return true;
 }
 
-// Cache warm-up by the workgroups that have no attention work: they read one
-// dword of every 128-byte line of this layer's wo, gate, up and down weights
-// (the values are discarded), so the memory-side cache holds those lines
-// when the next stages stream them.
-__device__ __forceinline__ void tf_p_warm(TfPA& a, TfPL& L, int idle_rank, int n_idle) {
-    const uint8_t* ptrs[4] = {L.wo, L.gate, L.up, L.down};
-    const size_t bytes[4] = {(size_t)a.E * L.cb_o, (size_t)a.F * L.cb_gu, (size_t)a.F * L.cb_gu,
-                             (size_t)a.E * L.cb_down};
-    const size_t stride = (size_t)n_idle * TF_P_THREADS;
-    uint32_t acc = 0;
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-        const size_t lines = bytes[m] / 128;
-        for (size_t ln = (size_t)idle_rank * TF_P_THREADS + tf_p_tid(); ln < lines; ln += stride)
-            acc ^= tf_gld(reinterpret_cast<const uint32_t*>(ptrs[m] + ln * 128));
-    }
-    asm volatile("" ::"v"(acc));
-}
-
 __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     const TfPAttnGeo g = tf_p_attn_geo(a, pos);
-    if (!g.active) {
-        const int n_att = a.KV * g.n_ws;
-        tf_p_warm(a, L, (int)blockIdx.x - n_att, (int)gridDim.x - n_att);
-        return true;
-    }
+    if (!g.active) return true;
     TfPAttnRegs ra;
     tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
@@ -1327,7 +1306,7 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     const bool ok = tf_p_attn_run(
         a, L, g, pos, ra, lds, tf_p_vec(a, TF_PK_Q, li), tf_p_vec(a, TF_PK_KV, li),
         tf_p_tag(tb, li, TF_PK_Q), tf_p_tag(tb, li, TF_PK_KV), tf_p_vec(a, TF_PK_O, li),
-        tf_p_tag(tb, li, TF_PK_O), tf_p_tag(tb, li, TF_PK_PART));
+        tf_p_tag(tb, li, TF_PK_O), tf_p_tag(tb, li, TF_PK_PART), 5 * li + 1);
     tf_p_stamp(a, 5 * li + 1, 3);
     return ok;
 }
