@@ -375,6 +375,194 @@ __device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* s
     __syncthreads();
 }
 
+// Q8 of four values held by one lane of an 8-lane group (lane j = lane & 7
+// holds values 4 j .. 4 j + 3 of the 32): the quantization of tf_q8_oct
+// spread over twice the lanes.  s_half: int sum over the lane's 16-value
+// half (lanes 0-3 or 4-7), s_other: the other half's; f_half the f32 sum of
+// the half in the pairwise tree ((x0 + x1) + (x2 + x3)) + ... .
+struct TfQ8Quad {
+    int q[4];
+    float d;
+    int s_half, s_other;
+    float f_half;
+};
+
+template <bool F32>
+__device__ __forceinline__ TfQ8Quad tf_q8_g8(const float (&x)[4]) {
+    TfQ8Quad r;
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) am = fmaxf(am, fabsf(x[i]));
+    uint32_t u = __builtin_bit_cast(uint32_t, am);  // magnitudes order as unsigned ints
+    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)u));
+    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_2301>((int)u));
+    u = max(u, (uint32_t)tf_dppi<TF_DPP_ROW_HALF_MIRROR>((int)u));
+    const float amax = __builtin_bit_cast(float, u);
+    r.d = amax * (1.0f / 127.0f);
+    const float rcp = __builtin_amdgcn_rcpf(r.d);
+    // as tf_q8_oct: the product is exact enough away from a .5 tie; near one
+    // (rare) the IEEE quotient decides
+    float y[4];
+    bool rk[4], any = false;
+    const bool tiny = !(r.d >= 1.17549435e-38f);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        y[i] = x[i] * rcp;
+        const float fr = fabsf(y[i] - __builtin_truncf(y[i]));
+        rk[i] = tiny || fabsf(fr - 0.5f) < 6.103515625e-05f;
+        any |= rk[i];
+    }
+    if (any) {
+        const float dd = amax == 0.f ? 1.f : r.d;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (rk[i]) y[i] = x[i] / dd;
+    }
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.q[i] = amax == 0.f ? 0 : (int)__builtin_rintf(y[i]);
+        s += r.q[i];
+    }
+    s += tf_dppi<TF_DPP_QUAD_1032>(s);
+    r.s_half = s + tf_dppi<TF_DPP_QUAD_2301>(s);
+    r.s_other = tf_dppi<TF_DPP_ROW_HALF_MIRROR>(r.s_half);  // lane 7 - j: the other half
+    r.f_half = 0.f;
+    if (F32) {
+        const float t4 = (x[0] + x[1]) + (x[2] + x[3]);
+        const float t8 = t4 + tf_dpp<TF_DPP_QUAD_1032>(t4);
+        r.f_half = t8 + tf_dpp<TF_DPP_QUAD_2301>(t8);
+    }
+    return r;
+}
+
+// The 4 norm weights per step a thread applies in tf_p_stage8b (values
+// 4 tid + 4 TF_P_THREADS step .. + 3), loaded before the stage's weights.
+template <int NS>
+__device__ __forceinline__ void tf_p_norm_wload4(const float* w, int n, float (&r)[NS][4]) {
+#pragma unroll
+    for (int st = 0; st < NS; st++) {
+        const int e0 = 4 * tf_p_tid() + 4 * TF_P_THREADS * st;
+        const tf_u32x4 v = tf_ld16(w + (e0 < n ? e0 : 0));
+        r[st][0] = __uint_as_float(v.x);
+        r[st][1] = __uint_as_float(v.y);
+        r[st][2] = __uint_as_float(v.z);
+        r[st][3] = __uint_as_float(v.w);
+    }
+}
+
+// tf_p_stage8 with eight lanes per group: every thread of the workgroup
+// takes four values per step (NS steps cover 4 TF_P_THREADS NS values).
+// Ends with a workgroup barrier.
+template <bool F32, bool NORM, int NS>
+__device__ __forceinline__ void tf_p_stage8b(uint8_t* lds, int nb, const float* src, float scale,
+                                             const float (&w)[NS][4]) {
+    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
+    float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
+    float* dss = d8s + nb * 8;
+    int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
+    float* xf = reinterpret_cast<float*>(s16 + nb * 16);
+    float* xs16 = xf + nb * 256;
+    const int n = nb * 256;
+    const int tid = tf_p_tid(), j = tid & 7;
+#pragma unroll
+    for (int st = 0; st < NS; st++) {
+        const int e0 = 4 * tid + 4 * TF_P_THREADS * st;
+        if (4 * TF_P_THREADS * st >= n) break;  // workgroup-uniform
+        const int e = e0 < n ? e0 : 0;
+        const int g = e >> 5;
+        const float4 a = *reinterpret_cast<const float4*>(src + e);
+        float x[4] = {a.x, a.y, a.z, a.w};
+        if (NORM) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] = x[i] * scale * w[st][i];
+        }
+        const TfQ8Quad r = tf_q8_g8<F32>(x);
+        if (e0 < n) {
+            uint32_t b = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) b |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
+            *reinterpret_cast<uint32_t*>(q8s + tf_q8_pad(e)) = b;
+            if ((j & 3) == 0) {
+                s16[2 * g + (j >> 2)] = r.s_half;
+                if (F32) xs16[2 * g + (j >> 2)] = r.f_half;
+            }
+            if (j == 0) {
+                d8s[g] = r.d;
+                dss[g] = r.d * (float)(r.s_half + r.s_other);
+            }
+            if (F32 && NORM) *reinterpret_cast<float4*>(xf + e) = make_float4(x[0], x[1], x[2], x[3]);
+        }
+    }
+    __syncthreads();
+}
+
+// Wave-level poll of n flagged f32 words into LDS (dst[i]) that also forms
+// the reference's RMS partials on the way: lane l takes words l + 64 k, in
+// passes of PK words, and p[k mod 4] accumulates their squares in k order --
+// partial t = l + 64 c of the reference sums x[t], x[t + 256], ... in turn,
+// which is p[c] of lane l.  Padding past n adds nothing (fmaf(0, 0, p) = p).
+// Returns 1 / sqrt(mean + eps) on every lane; a time-out or abort sets
+// tf_p_flag (the caller reads it after its next barrier).
+template <int PK, int PP>
+__device__ __forceinline__ float tf_p_poll_rms(TfPA& a, float* dst, const unsigned long long* src,
+                                               int n, unsigned tag, float eps) {
+    const int lane = tf_p_tid() & 63;
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+    bool bad = n > 64 * PK * PP;
+#pragma unroll
+    for (int pp = 0; pp < PP; pp++) {
+        unsigned long long v[PK];
+        auto load = [&]() {
+#pragma unroll
+            for (int k = 0; k < PK; k++) {
+                const int i = lane + 64 * (pp * PK + k);
+                v[k] = tf_ldc64(src + (i < n ? i : 0));
+            }
+        };
+        load();
+        for (int spins = 0; !bad;) {
+            bool miss = false;
+#pragma unroll
+            for (int k = 0; k < PK; k++)
+                miss |= (unsigned)(v[k] >> 32) != tag && lane + 64 * (pp * PK + k) < n;
+            if (!__builtin_amdgcn_ballot_w64(miss)) break;
+            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                bad = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            load();
+        }
+#pragma unroll
+        for (int k = 0; k < PK; k++) {
+            const int kk = pp * PK + k, i = lane + 64 * kk;
+            if (i < n) {
+                const float x = __uint_as_float((unsigned)v[k]);
+                dst[i] = x;
+                p[kk & 3] = fmaf(x, x, p[kk & 3]);
+            }
+        }
+    }
+    if (bad) {
+        tf_p_abort(a);
+        tf_p_flag = 1;
+    }
+    // red = (p0 + p2) + (p1 + p3), then the shift-down tree over offsets 32,
+    // 16, 8, 4, 2, 1 (lane 0 adds the value of lane k at each step): here as
+    // exchanges with lane ^ 32, ^ 16 and row rotations by 8 and 4 (the lanes
+    // they pair hold equal values after the earlier steps) and quad swaps, so
+    // every lane forms lane 0's sum
+    float v = (p[0] + p[2]) + (p[1] + p[3]);
+    v += __shfl_xor(v, 32, 64);
+    v += tf_swap16(v);
+    v += tf_dpp<TF_DPP_ROW_ROR8>(v);
+    v += tf_dpp<TF_DPP_ROW_ROR4>(v);
+    v += tf_dpp<TF_DPP_QUAD_2301>(v);
+    v += tf_dpp<TF_DPP_QUAD_1032>(v);
+    return 1.0f / sqrtf(v / (float)n + eps);
+}
+
 // 1 / sqrt(mean(x^2) + eps) of the n values x[0 .. n) in LDS, computed by
 // each wave on its own in the reference's order (kernels/ops.cu:4-34):
 // partial t (t < 256) = fused square-accumulate of x[t], x[t + 256], ... in
@@ -1346,9 +1534,13 @@ __device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int
     return true;
 }
 
+// LDS word carrying the RMS scale from the polling wave to the others.
+__shared__ float tf_p_rms;
+
 template <int SPR, int IT>
 __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     using M = TfPGuMap<SPR>;
+    constexpr int NS = SPR <= 8 ? 1 : 2;  // staging steps (E <= 2048 NS)
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
@@ -1361,20 +1553,20 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     const unsigned tag_x = tf_p_tag(tb, li, TF_PK_HX);
     float* raw = tf_p_raw(lds, nbE);
     // the norm weights first: waiting for them does not wait for the weights
-    float nw[8];
-    tf_p_norm_wload(L.ffn_norm, a.E, nw);
+    float nw[NS][4];
+    tf_p_norm_wload4<NS>(L.ffn_norm, a.E, nw);
     if (wave == 0) {
         tf_p_stamp(a, 5 * li + 3, 0);
         __syncthreads();  // the previous stage's LDS readers are done
-        auto put = [&](int i, uint32_t b) { raw[i] = __uint_as_float(b); };
         // E <= 256 SPR: 4 SPR words per lane, in passes of up to 32
         constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
-        tf_p_poll<PK, PP, decltype(put), false>(
-            put, tf_p_vec(a, TF_PK_XA, li), a.E, tf_p_tag(tb, li, TF_PK_XA), tf_p_tid() & 63, 64, a);
+        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
+                                               tf_p_tag(tb, li, TF_PK_XA), a.eps);
+        if (tf_p_tid() == 0) tf_p_rms = sc;
         tf_p_stamp(a, 5 * li + 3, 1);
-        __syncthreads();  // raw row in LDS
+        __syncthreads();  // raw row and scale in LDS
         if (tf_p_flag) return false;
-        tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+        tf_p_stage8b<false, true, NS>(lds, nbE, raw, sc, nw);
         tf_p_stamp(a, 5 * li + 3, 2);
         tf_p_gu_exchange(a, sp, fx, tag_x);
         __syncthreads();  // h of every compute wave in LDS
@@ -1388,9 +1580,9 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
 #pragma unroll
         for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
         __syncthreads();  // the previous stage's LDS readers are done
-        __syncthreads();  // raw row in LDS
+        __syncthreads();  // raw row and scale in LDS
         if (tf_p_flag) return false;
-        tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+        tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
         tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
         __syncthreads();  // h of every compute wave in LDS
         if (tf_p_flag) return false;

@@ -32,6 +32,8 @@ __device__ __forceinline__ int tf_dot4(int a, int b, int c) {
 #define TF_DPP_QUAD_2301 0x4E   // quad_perm [2,3,0,1]  (xor 2)
 #define TF_DPP_ROW_HALF_MIRROR 0x141
 #define TF_DPP_ROW_MIRROR 0x140
+#define TF_DPP_ROW_ROR8 0x128   // row_ror:8 (lane i of a row reads lane i ^ 8)
+#define TF_DPP_ROW_ROR4 0x124   // row_ror:4 (lane i reads lane (i - 4) mod 16)
 
 template <int CTRL>
 __device__ __forceinline__ float tf_dpp(float v) {
