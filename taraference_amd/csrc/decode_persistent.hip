@@ -166,8 +166,8 @@ __device__ __forceinline__ void tf_p_abort(TfPA& a) {
 // next memory wait) and are copied out at the end of the launch.
 __shared__ unsigned long long tf_p_tstamp[(5 * TF_P_MAX_LAYERS + 1) * 4];
 
-__device__ __forceinline__ void tf_p_stamp(TfPA& a, int k, int which) {
-    if (a.trace && tf_p_tid() == 0) tf_p_tstamp[k * 4 + which] = __builtin_amdgcn_s_memrealtime();
+__device__ __forceinline__ void tf_p_stamp(TfPA& a, int k, int which, int who = 0) {
+    if (a.trace && tf_p_tid() == who) tf_p_tstamp[k * 4 + which] = __builtin_amdgcn_s_memrealtime();
 }
 
 __device__ __forceinline__ void tf_p_trace_flush(TfPA& a) {
@@ -496,6 +496,9 @@ __device__ __forceinline__ void tf_p_stage8b(uint8_t* lds, int nb, const float* 
     }
     __syncthreads();
 }
+
+// LDS word carrying the RMS scale from the polling wave to the others.
+__shared__ float tf_p_rms;
 
 // Wave-level poll of n flagged f32 words into LDS (dst[i]) that also forms
 // the reference's RMS partials on the way: lane l takes words l + 64 k, in
@@ -844,6 +847,66 @@ __device__ __forceinline__ void tf_p_rows_load(const uint8_t* w, int cb, int nb,
     const uint8_t* col = w + (size_t)(valid ? j : 0) * cb;
     if constexpr (Q6) tf_q6k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r);
     else tf_q4k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r);
+}
+
+// Task `task` of a row GEMV issued unconditionally: a task past the end
+// reloads task 0 (its result is dropped), so a ring of such loads keeps exact
+// memory waits.
+template <int SPR, int IT, bool Q6>
+__device__ __forceinline__ void tf_p_rows_load_u(const uint8_t* w, int cb, int nb, int n_rows,
+                                                 int task, TfPRow<IT, Q6>& r) {
+    constexpr int UNITS = 16 / SPR;
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int j = task * UNITS + ln.unit;
+    const uint8_t* col = w + (size_t)(j < n_rows ? j : 0) * cb;
+    if constexpr (Q6) tf_q6k_row_load_u<SPR, IT>(col, nb, ln.sir, ln.t, r);
+    else tf_q4k_row_load_u<SPR, IT>(col, nb, ln.sir, ln.t, r);
+}
+
+// Ring over this wave's tasks w0, w0 + nwv, ... (nwv waves share the rows):
+// r[d] holds task w0 + (k D + d) nwv on entry to round k; every round runs
+// all D slots and refills each right after it is consumed, so the memory
+// waits stay exact.  EPI as tf_p_rows_run.
+template <int SPR, int IT, bool Q6, int D, int EPI, class Res>
+__device__ __forceinline__ void tf_p_rows_ring(const uint8_t* w, int cb, int nb, int n_rows,
+                                               const TfAct& x, TfPRow<IT, Q6> (&r)[D], int w0,
+                                               int nwv, Res res, unsigned long long* fout,
+                                               unsigned tag, float* out,
+                                               unsigned long long* amax, int slot) {
+    constexpr int UNITS = 16 / SPR;
+    const TfPLane ln = tf_p_lane<SPR>();
+    const int n_tasks = (n_rows + UNITS - 1) / UNITS;
+    const bool lead = (ln.lane & (4 * SPR - 1)) == 0;
+    unsigned long long best = 0;
+    for (int base = w0; base < n_tasks; base += D * nwv) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int task = base + d * nwv;
+            const int j = task * UNITS + ln.unit;
+            const bool valid = task < n_tasks && j < n_rows;
+            float acc;
+            if constexpr (Q6) acc = tf_q6k_row_partial<SPR, IT>(r[d], true, 0, nb, ln.sir, ln.t, x);
+            else acc = tf_q4k_row_partial<SPR, IT>(r[d], true, 0, nb, ln.sir, ln.t, x);
+            const int nt = task + D * nwv;
+            tf_p_rows_load_u<SPR, IT, Q6>(w, cb, nb, n_rows, nt < n_tasks ? nt : 0, r[d]);
+            acc = tf_group_sum<4 * SPR>(acc);
+            if (valid && lead) {
+                if constexpr (EPI == 0) {
+                    tf_p_putf(fout + j, acc + res(j), tag);
+                } else {
+                    *(TF_GAS float*)(out + j) = acc;
+                    const unsigned long long k = tf_argmax_key(acc, j);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    }
+    if constexpr (EPI == 1) {
+        best = tf_wave_max_u64(best);
+        if (ln.lane == 0 && best)
+            __hip_atomic_fetch_max((TF_GAS unsigned long long*)amax + (slot % TF_ARGMAX_SLOTS),
+                                   best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // Rows of one matrix.  EPI 0: residual stream (see below); EPI 1:
@@ -1442,13 +1505,15 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
-    const int nbE = a.E / 256, wid = tf_p_wid(), tid = tf_p_tid();
+    const int nbE = a.E / 256, tid = tf_p_tid(), wave = tid >> 6;
+    constexpr int NS = SPR <= 8 ? 1 : 2;
     const TfAct xE = tf_act_view(lds, nbE);
-    float* xf = const_cast<float*>(xE.xf);
+    // compute waves 1 .. 7 of every workgroup share the tasks; wave 0 polls
+    const int cwid = (wave - 1) * (int)gridDim.x + (int)blockIdx.x, ncw = gridDim.x * TF_P_CW;
+    float nw[NS][4];
+    tf_p_norm_wload4<NS>(L.attn_norm, a.E, nw);
     TfPQkvRegs<SPR, IT> rq;
-    tf_p_qkv_load<SPR, IT>(a, L, wid, rq);
-    float nw[8];
-    tf_p_norm_wload(L.attn_norm, a.E, nw);
+    if (wave != 0) tf_p_qkv_load<SPR, IT>(a, L, cwid, rq);
     float* raw = tf_p_raw(lds, nbE);
     tf_p_stamp(a, 5 * li, 0);
     __syncthreads();  // the previous stage's LDS readers are done
@@ -1461,23 +1526,31 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
             raw[i] = a.embd_q6k ? tf_q6k_value(blk, i & 255) : tf_q4k_value(blk, i & 255);
         }
         __syncthreads();
-    } else if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
-                   a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E, tf_p_tag(tb, li - 1, TF_PK_XB))) {
-        return false;
+        if (wave == 0) {  // the whole wave forms the sum (cross-lane steps)
+            const float sc = tf_p_rms_scale(raw, a.E, a.eps);
+            if (tid == 0) tf_p_rms = sc;
+        }
+    } else if (wave == 0) {
+        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
+        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
+                                               tf_p_tag(tb, li - 1, TF_PK_XB), a.eps);
+        if (tid == 0) tf_p_rms = sc;
     }
     tf_p_stamp(a, 5 * li, 1);
-    tf_p_stage8<true, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+    __syncthreads();  // raw row and scale in LDS
+    if (tf_p_flag) return false;
+    tf_p_stage8b<true, true, NS>(lds, nbE, raw, tf_p_rms, nw);
     tf_p_stamp(a, 5 * li, 2);
+    if (wave == 0) return true;
     const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
-    const int nwv = gridDim.x * TF_P_WAVES;
     unsigned long long* fq = tf_p_vec(a, TF_PK_Q, li);
     unsigned long long* fkv = tf_p_vec(a, TF_PK_KV, li);
     const unsigned tq = tf_p_tag(tb, li, TF_PK_Q), tkv = tf_p_tag(tb, li, TF_PK_KV);
-    for (int task = wid; task < g.n_tasks; task += nwv) {
-        if (task != wid) tf_p_qkv_load<SPR, IT>(a, L, task, rq);
+    for (int task = cwid; task < g.n_tasks; task += ncw) {
+        if (task != cwid) tf_p_qkv_load<SPR, IT>(a, L, task, rq);
         tf_p_qkv_task<SPR, IT>(a, L, task, pos, xE, rq, fq, fkv, tq, tkv);
     }
-    tf_p_stamp(a, 5 * li, 3);
+    tf_p_stamp(a, 5 * li, 3, 64);
     return true;
 }
 
@@ -1533,9 +1606,6 @@ __device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int
     tf_p_stamp(a, 5 * li + 2, 3);
     return true;
 }
-
-// LDS word carrying the RMS scale from the polling wave to the others.
-__shared__ float tf_p_rms;
 
 template <int SPR, int IT>
 __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
@@ -1634,22 +1704,35 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     TfPA& a = *pa;
     const int nbE = a.E / 256, tid = tf_p_tid(), L = a.n_layer;
     const TfAct xE = tf_act_view(lds, nbE);
-    constexpr int D = 4;
+    constexpr int D = 4, NS = SPR <= 8 ? 1 : 2;
+    const int wave = tid >> 6, nwv = gridDim.x * TF_P_WAVES, w0 = tf_p_wid();
+    const int n_tasks = (a.n_vocab + 16 / SPR - 1) / (16 / SPR);
+    float nw[NS][4];
+    tf_p_norm_wload4<NS>(a.out_norm, a.E, nw);
     TfPRow<IT, true> rh[D];
-    tf_p_rows_prefetch<SPR, IT, true, D>(a.head, a.head_cb, nbE, a.n_vocab, rh);
-    float nw[8];
-    tf_p_norm_wload(a.out_norm, a.E, nw);
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+        const int t = w0 + d * nwv;
+        tf_p_rows_load_u<SPR, IT, true>(a.head, a.head_cb, nbE, a.n_vocab, t < n_tasks ? t : 0,
+                                        rh[d]);
+    }
     float* raw = tf_p_raw(lds, nbE);
     tf_p_stamp(a, 5 * L, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    if (!tf_p_poll_xf<(4096 + TF_P_THREADS - 1) / TF_P_THREADS>(
-            a, raw, tf_p_vec(a, TF_PK_XB, L - 1), a.E, tf_p_tag(tb, L - 1, TF_PK_XB)))
-        return false;
+    if (wave == 0) {
+        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
+        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XB, L - 1), a.E,
+                                               tf_p_tag(tb, L - 1, TF_PK_XB), a.eps);
+        if (tid == 0) tf_p_rms = sc;
+    }
     tf_p_stamp(a, 5 * L, 1);
-    tf_p_stage8<false, true>(lds, nbE, raw, tf_p_rms_scale(raw, a.E, a.eps), nw);
+    __syncthreads();  // raw row and scale in LDS
+    if (tf_p_flag) return false;
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
     tf_p_stamp(a, 5 * L, 2);
-    tf_p_rows_run<SPR, IT, true, D, 1>(a.head, a.head_cb, nbE, a.n_vocab, xE, rh,
-                                       [](int) { return 0.f; }, nullptr, 0u, a.logits, a.amax);
+    tf_p_rows_ring<SPR, IT, true, D, 1>(a.head, a.head_cb, nbE, a.n_vocab, xE, rh, w0, nwv,
+                                        [](int) { return 0.f; }, nullptr, 0u, a.logits, a.amax,
+                                        w0);
     tf_p_stamp(a, 5 * L, 3);
     // ticket: the keys of this workgroup are in before its ticket
     __builtin_amdgcn_s_waitcnt(0);

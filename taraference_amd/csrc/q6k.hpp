@@ -131,6 +131,19 @@ __device__ __forceinline__ void tf_q6k_row_load(const uint8_t* __restrict__ col,
     }
 }
 
+// The same loads issued unconditionally (a super-block past the row reloads
+// super-block 0; tf_q6k_row_partial skips it), so the compiler can wait for
+// exactly the loads a computation needs.
+template <int SPR, int ITERS>
+__device__ __forceinline__ void tf_q6k_row_load_u(const uint8_t* __restrict__ col, int nb, int sir,
+                                                  int p, TfQ6kRow<ITERS>& r) {
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sir + i * SPR;
+        tf_q6k_load_c(col + (size_t)(sb < nb ? sb : 0) * 212, p, r.q[i]);
+    }
+}
+
 template <int SPR, int ITERS>
 __device__ __forceinline__ float tf_q6k_row_partial(const TfQ6kRow<ITERS>& r, bool valid,
                                                     int sb0, int sb1, int sir, int p,
