@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark: batch-1 greedy decode of a random-init Qwen2.5-3B-shaped
-Q4_K_M model on one MI355X, plus the kernel roofline
-(config 1a, the fused Q4_K gate+up GEMV, the largest per-layer kernel) and
-the CPU-oracle baseline timed on this host.
+Q4_K_M model on one MI355X (config 3 of the baseline), the roofline of its
+dominant kernel (the persistent decode-step kernel, one launch per token),
+the standalone config-1a Q4_K GEMV (fused gate+up) for the metric's GEMV
+part, and the CPU-oracle baseline timed on this host.
 
 Workload: --warmup W forced decode steps build the synthetic context
 (W = 512 by default, the config's context), then --steps K greedy decode
@@ -27,12 +28,18 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+# The dominant kernel of the timed workload: the persistent decode step (one
+# launch per token, 99% of the GPU time in the kernel trace).
+DECODE_KERNEL = "tf_decode_persistent_kernel<8,1,16,3> (whole decode step, one launch per token)"
+# Its HBM bytes per launch: rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per
+# dispatch) scaled by the same counters' reading on a 256 MiB device copy
+# (FETCH_SIZE counts half of what a read moves here: factor 2.000; WRITE_SIZE
+# factor 1.000); the counter runs are kept in profiles/.
+DECODE_TRAFFIC = int((974391.3 * 2.0 + 19600.0 * 1.0) * 1024)
+# The standalone config-1a GEMV (the tf_gemv_q4k_ffn entry point), reported
+# beside it for the metric's "Q4_K GEMV % of HBM peak" part.
 ROOFLINE_KERNEL = "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU, 2048 -> 2x11008)"
-# HBM bytes per launch of the roofline kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE
-# (KiB per dispatch) scaled by the same counters' reading on a 256 MiB device
-# copy; the counter runs and the factor are kept in profiles/.
-# FETCH_SIZE 12426.5 KiB x 2.000 (the 256 MiB copy reads 131084 KiB) +
-# WRITE_SIZE 86 KiB x 1.000 (the copy writes 262144 KiB)
+# FETCH_SIZE 12426.5 KiB x 2.000 + WRITE_SIZE 86 KiB x 1.000
 ROOFLINE_TRAFFIC = int((12426.5 * 2.0 + 86.0 * 1.0) * 1024)
 
 METRIC = "batch-1 decode tok/s, Qwen2.5-3B-shape Q4_K_M; Q4_K GEMV % of HBM peak"
@@ -64,12 +71,18 @@ def decode_throughput(m, cfg, warmup, steps, seed):
     # untimed: the forced context (graph capture happens on the first call)
     first = m.generate(prompt, 1, pos0=0, use_graph=True)
     torch.cuda.synchronize()
-    # timed: `steps` decode steps continuing from the greedy token
+    # timed: `steps` decode steps continuing from the greedy token; HIP events
+    # on the stream the step graph is replayed on bracket the same region
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    toks = m.generate([int(first[0])], steps - 1, pos0=len(prompt), use_graph=True)
+    e0.record(stream)
+    toks = m.generate([int(first[0])], steps, pos0=len(prompt), use_graph=True)
+    e1.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    return dt, toks
+    return dt, toks, e0.elapsed_time(e1) * 1e-3
 
 
 def kernel_roofline(iters):
@@ -232,7 +245,7 @@ def main():
     if args.path is not None:
         m.set_path(args.path)
     log("[bench] decode ...")
-    dt, toks = decode_throughput(m, cfg, args.warmup, steps, 3)
+    dt, toks, dt_ev = decode_throughput(m, cfg, args.warmup, steps, 3)
     tok_s = steps / dt
     log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
     wbytes = synth.weight_bytes(cfg)
@@ -241,30 +254,30 @@ def main():
     del m
     torch.cuda.empty_cache()
 
-    r = kernel_roofline(args.kernel_iters)
-    # average launch duration = event pair around a burst of back-to-back
-    # launches on the kernel's stream / launches
-    achieved = r["bytes"] / (r["b2b_us"] * 1e-6) / 1e9
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": ROOFLINE_TRAFFIC,
-            "kernel": ROOFLINE_KERNEL,
-            "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
-            "us_per_launch_single": round(r["per_us"], 3)}
-    # the decode step itself: one launch per token on the default path (the
-    # persistent kernel); algorithmic bytes per launch = the weights once
-    # plus the K/V cache the attention reads (mean context of the timed
-    # steps), over the measured time per step
+    # the dominant kernel: one launch per decode step; algorithmic bytes per
+    # launch = the weights once plus the K/V cache the attention reads (mean
+    # context of the timed steps); average launch duration = HIP events
+    # around the timed region on the launch stream / steps
     ctx_mean = args.warmup + steps / 2.0
     kv_bytes = int(2 * cfg["n_layer"] * ctx_mean * cfg["n_kv"] * cfg["head_dim"] * 2)
     step_bytes = wbytes + kv_bytes
-    step_gbs = step_bytes / (dt / steps) / 1e9
-    decode_roof = {"bound": "hbm", "kernel": (f"decode step, path {path}" +
-                                              (" (tf_decode_persistent_kernel, one launch per "
-                                               "token)" if path == 4 else "")),
-                   "bytes_per_launch": step_bytes, "us_per_launch": round(dt / steps * 1e6, 2),
-                   "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                   "frac": round(step_gbs / HBM_PEAK_GBS, 4)}
+    us_step = dt_ev / steps * 1e6
+    step_gbs = step_bytes / (us_step * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+            "traffic": DECODE_TRAFFIC if path == 4 else None,
+            "kernel": DECODE_KERNEL if path == 4 else f"decode step, path {path} (several kernels)",
+            "bytes_per_launch": step_bytes, "us_per_launch": round(us_step, 2)}
+    r = kernel_roofline(args.kernel_iters)
+    # average launch duration = event pair around a graph of back-to-back
+    # launches on the kernel's stream / launches
+    achieved = r["bytes"] / (r["b2b_us"] * 1e-6) / 1e9
+    roof_gemv = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                 "traffic": ROOFLINE_TRAFFIC,
+                 "kernel": ROOFLINE_KERNEL,
+                 "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
+                 "us_per_launch_single": round(r["per_us"], 3)}
     table = {} if args.no_kernels else kernel_table(args.kernel_iters)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
 
@@ -287,7 +300,7 @@ def main():
                    "effective_weight_GBs": round(wbytes * tok_s / 1e9, 1),
                    "parallelism": "single GPU"},
         "roofline": roof,
-        "roofline_decode_step": decode_roof,
+        "roofline_q4k_gemv": roof_gemv,
         "cpu_baseline": cpu,
         "kernels": table,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
