@@ -1207,27 +1207,47 @@ struct TfPAttnLayout {
     static constexpr int V_BYTES = TF_P_TILE * TF_P_HD * 2;
     static constexpr int Q_BYTES = 8 * TF_P_HD * 4;
     static constexpr int P_BYTES = 8 * TF_P_TILE * 4;
-    static constexpr int BYTES = K_BYTES + V_BYTES + Q_BYTES + P_BYTES;
+    // the waves of a head combine their token slices: per wave (m, l) and O
+    static constexpr int C_BYTES = TF_P_WAVES * (2 + TF_P_HD) * 4;
+    static constexpr int BYTES = K_BYTES + V_BYTES + Q_BYTES + P_BYTES + C_BYTES;
     static constexpr int CHUNKS = TF_P_TILE * TF_P_HD / 8 / TF_P_THREADS;  // 16 B per thread
 };
 
+// A workgroup serves (kv head kh, head group hg, split ws): the split's tiles
+// for HPW of the kv head's G query heads.  Each head gets WPH = 8 / HPW waves,
+// and wave slice sl takes tokens [sl T, sl T + T) of every 64-token tile
+// (T = 64 / WPH).  More head groups spread a short context over more CUs at
+// no extra merge cost (the partials stay per head and split); a long context
+// keeps one group so each K/V byte is read once.
 struct TfPAttnGeo {
-    int n_ws, tpw, kh, ws, t_begin, t_end;
+    int n_ws, tpw, kh, ws, hg, n_hg, hpw, wph, t_begin, t_end;
     bool active;
 };
 
 __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     TfPAttnGeo g;
     const int seq = pos + 1;
+    const int G = a.H / a.KV;
     const int n_tiles = (seq + TF_P_TILE - 1) / TF_P_TILE;
-    int per_kv = (int)gridDim.x / a.KV;
+    const int grid = (int)gridDim.x;
+    // the most head groups (4, 2, 1) that still give every tile its own split
+    g.n_hg = 1;
+    if (G >= 4 && a.KV * n_tiles * 4 <= grid) g.n_hg = 4;
+    else if (G >= 2 && a.KV * n_tiles * 2 <= grid) g.n_hg = 2;
+    g.hpw = (G + g.n_hg - 1) / g.n_hg;
+    g.hpw = g.hpw <= 2 ? 2 : (g.hpw <= 4 ? 4 : 8);  // a power of two dividing 8
+    g.n_hg = (G + g.hpw - 1) / g.hpw;
+    g.wph = TF_P_WAVES / g.hpw;
+    int per_kv = grid / (a.KV * g.n_hg);
     per_kv = per_kv < 1 ? 1 : (per_kv > TF_P_MAX_SPLIT ? TF_P_MAX_SPLIT : per_kv);
     const int n0 = n_tiles < per_kv ? n_tiles : per_kv;
     g.tpw = (n_tiles + n0 - 1) / n0;
     g.n_ws = (n_tiles + g.tpw - 1) / g.tpw;  // every split holds at least one tile
     const int b = blockIdx.x;
-    g.active = b < a.KV * g.n_ws;
-    g.kh = g.active ? b / g.n_ws : 0;
+    g.active = b < a.KV * g.n_hg * g.n_ws;
+    const int kg = g.active ? b / g.n_ws : 0;
+    g.kh = kg / g.n_hg;
+    g.hg = kg % g.n_hg;
     g.ws = g.active ? b % g.n_ws : 0;
     g.t_begin = g.ws * g.tpw * TF_P_TILE;
     const int te = (g.ws + 1) * g.tpw * TF_P_TILE;
@@ -1311,9 +1331,17 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     }
     tf_p_stamp(a, sk, 1);
 
-    const bool own = wave < G;  // wave-uniform: this wave owns head `wave`
+    // this wave: head hd (valid if hh < hpw and hd < G), token slice sl
+    const int hh = wave / g.wph, sl = wave % g.wph;
+    const int hd = g.hg * g.hpw + hh;
+    const bool valid = hd < G;                   // wave-uniform
+    const int T = TF_P_TILE / g.wph;             // tokens per slice
+    const int DS = HD / g.wph;                   // dims per lane for the scores
+    const int ti = lane % T, ds = lane / T;      // score lane: token ti, dim slice ds
     float m = TF_P_NEG_BIG, l = 0.f, o0 = 0.f, o1 = 0.f;
     const float scale = a.scale;
+    float* cm = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES +
+                                         LA::P_BYTES);  // [wave][2 + HD]
     for (int it = 0; it < g.tpw; it++) {
         const int t0 = g.t_begin + it * TF_P_TILE;
         __syncthreads();  // the previous tile is consumed
@@ -1334,15 +1362,16 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         if (it + 1 < g.tpw) tf_p_attn_load(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
         __syncthreads();
-        if (!own || t0 >= g.t_end) continue;
-        // ---- scores: lane = token, four chains of 32 terms
-        const int t = t0 + lane;
+        if (!valid || t0 >= g.t_end) continue;
+        // ---- scores: lane (ti, ds) sums dims ds DS .. + DS of token sl T + ti
+        // in four chains; the WPH dim slices are then added across lanes
+        const int tok = sl * T + ti;
+        const int t = t0 + tok;
         const bool tv = t < g.t_end;
-        const uint16_t* krow = k_lds + lane * TF_P_KROW;
-        const float* qh = q_lds + wave * HD;
+        const uint16_t* krow = k_lds + tok * TF_P_KROW + ds * DS;
+        const float* qh = q_lds + hd * HD + ds * DS;
         float sa[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int dd = 0; dd < HD / 8; dd++) {
+        for (int dd = 0; dd < DS / 8; dd++) {
             const tf_u32x4 kw = *reinterpret_cast<const tf_u32x4*>(krow + 8 * dd);
             const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * dd);
             const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * dd + 4);
@@ -1357,20 +1386,27 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
             acc += qb.w * tf_h2f(kw.w >> 16);
             sa[dd & 3] = acc;
         }
-        const float sv = tv ? ((sa[0] + sa[1]) + (sa[2] + sa[3])) * scale : TF_P_NEG_BIG;
-        // ---- online softmax (wave = head)
+        float sd = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+        if (g.wph == 4) {  // slices ds = lane / 16: add lanes ^ 16, ^ 32
+            sd += tf_swap16(sd);
+            sd += __shfl_xor(sd, 32, 64);
+        } else if (g.wph == 2) {  // slices ds = lane / 32
+            sd += __shfl_xor(sd, 32, 64);
+        }
+        const float sv = tv ? sd * scale : TF_P_NEG_BIG;
+        // ---- online softmax over the slice's T tokens (each held by WPH lanes)
         const float m_new = fmaxf(m, tf_wave_max(sv));
         const float alpha = __expf(m - m_new);
         const float e = tv ? __expf(sv - m_new) : 0.f;
-        p_lds[wave * TF_P_TILE + lane] = e;
-        l = l * alpha + tf_group_sum<64>(e);
+        if (lane < T) p_lds[wave * TF_P_TILE + ti] = e;
+        l = l * alpha + tf_group_sum<64>(lane < T ? e : 0.f);
         m = m_new;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // ---- PV: lane = dims 2 lane, 2 lane + 1; four chains over the tokens
-        const int tlen = min(TF_P_TILE, g.t_end - t0);
-        const uint32_t* vcol = reinterpret_cast<const uint32_t*>(v_lds) + lane;
+        // ---- PV: lane = dims 2 lane, 2 lane + 1 over the slice's tokens, four chains
+        const int tlen = max(0, min(T, g.t_end - t0 - sl * T));
+        const uint32_t* vcol = reinterpret_cast<const uint32_t*>(v_lds) + (sl * T) * (HD / 2) + lane;
         const float* pw = p_lds + wave * TF_P_TILE;
         float c0[4] = {0.f, 0.f, 0.f, 0.f}, c1[4] = {0.f, 0.f, 0.f, 0.f};
         for (int tt = 0; tt < tlen; tt += 4) {
@@ -1386,9 +1422,37 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
         o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
     }
+    // ---- the WPH slices of a head: log-sum-exp merge, in slice order, by slice 0
+    if (g.wph > 1) {
+        float* cw = cm + wave * (2 + HD);
+        if (lane == 0) {
+            cw[0] = m;
+            cw[1] = l;
+        }
+        cw[2 + 2 * lane] = o0;
+        cw[3 + 2 * lane] = o1;
+        __syncthreads();
+        if (valid && sl == 0) {
+            float M = TF_P_NEG_BIG;
+            for (int j = 0; j < g.wph; j++) M = fmaxf(M, cm[(wave + j) * (2 + HD)]);
+            float Lt = 0.f, A0 = 0.f, A1 = 0.f;
+            for (int j = 0; j < g.wph; j++) {
+                const float* cj = cm + (wave + j) * (2 + HD);
+                const float w = __expf(cj[0] - M);
+                Lt = fmaf(w, cj[1], Lt);
+                A0 = fmaf(w, cj[2 + 2 * lane], A0);
+                A1 = fmaf(w, cj[3 + 2 * lane], A1);
+            }
+            m = M;
+            l = Lt;
+            o0 = A0;
+            o1 = A1;
+        }
+    }
+    const bool own = valid && sl == 0;  // wave-uniform: this wave carries head hd
     tf_p_stamp(a, sk, 2);
     // output group of this lane's dims: (head, 32-dim group) in Q8
-    const int og = ((g.kh * G + wave) * HD + 2 * lane) / 32;
+    const int og = ((g.kh * G + hd) * HD + 2 * lane) / 32;
     if (g.n_ws == 1) {
         if (own) {
             const float den = fmaxf(l, 1e-20f);
@@ -1396,10 +1460,11 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         return true;
     }
-    // ---- publish this split's partial; head w is merged by wave w of split
-    // workgroup w mod n_ws (the merges spread over the splits)
+    // ---- publish this split's partial; head h is merged by the wave that
+    // carries it in split workgroup h mod n_ws (the merges spread over the
+    // splits)
     if (own) {
-        unsigned long long* pp = tf_p_part(a, g.kh, wave, g.ws);
+        unsigned long long* pp = tf_p_part(a, g.kh, hd, g.ws);
         if (lane == 0) {
             tf_p_putf(pp, m, tp);
             tf_p_putf(pp + 1, l, tp);
@@ -1407,12 +1472,12 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         tf_p_putf(pp + 2 + 2 * lane, o0, tp);
         tf_p_putf(pp + 3 + 2 * lane, o1, tp);
     }
-    if (!own || wave % g.n_ws != g.ws) return true;
+    if (!own || hd % g.n_ws != g.ws) return true;
     // lane s holds split s's (m, l); lane = dims 2 lane, 2 lane + 1 for O.
     // M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O = sum_s w_s O_s
     // (attn/flash.cu:222-255), the O sum in split order.  The (m, l) words
     // and the O words of the first 16 splits are polled together.
-    const unsigned long long* pbase = tf_p_part(a, g.kh, wave, 0);
+    const unsigned long long* pbase = tf_p_part(a, g.kh, hd, 0);
     constexpr size_t PS = 2 + HD;
     constexpr int CH = 16;  // splits per O poll
     float A0 = 0.f, A1 = 0.f, Lt = 0.f, ws_ = 0.f;
