@@ -406,6 +406,96 @@ const float *tf_model_logits(const tf_model *m);
 uint16_t *tf_model_k_cache(const tf_model *m, int li);
 uint16_t *tf_model_v_cache(const tf_model *m, int li);
 
+/* ------------------------------------------------------------- GGUF reader */
+/* crates/gguf/src/reader.rs:29-169 GgufFile::open and its accessors: the file
+ * is memory-mapped read-only; tensor bytes are pointers into the mapping (host
+ * memory) for the caller to upload (cuda/load.rs:178-271).  Versions 2 and 3;
+ * the checks of the reference (magic, version, counts <= 1e6, strings
+ * <= 64 MiB and valid UTF-8, arrays <= 1e7 items, n_dims <= 4, known ggml
+ * types, every tensor inside the file) map to the TF_GGUF_ERR_* codes. */
+#define TF_GGUF_ERR_ARG 1          /* hipErrorInvalidValue: bad argument */
+#define TF_GGUF_ERR_IO 1001        /* GgufError::Io */
+#define TF_GGUF_ERR_MAGIC 1002     /* GgufError::BadMagic */
+#define TF_GGUF_ERR_VERSION 1003   /* GgufError::UnsupportedVersion */
+#define TF_GGUF_ERR_EOF 1004       /* GgufError::UnexpectedEof */
+#define TF_GGUF_ERR_MALFORMED 1005 /* GgufError::Malformed */
+#define TF_GGUF_ERR_TENSOR_TYPE 1006 /* GgufError::UnknownTensorType */
+#define TF_GGUF_ERR_VALUE_TYPE 1007  /* GgufError::UnknownValueType */
+#define TF_GGUF_ERR_UTF8 1008      /* GgufError::InvalidUtf8 */
+#define TF_GGUF_ERR_NOT_FOUND 1009 /* no such key / tensor (Option::None) */
+#define TF_GGUF_ERR_TYPE 1010      /* the value does not convert (Option::None) */
+
+/* value.rs:8-23 ValueType ids */
+#define TF_GGUF_U8 0
+#define TF_GGUF_I8 1
+#define TF_GGUF_U16 2
+#define TF_GGUF_I16 3
+#define TF_GGUF_U32 4
+#define TF_GGUF_I32 5
+#define TF_GGUF_F32 6
+#define TF_GGUF_BOOL 7
+#define TF_GGUF_STRING 8
+#define TF_GGUF_ARRAY 9
+#define TF_GGUF_U64 10
+#define TF_GGUF_I64 11
+#define TF_GGUF_F64 12
+
+typedef struct tf_gguf tf_gguf;
+
+/* types.rs:193-201 GgufTensorInfo (+ its data slice, reader.rs:201-205);
+ * dims past n_dims read 1; name lives as long as the handle. */
+typedef struct tf_gguf_tensor {
+    const char *name;
+    int type;
+    int n_dims;
+    uint64_t dims[4];
+    uint64_t offset; /* relative to the data section */
+    uint64_t nbytes; /* types.rs:178-189 nbytes of the element count */
+    const uint8_t *data;
+} tf_gguf_tensor;
+
+int tf_gguf_open(const char *path, tf_gguf **out);
+void tf_gguf_close(tf_gguf *g);
+uint32_t tf_gguf_version(const tf_gguf *g);
+/* reader.rs:143-149: header end aligned to general.alignment (default 32) */
+uint64_t tf_gguf_data_offset(const tf_gguf *g);
+uint64_t tf_gguf_file_size(const tf_gguf *g);
+int64_t tf_gguf_n_tensors(const tf_gguf *g);
+int tf_gguf_tensor_at(const tf_gguf *g, int64_t i, tf_gguf_tensor *out);
+/* reader.rs:196-198 tensor(name) */
+int tf_gguf_find_tensor(const tf_gguf *g, const char *name, tf_gguf_tensor *out);
+/* metadata: the value type id of key, -1 if absent */
+int tf_gguf_meta_type(const tf_gguf *g, const char *key);
+/* value.rs:72-106 as_u32 / as_u64 / as_f32 / as_str / as_bool (the same
+ * conversions; TF_GGUF_ERR_TYPE where those return None) */
+int tf_gguf_meta_u32(const tf_gguf *g, const char *key, uint32_t *out);
+int tf_gguf_meta_u64(const tf_gguf *g, const char *key, uint64_t *out);
+int tf_gguf_meta_f32(const tf_gguf *g, const char *key, float *out);
+int tf_gguf_meta_str(const tf_gguf *g, const char *key, const char **s, uint64_t *len);
+int tf_gguf_meta_bool(const tf_gguf *g, const char *key, int *out);
+/* No reference counterpart (its Value enum is matched directly): any signed
+ * or unsigned integer as int64, any float as f64, array item type and length,
+ * and array items as string or as number. */
+int tf_gguf_meta_i64(const tf_gguf *g, const char *key, int64_t *out);
+int tf_gguf_meta_f64(const tf_gguf *g, const char *key, double *out);
+int tf_gguf_meta_array(const tf_gguf *g, const char *key, int *item_type, uint64_t *n);
+int tf_gguf_meta_array_str(const tf_gguf *g, const char *key, uint64_t i, const char **s,
+                           uint64_t *len);
+int tf_gguf_meta_array_f64(const tf_gguf *g, const char *key, uint64_t i, double *out);
+/* types.rs:109-180 ggml type table: block size, bytes per block (0 for an
+ * unknown type) and the bytes of n elements. */
+int tf_ggml_block_size(int type);
+int tf_ggml_type_size(int type);
+uint64_t tf_ggml_nbytes(int type, uint64_t n_elements);
+/* config.rs:107-175 ModelConfig::from_gguf, the dense-decoder fields: the
+ * {arch}.embedding_length, block_count, attention.head_count,
+ * feed_forward_length keys are required; head_count_kv defaults to
+ * head_count, key_length to embedding_length / head_count (value_length must
+ * equal it), vocab_size to token_embd.weight dims[1], rope.freq_base to 1e4
+ * for llama and 1e6 otherwise, attention.layer_norm_rms_epsilon to 1e-6.
+ * max_seq is the caller's KV capacity. */
+int tf_gguf_model_config(const tf_gguf *g, int max_seq, tf_model_config *cfg);
+
 /* ------------------------------------------------------- integer diagnostics */
 /* No reference counterpart: these expose the exact integer stage of the GEMV
  * kernels (the same device code) so that the int32 sums can be checked

@@ -117,6 +117,29 @@ static const char* const k_symbols[] = {
     "tf_rope_neox",
     "tf_copy_kv_f16",
     "tf_argmax",
+    "tf_gguf_open",
+    "tf_gguf_close",
+    "tf_gguf_version",
+    "tf_gguf_data_offset",
+    "tf_gguf_file_size",
+    "tf_gguf_n_tensors",
+    "tf_gguf_tensor_at",
+    "tf_gguf_find_tensor",
+    "tf_gguf_meta_type",
+    "tf_gguf_meta_u32",
+    "tf_gguf_meta_u64",
+    "tf_gguf_meta_f32",
+    "tf_gguf_meta_str",
+    "tf_gguf_meta_bool",
+    "tf_gguf_meta_i64",
+    "tf_gguf_meta_f64",
+    "tf_gguf_meta_array",
+    "tf_gguf_meta_array_str",
+    "tf_gguf_meta_array_f64",
+    "tf_ggml_block_size",
+    "tf_ggml_type_size",
+    "tf_ggml_nbytes",
+    "tf_gguf_model_config",
     "tf_model_create",
     "tf_model_destroy",
     "tf_model_forward",

@@ -61,15 +61,92 @@ def _bind(lib):
 
 
 class DecodeModel:
-    """Greedy batch-1 decoder over caller-supplied synthetic weights.
+    """Greedy batch-1 decoder over caller-supplied weights.
 
     cfg: dict with n_layer, n_embd, n_ff, n_head, n_kv, head_dim, n_vocab,
-    rope_theta, rms_eps and max_seq.  layers: iterable of synth.qwen_layer()
-    dicts (consumed one at a time, so host memory holds one layer).
-    embedding: (raw Q6_K bytes [n_vocab, col_bytes], col_bytes), tied lm_head.
+    rope_theta, rms_eps and max_seq.  layers: iterable of per-layer dicts
+    (synth.qwen_layer() or the GGUF loader; consumed one at a time, so host
+    memory holds one layer).  A matrix is (bytes [n_cols, col_bytes],
+    col_bytes) in the synthetic Q4_K_M placement (attn_v Q6_K, ffn_down Q6_K
+    when down_q6k), or (bytes, col_bytes, ggml type).  Biases may be None.
+    embedding: the token table (a matrix, Q6_K unless typed); output: a
+    separate lm_head (None: tied to the embedding); output_norm: the final
+    RMSNorm weight (None: ones).
     """
 
-    def __init__(self, cfg: dict, layers, embedding):
+    @classmethod
+    def from_gguf(cls, path, max_seq: int) -> "DecodeModel":
+        """cuda/load.rs:166-420 for a dense Qwen2/Llama Q4_K_M file: the
+        config from the metadata (config.rs:107-175), blk.{i}.* tensors by
+        the reference's names, a tied lm_head when output.weight is absent."""
+        from .gguf import GGML_F16, GGML_F32, GGML_Q4_K, GGML_Q6_K, GgufFile, ggml_nbytes
+
+        f = GgufFile(path)
+        try:
+            cfg = f.model_config(max_seq)
+
+            def mat(name, n_rows):
+                t = f.tensor(name)
+                if t is None:
+                    raise ValueError(f"{path}: missing tensor {name}")
+                if t.type not in (GGML_Q4_K, GGML_Q6_K):
+                    raise ValueError(f"{name}: ggml type {t.type} is not on the decode path "
+                                     "(Q4_K and Q6_K are)")
+                if t.n_dims != 2 or t.dims[0] != n_rows:
+                    raise ValueError(f"{name}: dims {list(t.dims[:t.n_dims])}, expected "
+                                     f"[{n_rows}, n]")
+                cb = ggml_nbytes(t.type, t.dims[0])
+                return f.tensor_data(t).reshape(int(t.dims[1]), cb), cb, t.type
+
+            def vec(name, n, required=True):
+                t = f.tensor(name)
+                if t is None:
+                    if required:
+                        raise ValueError(f"{path}: missing tensor {name}")
+                    return None
+                raw = f.tensor_data(t)
+                if t.type == GGML_F32:
+                    v = raw.view(np.float32)
+                elif t.type == GGML_F16:
+                    v = raw.view(np.float16).astype(np.float32)
+                else:
+                    raise ValueError(f"{name}: ggml type {t.type}, expected F32/F16")
+                if v.size != n:
+                    raise ValueError(f"{name}: {v.size} values, expected {n}")
+                return v
+
+            c = cfg
+            qd, kvd = c["n_head"] * c["head_dim"], c["n_kv"] * c["head_dim"]
+
+            def layers():
+                for i in range(c["n_layer"]):
+                    p = f"blk.{i}"
+                    ffn_norm = vec(f"{p}.ffn_norm.weight", c["n_embd"], required=False)
+                    if ffn_norm is None:
+                        ffn_norm = vec(f"{p}.post_attention_norm.weight", c["n_embd"])
+                    yield {
+                        "attn_norm": vec(f"{p}.attn_norm.weight", c["n_embd"]),
+                        "ffn_norm": ffn_norm,
+                        "wq": mat(f"{p}.attn_q.weight", c["n_embd"]),
+                        "wk": mat(f"{p}.attn_k.weight", c["n_embd"]),
+                        "wv": mat(f"{p}.attn_v.weight", c["n_embd"]),
+                        "bq": vec(f"{p}.attn_q.bias", qd, required=False),
+                        "bk": vec(f"{p}.attn_k.bias", kvd, required=False),
+                        "bv": vec(f"{p}.attn_v.bias", kvd, required=False),
+                        "wo": mat(f"{p}.attn_output.weight", qd),
+                        "gate": mat(f"{p}.ffn_gate.weight", c["n_embd"]),
+                        "up": mat(f"{p}.ffn_up.weight", c["n_embd"]),
+                        "down": mat(f"{p}.ffn_down.weight", c["n_ff"]),
+                    }
+
+            emb = mat("token_embd.weight", c["n_embd"])
+            out = mat("output.weight", c["n_embd"]) if f.tensor("output.weight") else None
+            return cls(cfg, layers(), emb, output=out,
+                       output_norm=vec("output_norm.weight", c["n_embd"]))
+        finally:
+            f.close()
+
+    def __init__(self, cfg: dict, layers, embedding, output=None, output_norm=None):
         self.lib = capi.load()
         _bind(self.lib)
         self.cfg = dict(cfg)
@@ -81,22 +158,25 @@ class DecodeModel:
             t = carr[li]
             t.attn_norm = self._f32(L["attn_norm"])
             t.ffn_norm = self._f32(L["ffn_norm"])
-            t.wq = self._q4(L["wq"], c["n_embd"])
-            t.wk = self._q4(L["wk"], c["n_embd"])
-            t.wv = self._q6(L["wv"], c["n_embd"], compact=False)
-            t.bq, t.bk, t.bv = self._f32(L["bq"]), self._f32(L["bk"]), self._f32(L["bv"])
-            t.wo = self._q4(L["wo"], c["n_head"] * c["head_dim"])
-            t.gate = self._q4(L["gate"], c["n_embd"])
-            t.up = self._q4(L["up"], c["n_embd"])
-            t.down = (self._q6(L["down"], c["n_ff"], compact=True) if L["down_q6k"]
-                      else self._q4(L["down"], c["n_ff"]))
-        self.embd = self._q6(embedding, c["n_embd"], compact=True)
-        self.output_norm = self._f32(np.ones(c["n_embd"], np.float32))
+            t.wq = self._mat(L["wq"], c["n_embd"], TYPE_Q4_K)
+            t.wk = self._mat(L["wk"], c["n_embd"], TYPE_Q4_K)
+            t.wv = self._mat(L["wv"], c["n_embd"], TYPE_Q6_K, compact=False)
+            t.bq, t.bk, t.bv = (self._f32(L.get(k)) for k in ("bq", "bk", "bv"))
+            t.wo = self._mat(L["wo"], c["n_head"] * c["head_dim"], TYPE_Q4_K)
+            t.gate = self._mat(L["gate"], c["n_embd"], TYPE_Q4_K)
+            t.up = self._mat(L["up"], c["n_embd"], TYPE_Q4_K)
+            t.down = self._mat(L["down"], c["n_ff"],
+                               TYPE_Q6_K if L.get("down_q6k") else TYPE_Q4_K, compact=True)
+        self.embd = self._mat(embedding, c["n_embd"], TYPE_Q6_K, compact=True)
+        self.out = (self.embd if output is None
+                    else self._mat(output, c["n_embd"], TYPE_Q6_K, compact=True))
+        self.output_norm = self._f32(np.ones(c["n_embd"], np.float32) if output_norm is None
+                                     else output_norm)
         cc = TfModelConfig(c["n_layer"], c["n_embd"], c["n_ff"], c["n_head"], c["n_kv"],
                            c["head_dim"], c["n_vocab"], c["max_seq"], c["rope_theta"],
                            c["rms_eps"])
         h = C.c_void_p()
-        rc = self.lib.tf_model_create(C.byref(cc), carr, C.byref(self.embd), C.byref(self.embd),
+        rc = self.lib.tf_model_create(C.byref(cc), carr, C.byref(self.embd), C.byref(self.out),
                                       self.output_norm, C.byref(h))
         if rc != 0:
             raise capi.HipError(f"tf_model_create returned {rc}")
@@ -105,12 +185,28 @@ class DecodeModel:
 
     # ---------------------------------------------------------------- upload
     def _dev(self, a: np.ndarray) -> torch.Tensor:
-        t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+        a = np.ascontiguousarray(a)
+        if not a.flags.writeable:  # a view of a mapped file: copy (one matrix at a time)
+            a = a.copy()
+        t = torch.from_numpy(a).to("cuda")
         self._keep.append(t)
         return t
 
-    def _f32(self, a) -> int:
+    def _f32(self, a) -> int | None:
+        if a is None:
+            return None
         return self._dev(np.asarray(a, np.float32)).data_ptr()
+
+    def _mat(self, wm, n_rows, default_type, compact: bool = False) -> TfMat:
+        """A matrix (bytes, col_bytes[, ggml type]); Q6_K ones the Q8 path reads
+        (compact=True) also get the 212-byte repack."""
+        typ = wm[2] if len(wm) > 2 else default_type
+        w = (wm[0], wm[1])
+        if typ == TYPE_Q4_K:
+            return self._q4(w, n_rows)
+        if typ == TYPE_Q6_K:
+            return self._q6(w, n_rows, compact)
+        raise ValueError(f"ggml type {typ} is not supported on the decode path")
 
     def _q4(self, wm, n_rows) -> TfMat:
         w, cb = wm
