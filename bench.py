@@ -117,6 +117,11 @@ def kernel_table(iters):
         ("cfg1c_q4k_qkv_2048x2560", lambda: B.case_q4k_qkv(2048, 2048, 256, 3, iters)),
         ("lm_head_q6k_2048x151936", lambda: B.case_q6k(2048, 151936, 6, max(10, iters // 4),
                                                        "tf_gemv_q6k_compact_q8", 0)),
+        # Qwen2.5-0.5B Q4_K_M widths (K = 896 is not a multiple of 256)
+        ("q8_0_lm_head_896x151936", lambda: B.case_block32("q8_0", 896, 151936, 8,
+                                                           max(10, iters // 4))),
+        ("q5_0_ffn_896x4864", lambda: B.case_block32("q5_0", 896, 4864, 9, iters)),
+        ("q5_0_qkv_896x1152", lambda: B.case_q5_0_qkv(896, 896, 128, 10, iters)),
     ]
     for L in (512, 4096, 32768):
         rows.append((f"cfg2_flash_L{L}_split8", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters, 8)))
@@ -220,6 +225,8 @@ def main():
                     help="decode kernel sequence (tf_model_set_path); default: the library's")
     ap.add_argument("--only-roofline", action="store_true",
                     help="run only the copy calibration and the roofline kernel (for counter runs)")
+    ap.add_argument("--only-kernels", action="store_true",
+                    help="run only the per-kernel table (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode path is single-GPU; "
@@ -237,6 +244,9 @@ def main():
         r = kernel_roofline(args.kernel_iters)
         print(json.dumps({"kernel": ROOFLINE_KERNEL, "bytes": int(r["bytes"]),
                           "us_b2b": round(r["b2b_us"], 3), "us_single": round(r["per_us"], 3)}))
+        return
+    if args.only_kernels:
+        print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
         return
     cfg = dict(synth.QWEN25_3B)
     steps = max(2, args.steps)

@@ -164,6 +164,78 @@ int tf_gemv_q6k_f32(const uint8_t *w, const float *x, float *out, int n_rows,
 int tf_q6k_compact_repack(const uint8_t *raw, uint8_t *dst, int n_rows,
                           int n_cols, int col_bytes, tf_stream_t stream);
 
+/* ------------------------------------------------ Q8_0 / Q5_0 GEMVs
+ * 32-value block formats (the tensors of width 896, not a multiple of 256,
+ * in Qwen2.5-0.5B Q4_K_M files).  Q8_0 block = f16 d | int8 qs[32] (34 B);
+ * Q5_0 block = f16 d | u32 qh | u8 qs[16] (22 B), value = d * (code - 16).
+ * n_rows % 32 == 0; column j holds n_rows/32 blocks at w + j*col_bytes;
+ * weights 2-byte aligned.  Q8_0 x Q8 uses a faster pair layout when
+ * n_rows/32 is even and the columns are 4-byte aligned.  The f32
+ * activations are 16-byte aligned (8 for the Q8_0 entry points that
+ * quantize); the f32 formats stage at most 16384 rows.            */
+
+/* kernels/gemv.cu:1614 gemv_q8_0_global (matmul.rs:142-302, 305-330):
+ * out[j] = sum over blocks of dw * xd * int8 dot [+res] [+bias]. */
+int tf_gemv_q8_0_q8(const uint8_t *w, const int8_t *xq, const float *xd,
+                    float *out, int n_rows, int n_cols, int col_bytes,
+                    int use_bias, const float *bias, int use_res,
+                    const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:1585 gemv_q8_0 (matmul.rs:346-412 gemv_baseline): as
+ * tf_gemv_q8_0_q8 with x f32, quantized in LDS bit-identically to
+ * tf_quantize_q8. */
+int tf_gemv_q8_0_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                     int n_cols, int col_bytes, int use_bias, const float *bias,
+                     int use_res, const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:1725 gemv_q8_0_global_splitk (matmul.rs:225-283):
+ * partial[s*n_cols + j] over blocks [floor(nb*s/n_split),
+ * floor(nb*(s+1)/n_split)), combined by tf_gemv_splitk_reduce.
+ * 1 <= n_split <= 64. */
+int tf_gemv_q8_0_q8_splitk(const uint8_t *w, const int8_t *xq,
+                           const float *xd, float *partial, int n_rows,
+                           int n_cols, int col_bytes, int n_split,
+                           tf_stream_t stream);
+
+/* kernels/gemv.cu:2117 gemv_q8_0_splitk (matmul.rs:416-500 gemv_splitk):
+ * f32 activation, fp32 products d * qs[t] * x[t]; partials as above. */
+int tf_gemv_q8_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                            int n_rows, int n_cols, int col_bytes,
+                            int n_split, tf_stream_t stream);
+
+/* kernels/gemv.cu:1751 gemv_q5_0 (matmul.rs:346-412): fp32 products
+ * d * (code - 16) * x [+res] [+bias]. */
+int tf_gemv_q5_0_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                     int n_cols, int col_bytes, int use_bias, const float *bias,
+                     int use_res, const float *residual, tf_stream_t stream);
+
+/* kernels/gemv.cu:2158 gemv_q5_0_splitk (matmul.rs:416-500). */
+int tf_gemv_q5_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                            int n_rows, int n_cols, int col_bytes,
+                            int n_split, tf_stream_t stream);
+
+/* kernels/gemv.cu:2298 gemv_q5_0_qk (matmul.rs:786-840): q = Wq x (+bq),
+ * k = Wk x (+bk) in one launch (also gate+up); both Q5_0, same K. */
+int tf_gemv_q5_0_qk(const uint8_t *wq, const uint8_t *wk, const float *x,
+                    float *q, float *k, int n_rows, int n_q, int n_k,
+                    int col_bytes, int use_bias, const float *bq,
+                    const float *bk, tf_stream_t stream);
+
+/* kernels/gemv.cu:2710 gemv_q5_0_qkv (matmul.rs:1087-1130). */
+int tf_gemv_q5_0_qkv(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
+                     const float *x, float *q, float *k, float *v, int n_rows,
+                     int n_q, int n_k, int n_v, int col_bytes, int use_bias,
+                     const float *bq, const float *bk, const float *bv,
+                     tf_stream_t stream);
+
+/* kernels/gemv.cu:2766 gemv_q8_0_qkv (matmul.rs:1003-1080): x f32,
+ * quantized in LDS as tf_quantize_q8, then as tf_gemv_q8_0_q8. */
+int tf_gemv_q8_0_qkv(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
+                     const float *x, float *q, float *k, float *v, int n_rows,
+                     int n_q, int n_k, int n_v, int col_bytes, int use_bias,
+                     const float *bq, const float *bk, const float *bv,
+                     tf_stream_t stream);
+
 /* ---------------------------------------------------- split-KV flash decode */
 
 /* kernels/attn/flash.cu:16 attn_flash_partial (layer.rs:2040-2103), n_q = 1.

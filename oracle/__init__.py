@@ -214,6 +214,77 @@ def gemv_q6k_f32_f64(w, x, n_rows, n_cols, col_bytes):
     return out, absn
 
 
+# ------------------------------------------------------ Q8_0 / Q5_0 GEMVs
+
+def gemv_q8_0_q8(w, xq, xd, n_rows, n_cols, col_bytes, bias=None, use_res=0,
+                 residual=None, out=None):
+    out = _f32(n_cols) if out is None else np.array(out, np.float32)
+    lib().or_gemv_q8_0_q8(_p(w), _p(xq), _p(xd), _p(out), n_rows, n_cols, col_bytes,
+                          int(bias is not None), _p(bias), use_res,
+                          _p(_res(use_res, residual, out)))
+    return out
+
+
+def gemv_q8_0_q8_splitk(w, xq, xd, n_rows, n_cols, col_bytes, n_split):
+    part = _f32(n_split * n_cols)
+    lib().or_gemv_q8_0_q8_splitk(_p(w), _p(xq), _p(xd), _p(part), n_rows, n_cols,
+                                 col_bytes, n_split)
+    return part
+
+
+def gemv_q8_0_f32_splitk(w, x, n_rows, n_cols, col_bytes, n_split):
+    part = _f32(n_split * n_cols)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemv_q8_0_f32_splitk(_p(w), _p(x), _p(part), n_rows, n_cols, col_bytes,
+                                  n_split)
+    return part
+
+
+def gemv_q5_0_f32(w, x, n_rows, n_cols, col_bytes, bias=None, use_res=0, residual=None,
+                  out=None):
+    out = _f32(n_cols) if out is None else np.array(out, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemv_q5_0_f32(_p(w), _p(x), _p(out), n_rows, n_cols, col_bytes,
+                           int(bias is not None), _p(bias), use_res,
+                           _p(_res(use_res, residual, out)))
+    return out
+
+
+def gemv_q5_0_f32_splitk(w, x, n_rows, n_cols, col_bytes, n_split):
+    part = _f32(n_split * n_cols)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemv_q5_0_f32_splitk(_p(w), _p(x), _p(part), n_rows, n_cols, col_bytes,
+                                  n_split)
+    return part
+
+
+def q8_0_block_sums(w, xq, n_rows, n_cols, col_bytes):
+    sums = np.zeros(n_cols * (n_rows // 32), np.int32)
+    lib().or_q8_0_block_sums(_p(w), _p(xq), _p(sums), n_rows, n_cols, col_bytes)
+    return sums.reshape(n_cols, -1)
+
+
+def gemv_q8_0_q8_f64(w, xq, xd, n_rows, n_cols, col_bytes):
+    out, absn = np.zeros(n_cols, np.float64), np.zeros(n_cols, np.float64)
+    lib().or_gemv_q8_0_q8_f64(_p(w), _p(xq), _p(xd), _p(out), _p(absn), n_rows, n_cols,
+                              col_bytes)
+    return out, absn
+
+
+def gemv_q8_0_f32_f64(w, x, n_rows, n_cols, col_bytes):
+    out, absn = np.zeros(n_cols, np.float64), np.zeros(n_cols, np.float64)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemv_q8_0_f32_f64(_p(w), _p(x), _p(out), _p(absn), n_rows, n_cols, col_bytes)
+    return out, absn
+
+
+def gemv_q5_0_f32_f64(w, x, n_rows, n_cols, col_bytes):
+    out, absn = np.zeros(n_cols, np.float64), np.zeros(n_cols, np.float64)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemv_q5_0_f32_f64(_p(w), _p(x), _p(out), _p(absn), n_rows, n_cols, col_bytes)
+    return out, absn
+
+
 # ------------------------------------------------------------------ attention
 
 def flash_partial(q, k_cache, v_cache, n_head, n_kv, head_dim, pos0, n_split, scale):

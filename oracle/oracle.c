@@ -608,6 +608,204 @@ void or_gemv_q6k_f32_f64(const uint8_t *w, const float *x, double *out,
     }
 }
 
+/* ------------------------------------------------------- Q8_0 / Q5_0 */
+
+static int q5_0_value(const uint8_t *blk, int v) {
+    const uint32_t qh = rdu32(blk + 2);
+    const uint8_t *qs = blk + 6;
+    const int t = v & 15;
+    int q;
+    if (v < 16) q = (qs[t] & 0x0F) | (int)(((qh >> t) << 4) & 0x10u);
+    else q = (qs[t] >> 4) | (int)((qh >> (t + 12)) & 0x10u);
+    return q - 16;
+}
+
+/* dot_q8_0_col_q8_range for one lane's blocks [bi0 + lane : bi1 : 32] */
+static float q8_0_lane(const uint8_t *col, const int8_t *xq, const float *xd,
+                       int bi0, int bi1, int lane) {
+    float acc = 0.f;
+    for (int bi = bi0 + lane; bi < bi1; bi += 32) {
+        const uint8_t *base = col + (size_t)bi * 34;
+        const float dw = or_f16_to_f32(rd16(base));
+        int32_t sum = 0;
+        for (int t = 0; t < 32; t += 4)
+            sum = dp4a(rd32(base + 2 + t), rd32(xq + bi * 32 + t), sum);
+        acc += dw * xd[bi] * (float)sum;
+    }
+    return acc;
+}
+
+void or_gemv_q8_0_q8(const uint8_t *w, const int8_t *xq, const float *xd,
+                     float *out, int n_rows, int n_cols, int col_bytes,
+                     int use_bias, const float *bias, int use_res,
+                     const float *residual) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++) {
+        const uint8_t *col = w + (size_t)j * col_bytes;
+        float acc[32];
+        for (int lane = 0; lane < 32; lane++) acc[lane] = q8_0_lane(col, xq, xd, 0, nb, lane);
+        out[j] = epilogue(warp_sum32(acc), j, out, use_bias, bias, use_res, residual);
+    }
+}
+
+void or_gemv_q8_0_q8_splitk(const uint8_t *w, const int8_t *xq,
+                            const float *xd, float *partial, int n_rows,
+                            int n_cols, int col_bytes, int n_split) {
+    const int nb = n_rows / 32;
+    for (int s = 0; s < n_split; s++) {
+        const int bi0 = nb * s / n_split, bi1 = nb * (s + 1) / n_split;
+        for (int j = 0; j < n_cols; j++) {
+            float acc[32];
+            for (int lane = 0; lane < 32; lane++)
+                acc[lane] = q8_0_lane(w + (size_t)j * col_bytes, xq, xd, bi0, bi1, lane);
+            partial[(size_t)s * n_cols + j] = bi0 >= bi1 ? 0.f : warp_sum32(acc);
+        }
+    }
+}
+
+void or_gemv_q8_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                             int n_rows, int n_cols, int col_bytes,
+                             int n_split) {
+    const int nb = n_rows / 32;
+    for (int s = 0; s < n_split; s++) {
+        const int bi0 = nb * s / n_split, bi1 = nb * (s + 1) / n_split;
+        for (int j = 0; j < n_cols; j++) {
+            const uint8_t *col = w + (size_t)j * col_bytes;
+            float acc[32];
+            for (int lane = 0; lane < 32; lane++) {
+                float a = 0.f;
+                for (int bi = bi0 + lane; bi < bi1; bi += 32) {
+                    const uint8_t *base = col + (size_t)bi * 34;
+                    const float d = or_f16_to_f32(rd16(base));
+                    const int8_t *qs = (const int8_t *)(base + 2);
+                    for (int t = 0; t < 32; t++) a += (float)qs[t] * d * x[bi * 32 + t];
+                }
+                acc[lane] = a;
+            }
+            partial[(size_t)s * n_cols + j] = bi0 >= bi1 ? 0.f : warp_sum32(acc);
+        }
+    }
+}
+
+/* one lane of gemv_q5_0 / gemv_q5_0_splitk over blocks [bi0 + lane : bi1 : 32] */
+static float q5_0_lane(const uint8_t *col, const float *x, int bi0, int bi1, int lane) {
+    float acc = 0.f;
+    for (int bi = bi0 + lane; bi < bi1; bi += 32) {
+        const uint8_t *base = col + (size_t)bi * 22;
+        const float d = or_f16_to_f32(rd16(base));
+        const uint32_t qh = rdu32(base + 2);
+        const uint8_t *qs = base + 6;
+        const float *xs = x + bi * 32;
+        for (int t = 0; t < 16; t++) {
+            const int x0 = (qs[t] & 0x0F) | (int)(((qh >> t) << 4) & 0x10u);
+            const int x1 = (qs[t] >> 4) | (int)((qh >> (t + 12)) & 0x10u);
+            acc += (float)(x0 - 16) * d * xs[t];
+            acc += (float)(x1 - 16) * d * xs[16 + t];
+        }
+    }
+    return acc;
+}
+
+void or_gemv_q5_0_f32(const uint8_t *w, const float *x, float *out,
+                      int n_rows, int n_cols, int col_bytes, int use_bias,
+                      const float *bias, int use_res, const float *residual) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++) {
+        float acc[32];
+        for (int lane = 0; lane < 32; lane++)
+            acc[lane] = q5_0_lane(w + (size_t)j * col_bytes, x, 0, nb, lane);
+        out[j] = epilogue(warp_sum32(acc), j, out, use_bias, bias, use_res, residual);
+    }
+}
+
+void or_gemv_q5_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                             int n_rows, int n_cols, int col_bytes,
+                             int n_split) {
+    const int nb = n_rows / 32;
+    for (int s = 0; s < n_split; s++) {
+        const int bi0 = nb * s / n_split, bi1 = nb * (s + 1) / n_split;
+        for (int j = 0; j < n_cols; j++) {
+            float acc[32];
+            for (int lane = 0; lane < 32; lane++)
+                acc[lane] = q5_0_lane(w + (size_t)j * col_bytes, x, bi0, bi1, lane);
+            partial[(size_t)s * n_cols + j] = bi0 >= bi1 ? 0.f : warp_sum32(acc);
+        }
+    }
+}
+
+void or_q8_0_block_sums(const uint8_t *w, const int8_t *xq, int32_t *sums,
+                        int n_rows, int n_cols, int col_bytes) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++)
+        for (int bi = 0; bi < nb; bi++) {
+            const int8_t *qs = (const int8_t *)(w + (size_t)j * col_bytes + (size_t)bi * 34 + 2);
+            int32_t s = 0;
+            for (int t = 0; t < 32; t++) s += (int32_t)qs[t] * xq[bi * 32 + t];
+            sums[(size_t)j * nb + bi] = s;
+        }
+}
+
+void or_gemv_q8_0_q8_f64(const uint8_t *w, const int8_t *xq, const float *xd,
+                         double *out, double *rowabs, int n_rows, int n_cols,
+                         int col_bytes) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++) {
+        double y = 0.0, a = 0.0;
+        for (int bi = 0; bi < nb; bi++) {
+            const uint8_t *base = w + (size_t)j * col_bytes + (size_t)bi * 34;
+            const double dw = or_f16_to_f32(rd16(base));
+            const int8_t *qs = (const int8_t *)(base + 2);
+            for (int t = 0; t < 32; t++) {
+                const double v = dw * (double)xd[bi] * qs[t] * xq[bi * 32 + t];
+                y += v;
+                a += fabs(v);
+            }
+        }
+        out[j] = y;
+        if (rowabs) rowabs[j] = a;
+    }
+}
+
+void or_gemv_q8_0_f32_f64(const uint8_t *w, const float *x, double *out,
+                          double *rowabs, int n_rows, int n_cols,
+                          int col_bytes) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++) {
+        double y = 0.0, a = 0.0;
+        for (int bi = 0; bi < nb; bi++) {
+            const uint8_t *base = w + (size_t)j * col_bytes + (size_t)bi * 34;
+            const double d = or_f16_to_f32(rd16(base));
+            for (int t = 0; t < 32; t++) {
+                const double v = d * (int8_t)base[2 + t] * (double)x[bi * 32 + t];
+                y += v;
+                a += fabs(v);
+            }
+        }
+        out[j] = y;
+        if (rowabs) rowabs[j] = a;
+    }
+}
+
+void or_gemv_q5_0_f32_f64(const uint8_t *w, const float *x, double *out,
+                          double *rowabs, int n_rows, int n_cols,
+                          int col_bytes) {
+    const int nb = n_rows / 32;
+    for (int j = 0; j < n_cols; j++) {
+        double y = 0.0, a = 0.0;
+        for (int bi = 0; bi < nb; bi++) {
+            const uint8_t *base = w + (size_t)j * col_bytes + (size_t)bi * 22;
+            const double d = or_f16_to_f32(rd16(base));
+            for (int v = 0; v < 32; v++) {
+                const double t = d * q5_0_value(base, v) * (double)x[bi * 32 + v];
+                y += t;
+                a += fabs(t);
+            }
+        }
+        out[j] = y;
+        if (rowabs) rowabs[j] = a;
+    }
+}
+
 /* -------------------------------------------------------------- flash decode */
 
 #define OR_ATTN_TILE 64

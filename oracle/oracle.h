@@ -112,6 +112,53 @@ void or_gemv_q6k_f32_f64(const uint8_t *w, const float *x, double *out,
                          double *rowabs, int n_rows, int n_cols,
                          int col_bytes);
 
+/* ------------------------------------------------ Q8_0 / Q5_0 GEMVs
+ * Q8_0 block (32 values, 34 bytes): f16 d | int8 qs[32]; value t = d*qs[t].
+ * Q5_0 block (32 values, 22 bytes): f16 d | u32 qh | u8 qs[16]; value t < 16
+ * = d*((qs[t] & 15 | bit t of qh << 4) - 16), value 16+t = d*((qs[t] >> 4 |
+ * bit 16+t of qh << 4) - 16).  A column holds floor(n_rows/32) blocks.    */
+
+/* kernels/gemv.cu:1558-1582 dot_q8_0_col_q8_range + :1614-1635
+ * gemv_q8_0_global: per lane acc += dw*xd[bi]*(float)isum over blocks
+ * bi = lane, lane+32, ..., warp_sum, then [+res] [+bias]. */
+void or_gemv_q8_0_q8(const uint8_t *w, const int8_t *xq, const float *xd,
+                     float *out, int n_rows, int n_cols, int col_bytes,
+                     int use_bias, const float *bias, int use_res,
+                     const float *residual);
+/* kernels/gemv.cu:1725-1749 gemv_q8_0_global_splitk: partial[s*n_cols+j]
+ * over blocks [floor(nb*s/n_split), floor(nb*(s+1)/n_split)). */
+void or_gemv_q8_0_q8_splitk(const uint8_t *w, const int8_t *xq,
+                            const float *xd, float *partial, int n_rows,
+                            int n_cols, int col_bytes, int n_split);
+/* kernels/gemv.cu:2117-2156 gemv_q8_0_splitk: f32 activation, fp32
+ * products acc += (float)qs[t]*d*x[t] in block order per lane. */
+void or_gemv_q8_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                             int n_rows, int n_cols, int col_bytes,
+                             int n_split);
+/* kernels/gemv.cu:1751-1804 gemv_q5_0 (and :2268-2296 dot_q5_0_col_xs):
+ * acc += (float)(q-16)*d*x[t] for t = 0..15, low then high half. */
+void or_gemv_q5_0_f32(const uint8_t *w, const float *x, float *out,
+                      int n_rows, int n_cols, int col_bytes, int use_bias,
+                      const float *bias, int use_res, const float *residual);
+/* kernels/gemv.cu:2158-2200 gemv_q5_0_splitk */
+void or_gemv_q5_0_f32_splitk(const uint8_t *w, const float *x, float *partial,
+                             int n_rows, int n_cols, int col_bytes,
+                             int n_split);
+/* Exact int32 sums of each Q8_0 block against the Q8 activation:
+ * sums[j*nb + bi]. */
+void or_q8_0_block_sums(const uint8_t *w, const int8_t *xq, int32_t *sums,
+                        int n_rows, int n_cols, int col_bytes);
+/* fp64 truth of the three products (rowabs as above). */
+void or_gemv_q8_0_q8_f64(const uint8_t *w, const int8_t *xq, const float *xd,
+                         double *out, double *rowabs, int n_rows, int n_cols,
+                         int col_bytes);
+void or_gemv_q8_0_f32_f64(const uint8_t *w, const float *x, double *out,
+                          double *rowabs, int n_rows, int n_cols,
+                          int col_bytes);
+void or_gemv_q5_0_f32_f64(const uint8_t *w, const float *x, double *out,
+                          double *rowabs, int n_rows, int n_cols,
+                          int col_bytes);
+
 /* kernels/attn/flash.cu:16-116 attn_flash_partial (n_q = 1, 128 threads) */
 void or_flash_partial(const float *q, const uint16_t *k_cache,
                       const uint16_t *v_cache, float *partial, int n_head,

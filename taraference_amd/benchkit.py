@@ -8,7 +8,7 @@ stream the kernels run on (torch's current stream, handed to the library):
   - back-to-back: one event pair around a burst of launches.
 Algorithmic bytes per launch follow the reference GGUF block sizes (Q4_K
 144 B, Q6_K 210 B per 256 weights, even where the 212-byte compact copy is
-read), plus the activation once and the output once (twice with an in-place
+read; Q8_0 34 B and Q5_0 22 B per 32 weights), plus the activation once and the output once (twice with an in-place
 residual).
 """
 from __future__ import annotations
@@ -176,6 +176,59 @@ def case_q6k(n_rows, n_cols, seed, iters, entry="tf_gemv_q6k_down_splitk", use_r
     per, b2b = time_launches(launch, len(ws), iters)
     alg = n_cols * (n_rows // 256) * 210 + n_rows + n_rows // 8 + 4 * n_cols * (2 if use_res == 2 else 1)
     return dict(per_us=per, b2b_us=b2b, bytes=alg)
+
+
+def case_block32(fmt, n_rows, n_cols, seed, iters, entry=None):
+    """Q8_0 x Q8 (tf_gemv_q8_0_q8) or Q5_0 x f32 (tf_gemv_q5_0_f32)."""
+    rng = np.random.default_rng(seed)
+    mk = synth.q8_0_matrix if fmt == "q8_0" else synth.q5_0_matrix
+    w, cb = mk(rng, n_rows, n_cols)
+    ws = _copies(w, w.nbytes)
+    x = _dev(synth.activation(rng, n_rows))
+    xq, xd = _q8(x)
+    out = torch.empty(n_cols, device="cuda")
+    lib = capi.load()
+    if fmt == "q8_0":
+        def launch(i, s):
+            lib.tf_gemv_q8_0_q8(ws[i].data_ptr(), xq.data_ptr(), xd.data_ptr(), out.data_ptr(),
+                                n_rows, n_cols, cb, 0, None, 0, None, s)
+        act = n_rows + n_rows // 8
+    else:
+        def launch(i, s):
+            lib.tf_gemv_q5_0_f32(ws[i].data_ptr(), x.data_ptr(), out.data_ptr(), n_rows,
+                                 n_cols, cb, 0, None, 0, None, s)
+        act = 4 * n_rows
+    per, b2b = time_launches(launch, len(ws), iters)
+    return dict(per_us=per, b2b_us=b2b, bytes=n_cols * cb + act + 4 * n_cols)
+
+
+def case_q5_0_qkv(n_rows, n_q, n_kv, seed, iters):
+    rng = np.random.default_rng(seed)
+    wq, cb = synth.q5_0_matrix(rng, n_rows, n_q)
+    wk, _ = synth.q5_0_matrix(rng, n_rows, n_kv)
+    wv, _ = synth.q5_0_matrix(rng, n_rows, n_kv)
+    total = wq.nbytes + wk.nbytes + wv.nbytes
+    qs = _copies(wq, total)
+    ks = [_dev(wk)]
+    ks += [ks[0].clone() for _ in range(len(qs) - 1)]
+    vs = [_dev(wv)]
+    vs += [vs[0].clone() for _ in range(len(qs) - 1)]
+    x = _dev(synth.activation(rng, n_rows))
+    q = torch.empty(n_q, device="cuda")
+    k = torch.empty(n_kv, device="cuda")
+    v = torch.empty(n_kv, device="cuda")
+    bq = torch.zeros(n_q, device="cuda")
+    bk = torch.zeros(n_kv, device="cuda")
+    lib = capi.load()
+
+    def launch(i, s):
+        lib.tf_gemv_q5_0_qkv(qs[i].data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(), x.data_ptr(),
+                             q.data_ptr(), k.data_ptr(), v.data_ptr(), n_rows, n_q, n_kv, n_kv,
+                             cb, 1, bq.data_ptr(), bk.data_ptr(), bk.data_ptr(), s)
+
+    per, b2b = time_launches(launch, len(qs), iters)
+    n = n_q + 2 * n_kv
+    return dict(per_us=per, b2b_us=b2b, bytes=n * cb + 4 * n_rows + 8 * n)
 
 
 def case_flash(L, n_head, n_kv, hd, seed, iters, n_split=None):

@@ -34,6 +34,15 @@ SIGNATURES: dict[str, list] = {
     "tf_gemv_q6k_down_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "tf_gemv_q6k_compact_q8_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "tf_gemv_q6k_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q8_0_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q8_0_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q8_0_q8_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_q8_0_f32_splitk": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_q5_0_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "tf_gemv_q5_0_f32_splitk": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemv_q5_0_qk": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P],
+    "tf_gemv_q5_0_qkv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+    "tf_gemv_q8_0_qkv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "tf_q6k_compact_repack": [_P, _P, _I, _I, _I, _P],
     "tf_flash_decode_partial": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
     "tf_flash_decode_partial_d": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _F, _P],

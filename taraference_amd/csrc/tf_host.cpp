@@ -97,6 +97,15 @@ static const char* const k_symbols[] = {
     "tf_gemv_q6k_compact_q8_splitk",
     "tf_gemv_q6k_f32",
     "tf_q6k_compact_repack",
+    "tf_gemv_q8_0_q8",
+    "tf_gemv_q8_0_f32",
+    "tf_gemv_q8_0_q8_splitk",
+    "tf_gemv_q8_0_f32_splitk",
+    "tf_gemv_q5_0_f32",
+    "tf_gemv_q5_0_f32_splitk",
+    "tf_gemv_q5_0_qk",
+    "tf_gemv_q5_0_qkv",
+    "tf_gemv_q8_0_qkv",
     "tf_flash_decode_partial",
     "tf_flash_decode_partial_d",
     "tf_flash_decode_reduce",

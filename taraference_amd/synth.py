@@ -3,6 +3,10 @@
 Block formats follow the GGUF / reference layout (kernels/common.cu:40-186):
   Q4_K, 144 B: d f16, dmin f16, 12 packed 6-bit scale/min bytes, 128 qs bytes.
   Q6_K, 210 B: ql[128], qh[64], int8 scales[16], d f16.
+  Q8_0, 34 B (32 values): d f16, int8 qs[32].
+  Q5_0, 22 B (32 values): d f16, u32 qh, qs[16] (value t < 16 in the low
+  nibble of qs[t], value 16 + t in its high nibble, bit 4 of value v in bit v
+  of qh).
 Distributions (BASELINE.json configs): d and dmin ~ U[1e-3, 1e-2] as f16;
 6-bit scales and mins ~ U{0..63}; nibbles ~ U{0..15}; Q6_K ql/qh bytes
 uniform, scales ~ U[-32, 31]; activations ~ N(0, 1) f32.
@@ -18,6 +22,8 @@ import numpy as np
 Q4K_BYTES = 144
 Q6K_BYTES = 210
 Q6K_COMPACT_BYTES = 212
+Q8_0_BYTES = 34
+Q5_0_BYTES = 22
 
 SEED_BASE = 0x7A7A0000
 
@@ -88,6 +94,48 @@ def q6k_compact(raw: np.ndarray, n_rows: int) -> tuple[np.ndarray, int]:
     out = np.zeros((n_cols, nb, Q6K_COMPACT_BYTES), np.uint8)
     out[:, :, :Q6K_BYTES] = raw[:, : nb * Q6K_BYTES].reshape(n_cols, nb, Q6K_BYTES)
     return out.reshape(n_cols, nb * Q6K_COMPACT_BYTES), nb * Q6K_COMPACT_BYTES
+
+
+def q8_0_pack(d: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """Q8_0 blocks [n, 34] from f16 scales d [n] and int8 values q [n, 32]."""
+    n = q.shape[0]
+    blk = np.empty((n, Q8_0_BYTES), np.uint8)
+    blk[:, 0:2] = np.asarray(d, np.float16).view(np.uint8).reshape(n, 2)
+    blk[:, 2:] = np.asarray(q, np.int8).view(np.uint8)
+    return blk
+
+
+def q5_0_pack(d: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """Q5_0 blocks [n, 22] from f16 scales d [n] and 5-bit codes q [n, 32]
+    (0..31; the value is d * (q - 16))."""
+    q = np.asarray(q, np.uint32)
+    n = q.shape[0]
+    blk = np.empty((n, Q5_0_BYTES), np.uint8)
+    blk[:, 0:2] = np.asarray(d, np.float16).view(np.uint8).reshape(n, 2)
+    qh = ((q >> 4) << np.arange(32, dtype=np.uint32)).sum(axis=1, dtype=np.uint32)
+    blk[:, 2:6] = qh.astype("<u4").view(np.uint8).reshape(n, 4)
+    blk[:, 6:] = ((q[:, :16] & 15) | ((q[:, 16:] & 15) << 4)).astype(np.uint8)
+    return blk
+
+
+def q8_0_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
+    """Q8_0 matrix [n_cols, col_bytes]; col_bytes = n_rows/32 * 34; d ~ U[1e-3,
+    1e-2] as f16, values ~ U{-127..127}."""
+    nb = n_rows // 32
+    d = rng.uniform(1e-3, 1e-2, n_cols * nb).astype(np.float16)
+    q = rng.integers(-127, 128, (n_cols * nb, 32), dtype=np.int8)
+    return np.ascontiguousarray(q8_0_pack(d, q).reshape(n_cols, nb * Q8_0_BYTES)), \
+        nb * Q8_0_BYTES
+
+
+def q5_0_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
+    """Q5_0 matrix [n_cols, col_bytes]; col_bytes = n_rows/32 * 22; codes
+    ~ U{0..31}."""
+    nb = n_rows // 32
+    d = rng.uniform(1e-3, 1e-2, n_cols * nb).astype(np.float16)
+    q = rng.integers(0, 32, (n_cols * nb, 32), dtype=np.uint8)
+    return np.ascontiguousarray(q5_0_pack(d, q).reshape(n_cols, nb * Q5_0_BYTES)), \
+        nb * Q5_0_BYTES
 
 
 def activation(rng, n: int) -> np.ndarray:

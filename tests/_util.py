@@ -71,6 +71,35 @@ def q6k_dequant(blk: np.ndarray) -> np.ndarray:
     return d * sc[:, np.arange(256) // 16] * q6k_quants(blk)
 
 
+# --------------------------------------------------------------- Q8_0 / Q5_0
+
+def q8_0_dequant(blk: np.ndarray) -> np.ndarray:
+    """uint8 [n, 34] -> float64 [n, 32] (dequantize_row_q8_0: d * qs[t])."""
+    d = f16(blk[:, 0:2].reshape(-1, 1, 2)).reshape(-1, 1)
+    return d * np.ascontiguousarray(blk[:, 2:34]).view(np.int8).astype(np.float64)
+
+
+def q5_0_dequant(blk: np.ndarray) -> np.ndarray:
+    """uint8 [n, 22] -> float64 [n, 32] (dequantize_row_q5_0: value t < 16
+    from the low nibble of qs[t], 16 + t from its high nibble; bit 4 of value
+    v is bit v of the little-endian u32 qh; value = d * (code - 16))."""
+    d = f16(blk[:, 0:2].reshape(-1, 1, 2)).reshape(-1, 1)
+    qh = np.ascontiguousarray(blk[:, 2:6]).view("<u4").astype(np.int64)  # [n, 1]
+    qs = blk[:, 6:22].astype(np.int64)
+    nib = np.concatenate([qs & 15, qs >> 4], axis=1)
+    hi = (qh >> np.arange(32)) & 1
+    return d * (nib + 16 * hi - 16)
+
+
+def gemv_block32_ref(w, n_rows, xvec, block_bytes):
+    """fp64 W x for a 32-value block format (34: Q8_0, 22: Q5_0)."""
+    nb = n_rows // 32
+    blocks = w[:, : nb * block_bytes].reshape(-1, block_bytes)
+    deq = q8_0_dequant if block_bytes == 34 else q5_0_dequant
+    W = deq(blocks).reshape(w.shape[0], nb * 32)
+    return W @ np.asarray(xvec, np.float64)[: nb * 32]
+
+
 # --------------------------------------------------------------- matrices
 
 def matrix_blocks(w: np.ndarray, n_rows: int, block_bytes: int) -> np.ndarray:
