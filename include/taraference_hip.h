@@ -236,6 +236,40 @@ int tf_gemv_q8_0_qkv(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv,
                      const float *bq, const float *bk, const float *bv,
                      tf_stream_t stream);
 
+/* ------------------------------------------------------------- prefill
+ * n_tok > 1 (the prompt).  x, q and out are row-major per token:
+ * x[t*n_rows + k], out[t*n_cols + j], q/out of attention [t][n_head*hd].  */
+
+/* kernels/gemm.cu:6 gemm_q4_k (matmul.rs:1269-1323 gemm): out[t][j] =
+ * sum_k W[k][j] x[t][k], x f32, fp32 accuracy (matrix cores on exact
+ * integer weights and a three-part bf16 split of x; scales in fp32).
+ * n_rows % 4 == 0 (floor(n_rows/256) super-blocks are used, as the
+ * reference), x and out 16-byte aligned, w and col_bytes 4-byte aligned. */
+int tf_gemm_q4k_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                    int n_cols, int col_bytes, int n_tok, tf_stream_t stream);
+
+/* kernels/gemm.cu:69 gemm_q6_k: the same over raw 210-byte Q6_K blocks
+ * (2-byte aligned). */
+int tf_gemm_q6k_f32(const uint8_t *w, const float *x, float *out, int n_rows,
+                    int n_cols, int col_bytes, int n_tok, tf_stream_t stream);
+
+/* kernels/attn/fast_v2.cu:12 attn_fast_v2 (layer.rs prefill attention):
+ * causal attention of n_q queries at positions pos0 .. pos0+n_q-1 over the
+ * f16 cache [seq][n_kv*head_dim] (rows 0 .. pos0+n_q-1 written),
+ * out = softmax(q k^T * scale) v per head, GQA head h -> kv h/(n_head/n_kv).
+ * head_dim 64, 128 or 256; q/out 16-byte aligned. */
+int tf_attn_prefill(const float *q, const uint16_t *k_cache,
+                    const uint16_t *v_cache, float *out, int n_head, int n_kv,
+                    int head_dim, int pos0, int n_q, float scale,
+                    tf_stream_t stream);
+
+/* kernels/attn/fast_v2.cu:103 attn_fast_v2_d: pos0 read from device memory
+ * (graph-capturable). */
+int tf_attn_prefill_d(const float *q, const uint16_t *k_cache,
+                      const uint16_t *v_cache, float *out, int n_head, int n_kv,
+                      int head_dim, const int *pos0_dev, int n_q, float scale,
+                      tf_stream_t stream);
+
 /* ---------------------------------------------------- split-KV flash decode */
 
 /* kernels/attn/flash.cu:16 attn_flash_partial (layer.rs:2040-2103), n_q = 1.

@@ -285,7 +285,30 @@ def gemv_q5_0_f32_f64(w, x, n_rows, n_cols, col_bytes):
     return out, absn
 
 
+# ------------------------------------------------------------- prefill GEMMs
+
+def gemm_q4k(w, x, n_rows, n_cols, col_bytes, n_tok):
+    out = _f32(n_tok * n_cols)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemm_q4k(_p(w), _p(x), _p(out), n_rows, n_cols, col_bytes, n_tok)
+    return out.reshape(n_tok, n_cols)
+
+
+def gemm_q6k(w, x, n_rows, n_cols, col_bytes, n_tok):
+    out = _f32(n_tok * n_cols)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().or_gemm_q6k(_p(w), _p(x), _p(out), n_rows, n_cols, col_bytes, n_tok)
+    return out.reshape(n_tok, n_cols)
+
+
 # ------------------------------------------------------------------ attention
+
+def attn_prefill(q, k_cache, v_cache, n_head, n_kv, head_dim, pos0, n_q, scale):
+    out = _f32(n_q * n_head * head_dim)
+    lib().or_attn_prefill(_p(np.ascontiguousarray(q, np.float32)), _p(k_cache), _p(v_cache),
+                          _p(out), n_head, n_kv, head_dim, pos0, n_q, C.c_float(scale))
+    return out.reshape(n_q, n_head * head_dim)
+
 
 def flash_partial(q, k_cache, v_cache, n_head, n_kv, head_dim, pos0, n_split, scale):
     part = _f32(n_head * n_split * (2 + head_dim))

@@ -806,6 +806,146 @@ void or_gemv_q5_0_f32_f64(const uint8_t *w, const float *x, double *out,
     }
 }
 
+/* -------------------------------------------------------------- prefill GEMM */
+
+/* common.cu:64-84: the 256 f32 weights of one Q4_K super-block */
+static void dequant_q4k_f32(const uint8_t *base, float *dq) {
+    const float d = or_f16_to_f32(rd16(base));
+    const float minv = or_f16_to_f32(rd16(base + 2));
+    const uint8_t *q = base + 16;
+    for (int t = 0; t < 4; t++) {
+        int sc, m;
+        scale_min_k4(2 * t, base + 4, &sc, &m);
+        const float d1 = d * (float)sc, m1 = minv * (float)m;
+        scale_min_k4(2 * t + 1, base + 4, &sc, &m);
+        const float d2 = d * (float)sc, m2 = minv * (float)m;
+        for (int l = 0; l < 32; l++) {
+            dq[t * 64 + l] = d1 * (float)(q[t * 32 + l] & 0xF) - m1;
+            dq[t * 64 + 32 + l] = d2 * (float)(q[t * 32 + l] >> 4) - m2;
+        }
+    }
+}
+
+/* common.cu:164-186: the 256 f32 weights of one raw Q6_K super-block */
+static void dequant_q6k_f32(const uint8_t *base, float *dq) {
+    const uint8_t *ql = base, *qh = base + 128;
+    const int8_t *sc = (const int8_t *)(base + 192);
+    const float d = or_f16_to_f32(rd16(base + 208));
+    for (int n = 0; n < 2; n++) {
+        const int ql_i = n * 64, qh_i = n * 32, sc_i = n * 8, y0 = n * 128;
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q1 = (int)((ql[ql_i + l] & 0xF) | (((qh[qh_i + l] >> 0) & 3) << 4)) - 32;
+            const int q2 = (int)((ql[ql_i + 32 + l] & 0xF) | (((qh[qh_i + l] >> 2) & 3) << 4)) - 32;
+            const int q3 = (int)((ql[ql_i + l] >> 4) | (((qh[qh_i + l] >> 4) & 3) << 4)) - 32;
+            const int q4 = (int)((ql[ql_i + 32 + l] >> 4) | (((qh[qh_i + l] >> 6) & 3) << 4)) - 32;
+            dq[y0 + l] = d * (float)sc[sc_i + is] * (float)q1;
+            dq[y0 + 32 + l] = d * (float)sc[sc_i + is + 2] * (float)q2;
+            dq[y0 + 64 + l] = d * (float)sc[sc_i + is + 4] * (float)q3;
+            dq[y0 + 96 + l] = d * (float)sc[sc_i + is + 6] * (float)q4;
+        }
+    }
+}
+
+static void gemm_ref_order(const uint8_t *w, const float *x, float *out, int n_rows,
+                           int n_cols, int col_bytes, int n_tok, int block_bytes,
+                           void (*deq)(const uint8_t *, float *)) {
+    const int nb = n_rows / 256;
+    float *dq = (float *)malloc((size_t)nb * 256 * sizeof(float));
+    float acc[32];
+    for (int j = 0; j < n_cols; j++) {
+        const uint8_t *col = w + (size_t)j * col_bytes;
+        for (int bi = 0; bi < nb; bi++) deq(col + (size_t)bi * block_bytes, dq + bi * 256);
+        for (int t = 0; t < n_tok; t++) {
+            const float *xt = x + (size_t)t * n_rows;
+            for (int l = 0; l < 32; l++) {
+                float a = 0.f;
+                for (int bi = 0; bi < nb; bi++)
+                    for (int i = l; i < 256; i += 32) a += dq[bi * 256 + i] * xt[bi * 256 + i];
+                acc[l] = a;
+            }
+            out[(size_t)t * n_cols + j] = warp_sum32(acc);
+        }
+    }
+    free(dq);
+}
+
+void or_gemm_q4k(const uint8_t *w, const float *x, float *out, int n_rows,
+                 int n_cols, int col_bytes, int n_tok) {
+    gemm_ref_order(w, x, out, n_rows, n_cols, col_bytes, n_tok, 144, dequant_q4k_f32);
+}
+
+void or_gemm_q6k(const uint8_t *w, const float *x, float *out, int n_rows,
+                 int n_cols, int col_bytes, int n_tok) {
+    gemm_ref_order(w, x, out, n_rows, n_cols, col_bytes, n_tok, 210, dequant_q6k_f32);
+}
+
+/* ops.cu:507-529 block_max / block_sum over 128 threads (halving tree) */
+static float block_tree128(float *buf, int is_max) {
+    for (int s = 64; s > 0; s >>= 1)
+        for (int i = 0; i < s; i++)
+            buf[i] = is_max ? fmaxf(buf[i], buf[i + s]) : buf[i] + buf[i + s];
+    return buf[0];
+}
+
+void or_attn_prefill(const float *q, const uint16_t *k_cache,
+                     const uint16_t *v_cache, float *out, int n_head, int n_kv,
+                     int head_dim, int pos0, int n_q, float scale) {
+    const int rep = n_head / n_kv, stride = n_kv * head_dim, NT = 128, TILE = 64;
+    float scores[64], buf[128];
+    for (int qi = 0; qi < n_q; qi++)
+        for (int h = 0; h < n_head; h++) {
+            const int kv_h = h / rep, seq_len = pos0 + qi + 1;
+            const float *qh = q + (size_t)qi * n_head * head_dim + (size_t)h * head_dim;
+            float m = -1e30f, l = 0.f, acc0[128], acc1[128];
+            for (int t = 0; t < NT; t++) acc0[t] = acc1[t] = 0.f;
+            for (int t0 = 0; t0 < seq_len; t0 += TILE) {
+                const int tlen = seq_len - t0 < TILE ? seq_len - t0 : TILE;
+                for (int t = 0; t < tlen; t++) {
+                    const uint16_t *row = k_cache + (size_t)(t0 + t) * stride + (size_t)kv_h * head_dim;
+                    float dot = 0.f;
+                    for (int d = 0; d < head_dim; d++) dot += qh[d] * or_f16_to_f32(row[d]);
+                    scores[t] = dot * scale;
+                }
+                for (int tid = 0; tid < NT; tid++) buf[tid] = tid < tlen ? scores[tid] : -1e30f;
+                const float m_new = fmaxf(m, block_tree128(buf, 1));
+                const float alpha = expf(m - m_new);
+                for (int tid = 0; tid < NT; tid++) {
+                    float e = 0.f;
+                    if (tid < tlen) {
+                        e = expf(scores[tid] - m_new);
+                        scores[tid] = e;
+                    }
+                    buf[tid] = e;
+                }
+                const float tile_l = block_tree128(buf, 0);
+                for (int tid = 0; tid < NT; tid++) {
+                    const int d0 = tid, d1 = tid + NT;
+                    acc0[tid] *= alpha;
+                    if (d1 < head_dim) acc1[tid] *= alpha;
+                    if (d0 < head_dim) {
+                        float a0 = 0.f, a1 = 0.f;
+                        for (int t = 0; t < tlen; t++) {
+                            const uint16_t *vr = v_cache + (size_t)(t0 + t) * stride + (size_t)kv_h * head_dim;
+                            a0 += scores[t] * or_f16_to_f32(vr[d0]);
+                            if (d1 < head_dim) a1 += scores[t] * or_f16_to_f32(vr[d1]);
+                        }
+                        acc0[tid] += a0;
+                        acc1[tid] += a1;
+                    }
+                }
+                l = l * alpha + tile_l;
+                m = m_new;
+            }
+            const float inv = 1.f / fmaxf(l, 1e-20f);
+            float *oh = out + (size_t)qi * n_head * head_dim + (size_t)h * head_dim;
+            for (int tid = 0; tid < NT; tid++) {
+                if (tid < head_dim) oh[tid] = acc0[tid] * inv;
+                if (tid + NT < head_dim) oh[tid + NT] = acc1[tid] * inv;
+            }
+        }
+}
+
 /* -------------------------------------------------------------- flash decode */
 
 #define OR_ATTN_TILE 64

@@ -159,6 +159,28 @@ void or_gemv_q5_0_f32_f64(const uint8_t *w, const float *x, double *out,
                           double *rowabs, int n_rows, int n_cols,
                           int col_bytes);
 
+/* ------------------------------------------------------ prefill GEMMs
+ * out[t*n_cols + j] = sum_i W[i][j] * x[t*n_rows + i] for n_tok tokens.
+ * kernels/gemm.cu:6-67 gemm_q4_k and :69-121 gemm_q6_k (32 threads per
+ * column): each super-block is dequantized to f32 as
+ * common.cu:64-84 dequant_q4_k_block_smem (d*sc*q - dmin*m) or :164-186
+ * dequant_q6_k_block_smem (d*sc*q); thread l accumulates wv*x over values
+ * l, l+32, ... of every super-block in order; warp_sum.  The Q6_K weights
+ * are raw 210-byte blocks.                                            */
+void or_gemm_q4k(const uint8_t *w, const float *x, float *out, int n_rows,
+                 int n_cols, int col_bytes, int n_tok);
+void or_gemm_q6k(const uint8_t *w, const float *x, float *out, int n_rows,
+                 int n_cols, int col_bytes, int n_tok);
+
+/* kernels/attn/fast_v2.cu:12-103 attn_fast_v2 (128 threads): causal
+ * attention of n_q queries at positions pos0 .. pos0+n_q-1 over the f16
+ * cache; 64-key tiles, online softmax with expf, block_max / block_sum
+ * halving trees (ops.cu:507-529), out = acc / max(l, 1e-20).  q and out
+ * are [n_q][n_head*head_dim].                                        */
+void or_attn_prefill(const float *q, const uint16_t *k_cache,
+                     const uint16_t *v_cache, float *out, int n_head, int n_kv,
+                     int head_dim, int pos0, int n_q, float scale);
+
 /* kernels/attn/flash.cu:16-116 attn_flash_partial (n_q = 1, 128 threads) */
 void or_flash_partial(const float *q, const uint16_t *k_cache,
                       const uint16_t *v_cache, float *partial, int n_head,

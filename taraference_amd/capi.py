@@ -45,6 +45,10 @@ SIGNATURES: dict[str, list] = {
     "tf_gemv_q8_0_qkv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "tf_q6k_compact_repack": [_P, _P, _I, _I, _I, _P],
     "tf_flash_decode_partial": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P],
+    "tf_gemm_q4k_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_gemm_q6k_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "tf_attn_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
+    "tf_attn_prefill_d": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _F, _P],
     "tf_flash_decode_partial_d": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _F, _P],
     "tf_flash_decode_reduce": [_P, _P, _I, _I, _I, _I, _P],
     "tf_flash_decode_n_split": [_I, _I],

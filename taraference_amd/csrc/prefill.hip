@@ -1,0 +1,453 @@
+// Prefill (n_tok > 1) for gfx950: Q4_K / Q6_K GEMMs on the matrix cores and
+// causal tiled attention.
+//
+// Replaces kernels/gemm.cu gemm_q4_k (:6) and gemm_q6_k (:69) (matmul.rs:1269
+// gemm) and kernels/attn/fast_v2.cu attn_fast_v2 / attn_fast_v2_d (:12, :103).
+//
+// GEMM: out[t][j] = sum_k W[k][j] x[t][k] with x f32.  The reference
+// dequantizes each weight to f32 and accumulates in fp32; the result must
+// stay within fp32 GEMV accuracy, so the matrix cores are used as follows.
+// A K-quant weight is (scale of its sub-block) x (small integer):
+//   Q4_K  W = d*sc_s*q - dmin*m_s, q in 0..15, sub-blocks of 32,
+//   Q6_K  W = d*sc_s*(q - 32),     q - 32 in -32..31, sub-blocks of 16.
+// Small integers are exact in bf16, and x is split exactly into three bf16
+// parts, x = x0 + x1 + x2 (each the truncation of the remainder, so the
+// error is below 2^-21 |x|).  Per sub-block, v_mfma_f32_16x16x16_bf16 forms
+// sum(q x) with fp32 accumulation (three MFMAs per 16-deep K step, one per
+// part), and the fp32 epilogue applies the scales:
+//   acc += (d*sc_s) * sum(q x) - (dmin*m_s) * sum(x)      (Q4_K)
+//   acc += (d*sc_s) * sum((q-32) x)                        (Q6_K).
+// The products of the matrix cores are exact; only the fp32 summation order
+// differs from the reference's.
+//
+// Tiling: a workgroup (4 waves) owns 128 output columns x 32 tokens; a wave
+// owns 32 columns (two 16-column tiles) x 32 tokens (two 16-token tiles).
+// Per 256-value super-block the workgroup stages x (f32, padded rows) and
+// the per-sub-block scales of its columns in LDS; each wave reads its own
+// columns' quant bytes straight from global memory, issued before the
+// staging barrier.  Consecutive workgroups share columns (token tiles are
+// the fast grid dimension), so a column's bytes are re-read from L2.
+//
+// MFMA 16x16x16 bf16 operand layout (lane l, g = l / 16):
+//   A[i][k]: i = l % 16, k = 4g .. 4g+3;  B[k][j]: j = l % 16, k = 4g .. 4g+3;
+//   C[i][j]: j = l % 16, i = 4g .. 4g+3.
+// Here A rows are output columns, B columns are tokens.
+#include "tf_common.hpp"
+#include "tf_host.hpp"
+
+typedef short tf_bf16x4 __attribute__((ext_vector_type(4)));
+typedef float tf_f32x4 __attribute__((ext_vector_type(4)));
+
+#define TF_PF_COLS 128  // output columns per workgroup
+#define TF_PF_TOKS 32   // tokens per workgroup
+#define TF_PF_XSTRIDE 260  // floats per staged token row (256 + 4: no bank conflicts)
+
+// Three-part bf16 split of four floats (truncation; every remainder exact).
+struct TfSplit3 {
+    tf_bf16x4 p[3];
+};
+__device__ __forceinline__ TfSplit3 tf_split3(float4 v) {
+    TfSplit3 s;
+    float r[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int part = 0; part < 3; part++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t b = __float_as_uint(r[i]) & 0xffff0000u;
+            s.p[part][i] = (short)(b >> 16);
+            r[i] -= __uint_as_float(b);
+        }
+    }
+    return s;
+}
+
+// bf16 bits of a small integer (exact).
+__device__ __forceinline__ short tf_bf16_int(int q) {
+    return (short)(__float_as_uint((float)q) >> 16);
+}
+
+__device__ __forceinline__ tf_f32x4 tf_mfma3(tf_bf16x4 a, const TfSplit3& b, tf_f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[2], c, 0, 0, 0);
+    return c;
+}
+
+__device__ __forceinline__ uint32_t tf_pf_u16x2(const uint8_t* p) {
+    const TF_GAS uint16_t* s = (const TF_GAS uint16_t*)p;
+    return s[0] | ((uint32_t)s[1] << 16);
+}
+
+// Q4_K 6-bit scale and min of sub-block j (the GGML packing).
+__device__ __forceinline__ void tf_pf_scale_min(const uint8_t* s12, int j, int& sc, int& m) {
+    if (j < 4) {
+        sc = s12[j] & 63;
+        m = s12[j + 4] & 63;
+    } else {
+        sc = (s12[j + 4] & 0xF) | ((s12[j - 4] >> 6) << 4);
+        m = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
+    }
+}
+
+// Per-lane quant bytes of one column for one super-block.
+//   Q4_K: w[c*2 + h] = qs dword 32c + 16h + 4g (values of sub-blocks 2c, 2c+1).
+//   Q6_K: w[0..7] = ql dwords (n, qd&1, half), w[8..11] = qh dwords (n, half).
+template <bool Q6>
+struct TfPfCol {
+    uint32_t w[Q6 ? 12 : 8];
+};
+
+template <bool Q6>
+__device__ __forceinline__ void tf_pf_load_col(const uint8_t* blk, int g, TfPfCol<Q6>& c) {
+    if constexpr (!Q6) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            c.w[i] = tf_gld(reinterpret_cast<const uint32_t*>(blk + 16 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g));
+    } else {
+        // raw 210-byte blocks are 2-byte aligned: 16-bit loads
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int n = i >> 2, odd = (i >> 1) & 1, half = i & 1;
+            c.w[i] = tf_pf_u16x2(blk + 64 * n + 32 * odd + 16 * half + 4 * g);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = i >> 1, half = i & 1;
+            c.w[8 + i] = tf_pf_u16x2(blk + 128 + 32 * n + 16 * half + 4 * g);
+        }
+    }
+}
+
+// A operand (4 integers as bf16) of K step st (values 16 st + 4g .. +3).
+template <bool Q6>
+__device__ __forceinline__ tf_bf16x4 tf_pf_a(const TfPfCol<Q6>& c, int st) {
+    tf_bf16x4 a;
+    if constexpr (!Q6) {
+        const int s = st >> 1;
+        const uint32_t wd = c.w[(st >> 2) * 2 + (st & 1)] >> (4 * (s & 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[i] = tf_bf16_int((wd >> (8 * i)) & 15);
+    } else {
+        const int n = st >> 3, qd = (st & 7) >> 1, half = st & 1;
+        const uint32_t ql = c.w[n * 4 + (qd & 1) * 2 + half] >> (4 * (qd >> 1));
+        const uint32_t qh = c.w[8 + n * 2 + half] >> (2 * qd);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            a[i] = tf_bf16_int((int)(((ql >> (8 * i)) & 15) | (((qh >> (8 * i)) & 3) << 4)) - 32);
+    }
+    return a;
+}
+
+template <bool Q6>
+__global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restrict__ w,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ out, int n_rows,
+                                                          int n_cols, int col_bytes, int n_tok) {
+    constexpr int NSUB = Q6 ? 16 : 8;
+    constexpr int BLK = Q6 ? 210 : 144;
+    __shared__ __align__(16) float xs[TF_PF_TOKS * TF_PF_XSTRIDE];
+    __shared__ float xsum[Q6 ? 1 : TF_PF_TOKS * 8];
+    __shared__ __align__(16) float scl[NSUB * TF_PF_COLS];
+    __shared__ __align__(16) float mnl[Q6 ? 1 : 8 * TF_PF_COLS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int t0 = blockIdx.x * TF_PF_TOKS;
+    const int c0 = blockIdx.y * TF_PF_COLS;
+    const int nb = n_rows / 256;
+    // this lane's A columns (one per 16-column tile), clamped for loads
+    int colA[2];
+    for (int ct = 0; ct < 2; ct++) {
+        const int c = c0 + 32 * wave + 16 * ct + l16;
+        colA[ct] = c < n_cols ? c : n_cols - 1;
+    }
+    tf_f32x4 acc[2][2];
+    for (int ct = 0; ct < 2; ct++)
+        for (int tt = 0; tt < 2; tt++) acc[ct][tt] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int sb = 0; sb < nb; sb++) {
+        TfPfCol<Q6> wc[2];
+        for (int ct = 0; ct < 2; ct++)
+            tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)sb * BLK, g, wc[ct]);
+        __syncthreads();  // the previous super-block's LDS reads are done
+        // stage x: 32 tokens x 256 floats, 8 float4 per thread
+        for (int i = tid; i < TF_PF_TOKS * 64; i += 256) {
+            const int t = i >> 6, v4 = i & 63;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t0 + t < n_tok)
+                v = *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * n_rows + sb * 256 + 4 * v4);
+            *reinterpret_cast<float4*>(xs + t * TF_PF_XSTRIDE + 4 * v4) = v;
+        }
+        // scales of the workgroup's columns
+        if (tid < TF_PF_COLS) {
+            const int c = c0 + tid < n_cols ? c0 + tid : n_cols - 1;
+            const uint8_t* blk = w + (size_t)c * col_bytes + (size_t)sb * BLK;
+            if constexpr (!Q6) {
+                const float d = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk)));
+                const float dmin = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk + 2)));
+                uint8_t s12[12];
+                for (int i = 0; i < 12; i++) s12[i] = blk[4 + i];
+                for (int s = 0; s < 8; s++) {
+                    int sc, m;
+                    tf_pf_scale_min(s12, s, sc, m);
+                    scl[s * TF_PF_COLS + tid] = d * (float)sc;
+                    mnl[s * TF_PF_COLS + tid] = dmin * (float)m;
+                }
+            } else {
+                const float d = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk + 208)));
+                for (int s = 0; s < 16; s++)
+                    scl[s * TF_PF_COLS + tid] = d * (float)(int8_t)blk[192 + s];
+            }
+        }
+        __syncthreads();
+        if constexpr (!Q6) {
+            // sum of x over each 32-value group, per token
+            const int t = tid >> 3, s = tid & 7;
+            float a = 0.f;
+            for (int i = 0; i < 32; i++) a += xs[t * TF_PF_XSTRIDE + 32 * s + ((i + 4 * s) & 31)];
+            xsum[t * 8 + s] = a;
+            __syncthreads();
+        }
+        tf_f32x4 part[2][2];
+        for (int st = 0; st < 16; st++) {
+            const bool first = Q6 || (st & 1) == 0;
+            TfSplit3 b[2];
+            for (int tt = 0; tt < 2; tt++)
+                b[tt] = tf_split3(*reinterpret_cast<const float4*>(
+                    xs + (16 * tt + l16) * TF_PF_XSTRIDE + 16 * st + 4 * g));
+            for (int ct = 0; ct < 2; ct++) {
+                const tf_bf16x4 a = tf_pf_a<Q6>(wc[ct], st);
+                for (int tt = 0; tt < 2; tt++)
+                    part[ct][tt] = tf_mfma3(a, b[tt], first ? tf_f32x4{0.f, 0.f, 0.f, 0.f}
+                                                            : part[ct][tt]);
+            }
+            const bool last = Q6 || (st & 1) == 1;
+            if (last) {
+                const int s = Q6 ? st : (st >> 1);
+                for (int ct = 0; ct < 2; ct++) {
+                    // scales of C rows 4g..4g+3 = columns 16 ct + 4g + r of this wave
+                    const float4 sc4 = *reinterpret_cast<const float4*>(
+                        scl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
+                    float4 mn4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if constexpr (!Q6)
+                        mn4 = *reinterpret_cast<const float4*>(
+                            mnl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
+                    const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+                    const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+                    for (int tt = 0; tt < 2; tt++) {
+                        const float xs_s = Q6 ? 0.f : xsum[(16 * tt + l16) * 8 + (s & 7)];
+                        for (int r = 0; r < 4; r++) {
+                            float v = acc[ct][tt][r] + scv[r] * part[ct][tt][r];
+                            if constexpr (!Q6) v -= mnv[r] * xs_s;
+                            acc[ct][tt][r] = v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // C rows 4g..4g+3 -> columns, C column l16 -> token
+    for (int ct = 0; ct < 2; ct++) {
+        const int cb = c0 + 32 * wave + 16 * ct + 4 * g;
+        for (int tt = 0; tt < 2; tt++) {
+            const int t = t0 + 16 * tt + l16;
+            if (t >= n_tok) continue;
+            float* o = out + (size_t)t * n_cols + cb;
+            if (cb + 3 < n_cols && ((n_cols & 3) == 0)) {
+                *reinterpret_cast<float4*>(o) = make_float4(acc[ct][tt][0], acc[ct][tt][1],
+                                                            acc[ct][tt][2], acc[ct][tt][3]);
+            } else {
+                for (int r = 0; r < 4; r++)
+                    if (cb + r < n_cols) o[r] = acc[ct][tt][r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- attention
+//
+// Causal attention of n_q queries (positions pos0 .. pos0+n_q-1) over the
+// f16 cache, fp32 arithmetic.  A workgroup (256 threads) owns one head and
+// 16 consecutive queries; K/V tiles of T keys (64, 32, 16 for head_dim 64,
+// 128, 256: about 45 KB of LDS) are staged in LDS as f32 and shared by the
+// 16 queries.  Thread (query qi = tid / 16, m = tid % 16): scores of keys
+// m, m+16, ... of the tile (a DPP row holds one query, so the row max and
+// sum are row reductions), then output dims DPT m .. DPT m + DPT-1 with
+// DPT = head_dim / 16.  Online softmax as
+// the reference: m_new = max(m, tile max), alpha = e^(m - m_new),
+// l = l alpha + tile sum, out = acc / max(l, 1e-20).
+
+#define TF_PA_Q 16
+
+template <int HD>
+__global__ __launch_bounds__(256) void tf_attn_prefill_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ out, int n_head, int n_kv, int pos0_arg, const int* __restrict__ pos0_ptr,
+    int n_q, float scale) {
+    constexpr int DPT = HD / 16;  // output dims per thread
+    constexpr int TF_PA_T = HD == 64 ? 64 : (HD == 128 ? 32 : 16);  // keys per tile
+    constexpr int NS = TF_PA_T / 16;                                // scores per thread
+    __shared__ __align__(16) float qs[TF_PA_Q * (HD + 4)];
+    __shared__ __align__(16) float ks[TF_PA_T * (HD + 4)];
+    __shared__ __align__(16) float vs[TF_PA_T * HD];
+    __shared__ float ps[TF_PA_Q * (TF_PA_T + 1)];
+    const int pos0 = pos0_ptr ? pos0_ptr[0] : pos0_arg;
+    const int h = blockIdx.y, q0 = blockIdx.x * TF_PA_Q;
+    const int tid = threadIdx.x, qi = tid >> 4, m = tid & 15;
+    const int kv_h = h / (n_head / n_kv), stride = n_kv * HD;
+    const int qn = q0 + qi;
+    const bool qvalid = qn < n_q;
+    const int my_len = pos0 + (qvalid ? qn : q0) + 1;           // keys this query sees
+    const int last_q = (q0 + TF_PA_Q < n_q ? q0 + TF_PA_Q : n_q) - 1;
+    const int seq_len = pos0 + last_q + 1;                         // keys of the workgroup
+    for (int i = tid; i < TF_PA_Q * HD / 4; i += 256) {
+        const int r = i / (HD / 4), c4 = i % (HD / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (q0 + r < n_q)
+            v = *reinterpret_cast<const float4*>(q + (size_t)(q0 + r) * n_head * HD + h * HD + 4 * c4);
+        *reinterpret_cast<float4*>(qs + r * (HD + 4) + 4 * c4) = v;
+    }
+    float mx = -1e30f, l = 0.f, acc[DPT];
+    for (int i = 0; i < DPT; i++) acc[i] = 0.f;
+    for (int t0 = 0; t0 < seq_len; t0 += TF_PA_T) {
+        const int tlen = seq_len - t0 < TF_PA_T ? seq_len - t0 : TF_PA_T;
+        __syncthreads();  // q staged / previous tile consumed
+        for (int i = tid; i < TF_PA_T * HD / 4; i += 256) {
+            const int r = i / (HD / 4), c4 = i % (HD / 4);
+            float4 kf = make_float4(0.f, 0.f, 0.f, 0.f), vf = kf;
+            if (r < tlen) {
+                const size_t off = (size_t)(t0 + r) * stride + (size_t)kv_h * HD + 4 * c4;
+                const uint2 kb = *reinterpret_cast<const uint2*>(kc + off);
+                const uint2 vb = *reinterpret_cast<const uint2*>(vc + off);
+                kf = make_float4(tf_h2f(kb.x), tf_h2f(kb.x >> 16), tf_h2f(kb.y), tf_h2f(kb.y >> 16));
+                vf = make_float4(tf_h2f(vb.x), tf_h2f(vb.x >> 16), tf_h2f(vb.y), tf_h2f(vb.y >> 16));
+            }
+            *reinterpret_cast<float4*>(ks + r * (HD + 4) + 4 * c4) = kf;
+            *reinterpret_cast<float4*>(vs + r * HD + 4 * c4) = vf;
+        }
+        __syncthreads();
+        // scores of keys m + 16 j
+        float s[NS];
+        const float* qrow = qs + qi * (HD + 4);
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const float* krow = ks + (m + 16 * j) * (HD + 4);
+            float a0 = 0.f, a1 = 0.f;
+            for (int d = 0; d < HD; d += 8) {
+                const float4 qa = *reinterpret_cast<const float4*>(qrow + d);
+                const float4 qb = *reinterpret_cast<const float4*>(qrow + d + 4);
+                const float4 ka = *reinterpret_cast<const float4*>(krow + d);
+                const float4 kb = *reinterpret_cast<const float4*>(krow + d + 4);
+                a0 += qa.x * ka.x + qa.y * ka.y + qa.z * ka.z + qa.w * ka.w;
+                a1 += qb.x * kb.x + qb.y * kb.y + qb.z * kb.z + qb.w * kb.w;
+            }
+            const int key = t0 + m + 16 * j;
+            s[j] = key < my_len ? (a0 + a1) * scale : -1e30f;
+        }
+        float tmax = s[0];
+#pragma unroll
+        for (int j = 1; j < NS; j++) tmax = fmaxf(tmax, s[j]);
+        tmax = tf_row16_max(tmax);
+        const float m_new = fmaxf(mx, tmax);
+        const float alpha = __expf(mx - m_new);
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const float e = s[j] > -1e29f ? __expf(s[j] - m_new) : 0.f;
+            ps[qi * (TF_PA_T + 1) + m + 16 * j] = e;
+            ls += e;
+        }
+        ls = tf_row16_sum(ls);
+        l = l * alpha + ls;
+        mx = m_new;
+        for (int i = 0; i < DPT; i++) acc[i] *= alpha;
+        __syncthreads();  // ps complete (the row's other lanes wrote it)
+        const float* prow = ps + qi * (TF_PA_T + 1);
+        for (int t = 0; t < tlen; t++) {
+            const float p = prow[t];
+            const float* vrow = vs + t * HD + DPT * m;
+#pragma unroll
+            for (int i = 0; i < DPT; i += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(vrow + i);
+                acc[i] += p * v.x;
+                acc[i + 1] += p * v.y;
+                acc[i + 2] += p * v.z;
+                acc[i + 3] += p * v.w;
+            }
+        }
+    }
+    if (qvalid) {
+        const float inv = 1.f / fmaxf(l, 1e-20f);
+        float* o = out + (size_t)qn * n_head * HD + h * HD + DPT * m;
+        for (int i = 0; i < DPT; i += 4)
+            *reinterpret_cast<float4*>(o + i) =
+                make_float4(acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv, acc[i + 3] * inv);
+    }
+}
+
+// ---------------------------------------------------------------- C ABI
+
+static int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows,
+                      int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    const int blk = q6 ? 210 : 144;
+    TF_CHECK_ARG(w && x && out && nb > 0 && n_cols > 0 && n_tok > 0);
+    TF_CHECK_ARG(col_bytes >= nb * blk && (n_rows & 3) == 0 && ((uintptr_t)x & 15) == 0);
+    if (q6) TF_CHECK_ARG(((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
+    else TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0);
+    TF_CHECK_ARG(((uintptr_t)out & 15) == 0);
+    const dim3 grid((n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS, (n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
+    TF_CHECK_ARG(grid.y <= 65535);
+    if (q6)
+        hipLaunchKernelGGL(tf_gemm_kq_kernel<true>, grid, dim3(256), 0, tf_stream(stream), w, x,
+                           out, n_rows, n_cols, col_bytes, n_tok);
+    else
+        hipLaunchKernelGGL(tf_gemm_kq_kernel<false>, grid, dim3(256), 0, tf_stream(stream), w, x,
+                           out, n_rows, n_cols, col_bytes, n_tok);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_gemm_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
+                               int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
+    return tf_gemm_kq(false, w, x, out, n_rows, n_cols, col_bytes, n_tok, stream);
+}
+
+extern "C" int tf_gemm_q6k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
+                               int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
+    return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, stream);
+}
+
+static int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                               float* out, int n_head, int n_kv, int head_dim, int pos0,
+                               const int* pos0_dev, int n_q, float scale, tf_stream_t stream) {
+    TF_CHECK_ARG(q && k_cache && v_cache && out && n_head > 0 && n_kv > 0 && n_q > 0);
+    TF_CHECK_ARG(n_head % n_kv == 0 && (pos0_dev || pos0 >= 0));
+    TF_CHECK_ARG(head_dim == 64 || head_dim == 128 || head_dim == 256);
+    TF_CHECK_ARG(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0);
+    TF_CHECK_ARG(((uintptr_t)k_cache & 7) == 0 && ((uintptr_t)v_cache & 7) == 0);
+    const dim3 grid((n_q + TF_PA_Q - 1) / TF_PA_Q, n_head);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, tf_stream(stream), q, k_cache, v_cache, out,
+                           n_head, n_kv, pos0, pos0_dev, n_q, scale);
+    };
+    if (head_dim == 64) go(tf_attn_prefill_kernel<64>);
+    else if (head_dim == 128) go(tf_attn_prefill_kernel<128>);
+    else go(tf_attn_prefill_kernel<256>);
+    return TF_LAUNCH_RESULT();
+}
+
+extern "C" int tf_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                               float* out, int n_head, int n_kv, int head_dim, int pos0, int n_q,
+                               float scale, tf_stream_t stream) {
+    return tf_attn_prefill_any(q, k_cache, v_cache, out, n_head, n_kv, head_dim, pos0, nullptr,
+                               n_q, scale, stream);
+}
+
+extern "C" int tf_attn_prefill_d(const float* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, float* out, int n_head, int n_kv,
+                                 int head_dim, const int* pos0_dev, int n_q, float scale,
+                                 tf_stream_t stream) {
+    TF_CHECK_ARG(pos0_dev != nullptr);
+    return tf_attn_prefill_any(q, k_cache, v_cache, out, n_head, n_kv, head_dim, 0, pos0_dev, n_q,
+                               scale, stream);
+}

@@ -106,6 +106,10 @@ static const char* const k_symbols[] = {
     "tf_gemv_q5_0_qk",
     "tf_gemv_q5_0_qkv",
     "tf_gemv_q8_0_qkv",
+    "tf_gemm_q4k_f32",
+    "tf_gemm_q6k_f32",
+    "tf_attn_prefill",
+    "tf_attn_prefill_d",
     "tf_flash_decode_partial",
     "tf_flash_decode_partial_d",
     "tf_flash_decode_reduce",

@@ -127,6 +127,18 @@ def gemv_q6k_ref(w, n_rows, xvec, block_bytes=210):
     return W @ xvec[: nb * 256]
 
 
+def gemm_ref(fmt, w, n_rows, x):
+    """fp64 (Y, sum |terms|) of the prefill GEMM Y[t] = W x[t] for a Q4_K
+    ("q4k", 144-byte) or raw Q6_K ("q6k", 210-byte) matrix."""
+    bb = 144 if fmt == "q4k" else 210
+    blocks = matrix_blocks(w, n_rows, bb)
+    n_cols, nb = blocks.shape[:2]
+    deq = q4k_dequant if fmt == "q4k" else q6k_dequant
+    W = deq(blocks.reshape(-1, bb)).reshape(n_cols, nb * 256)
+    X = np.asarray(x, np.float64)[:, : nb * 256]
+    return X @ W.T, np.abs(X) @ np.abs(W).T
+
+
 # --------------------------------------------------------------- tolerances
 
 GEMV_RTOL = 1e-5        # north-star fp32 GEMV tolerance (relative)
