@@ -122,6 +122,13 @@ def kernel_table(iters):
                                                            max(10, iters // 4))),
         ("q5_0_ffn_896x4864", lambda: B.case_block32("q5_0", 896, 4864, 9, iters)),
         ("q5_0_qkv_896x1152", lambda: B.case_q5_0_qkv(896, 896, 128, 10, iters)),
+        # prefill (512-token prompt, Qwen2.5-3B shapes)
+        ("prefill_gemm_q4k_2048x11008_T512", lambda: B.case_gemm("q4k", 2048, 11008, 512, 11,
+                                                                 max(5, iters // 10))),
+        ("prefill_gemm_q6k_11008x2048_T512", lambda: B.case_gemm("q6k", 11008, 2048, 512, 12,
+                                                                 max(5, iters // 10))),
+        ("prefill_attn_16x2x128_T512", lambda: B.case_attn_prefill(16, 2, 128, 512, 13,
+                                                                   max(5, iters // 10))),
     ]
     for L in (512, 4096, 32768):
         rows.append((f"cfg2_flash_L{L}_split8", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters, 8)))
@@ -134,6 +141,8 @@ def kernel_table(iters):
                      "frac_hbm": round(r["frac"], 4)}
         if "n_split" in r:
             out[name]["n_split"] = r["n_split"]
+        if "flops" in r:
+            out[name]["TFLOPs"] = round(r["flops"] / (r["b2b_us"] * 1e-6) / 1e12, 1)
         log(f"[bench] {name}: {out[name]}")
     return out
 

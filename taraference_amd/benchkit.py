@@ -231,6 +231,45 @@ def case_q5_0_qkv(n_rows, n_q, n_kv, seed, iters):
     return dict(per_us=per, b2b_us=b2b, bytes=n * cb + 4 * n_rows + 8 * n)
 
 
+def case_gemm(fmt, n_rows, n_cols, n_tok, seed, iters):
+    """Prefill GEMM (tf_gemm_q4k_f32 / tf_gemm_q6k_f32), x f32 [n_tok][K]."""
+    rng = np.random.default_rng(seed)
+    w, cb = (synth.q4k_matrix if fmt == "q4k" else synth.q6k_matrix)(rng, n_rows, n_cols)
+    ws = _copies(w, w.nbytes)
+    x = _dev(rng.standard_normal((n_tok, n_rows)).astype(np.float32))
+    out = torch.empty(n_tok * n_cols, device="cuda")
+    fn = getattr(capi.load(), f"tf_gemm_{fmt}_f32")
+
+    def launch(i, s):
+        fn(ws[i].data_ptr(), x.data_ptr(), out.data_ptr(), n_rows, n_cols, cb, n_tok, s)
+
+    per, b2b = time_launches(launch, len(ws), iters)
+    nb = n_rows // 256
+    return dict(per_us=per, b2b_us=b2b, bytes=w.nbytes + 4 * n_tok * (n_rows + n_cols),
+                flops=2.0 * n_tok * nb * 256 * n_cols)
+
+
+def case_attn_prefill(n_head, n_kv, hd, n_q, seed, iters):
+    rng = np.random.default_rng(seed)
+    Kc = synth.kv_cache(rng, n_q, n_kv, hd)
+    Vc = synth.kv_cache(rng, n_q, n_kv, hd)
+    k, v = _dev(Kc), _dev(Vc)
+    q = _dev(rng.standard_normal(n_q * n_head * hd).astype(np.float32))
+    out = torch.empty(n_q * n_head * hd, device="cuda")
+    lib = capi.load()
+    scale = float(np.float32(1 / np.sqrt(hd)))
+
+    def launch(i, s):
+        lib.tf_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), n_head,
+                            n_kv, hd, 0, n_q, scale, s)
+
+    per, b2b = time_launches(launch, 1, iters)
+    # causal: query i attends i + 1 keys; QK^T and PV are 2 flops per MAC each
+    pairs = n_q * (n_q + 1) / 2
+    return dict(per_us=per, b2b_us=b2b, bytes=Kc.nbytes + Vc.nbytes + 8 * n_q * n_head * hd,
+                flops=4.0 * n_head * hd * pairs)
+
+
 def case_flash(L, n_head, n_kv, hd, seed, iters, n_split=None):
     rng = np.random.default_rng(seed)
     Kc = synth.kv_cache(rng, L, n_kv, hd)

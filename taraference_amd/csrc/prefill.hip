@@ -12,9 +12,10 @@
 //   Q6_K  W = d*sc_s*(q - 32),     q - 32 in -32..31, sub-blocks of 16.
 // Small integers are exact in bf16, and x is split exactly into three bf16
 // parts, x = x0 + x1 + x2 (each the truncation of the remainder, so the
-// error is below 2^-21 |x|).  Per sub-block, v_mfma_f32_16x16x16_bf16 forms
-// sum(q x) with fp32 accumulation (three MFMAs per 16-deep K step, one per
-// part), and the fp32 epilogue applies the scales:
+// error is below 2^-21 |x|).  Per sub-block the matrix cores form sum(q x)
+// with fp32 accumulation, one MFMA per part (Q4_K: v_mfma_f32_16x16x32_bf16,
+// one 32-deep step per sub-block; Q6_K: v_mfma_f32_16x16x16_bf16, one
+// 16-deep step per sub-block), and the fp32 epilogue applies the scales:
 //   acc += (d*sc_s) * sum(q x) - (dmin*m_s) * sum(x)      (Q4_K)
 //   acc += (d*sc_s) * sum((q-32) x)                        (Q6_K).
 // The products of the matrix cores are exact; only the fp32 summation order
@@ -22,16 +23,17 @@
 //
 // Tiling: a workgroup (4 waves) owns 128 output columns x 32 tokens; a wave
 // owns 32 columns (two 16-column tiles) x 32 tokens (two 16-token tiles).
-// Per 256-value super-block the workgroup stages x (f32, padded rows) and
-// the per-sub-block scales of its columns in LDS; each wave reads its own
+// Per 256-value super-block the workgroup stages x in LDS already split into
+// its three bf16 planes (once per workgroup, with the per-group sums of x)
+// and the per-sub-block scales of its columns; each wave reads its own
 // columns' quant bytes straight from global memory, issued before the
 // staging barrier.  Consecutive workgroups share columns (token tiles are
 // the fast grid dimension), so a column's bytes are re-read from L2.
 //
-// MFMA 16x16x16 bf16 operand layout (lane l, g = l / 16):
-//   A[i][k]: i = l % 16, k = 4g .. 4g+3;  B[k][j]: j = l % 16, k = 4g .. 4g+3;
-//   C[i][j]: j = l % 16, i = 4g .. 4g+3.
-// Here A rows are output columns, B columns are tokens.
+// MFMA operand layouts (lane l, g = l / 16), A rows = output columns,
+// B columns = tokens, C[i][j] with j = l % 16, i = 4g .. 4g+3:
+//   16x16x16: A[l % 16][4g .. 4g+3], B[4g .. 4g+3][l % 16];
+//   16x16x32: A[l % 16][8g .. 8g+7], B[8g .. 8g+7][l % 16].
 #include "tf_common.hpp"
 #include "tf_host.hpp"
 
@@ -40,7 +42,6 @@ typedef float tf_f32x4 __attribute__((ext_vector_type(4)));
 
 #define TF_PF_COLS 128  // output columns per workgroup
 #define TF_PF_TOKS 32   // tokens per workgroup
-#define TF_PF_XSTRIDE 260  // floats per staged token row (256 + 4: no bank conflicts)
 
 // Three-part bf16 split of four floats (truncation; every remainder exact).
 struct TfSplit3 {
@@ -66,13 +67,6 @@ __device__ __forceinline__ short tf_bf16_int(int q) {
     return (short)(__float_as_uint((float)q) >> 16);
 }
 
-__device__ __forceinline__ tf_f32x4 tf_mfma3(tf_bf16x4 a, const TfSplit3& b, tf_f32x4 c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[0], c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[1], c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b.p[2], c, 0, 0, 0);
-    return c;
-}
-
 __device__ __forceinline__ uint32_t tf_pf_u16x2(const uint8_t* p) {
     const TF_GAS uint16_t* s = (const TF_GAS uint16_t*)p;
     return s[0] | ((uint32_t)s[1] << 16);
@@ -89,9 +83,15 @@ __device__ __forceinline__ void tf_pf_scale_min(const uint8_t* s12, int j, int& 
     }
 }
 
+typedef __bf16 tf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef short tf_s16x8 __attribute__((ext_vector_type(8)));
+
 // Per-lane quant bytes of one column for one super-block.
-//   Q4_K: w[c*2 + h] = qs dword 32c + 16h + 4g (values of sub-blocks 2c, 2c+1).
-//   Q6_K: w[0..7] = ql dwords (n, qd&1, half), w[8..11] = qh dwords (n, half).
+//   Q4_K (16x16x32 steps, K step = sub-block s, lane values 32 s + 8g .. +7):
+//     w[2c], w[2c+1] = qs bytes 32c + 8g .. +7 (sub-blocks 2c low nibbles,
+//     2c+1 high nibbles).
+//   Q6_K (16x16x16 steps, K step = sub-block st, lane values 16 st + 4g .. +3):
+//     w[0..7] = ql dwords (n, qd&1, half), w[8..11] = qh dwords (n, half).
 template <bool Q6>
 struct TfPfCol {
     uint32_t w[Q6 ? 12 : 8];
@@ -101,8 +101,11 @@ template <bool Q6>
 __device__ __forceinline__ void tf_pf_load_col(const uint8_t* blk, int g, TfPfCol<Q6>& c) {
     if constexpr (!Q6) {
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            c.w[i] = tf_gld(reinterpret_cast<const uint32_t*>(blk + 16 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g));
+        for (int i = 0; i < 4; i++) {
+            const tf_u32x2 v = *(const TF_GAS tf_u32x2*)(blk + 16 + 32 * i + 8 * g);
+            c.w[2 * i] = v.x;
+            c.w[2 * i + 1] = v.y;
+        }
     } else {
         // raw 210-byte blocks are 2-byte aligned: 16-bit loads
 #pragma unroll
@@ -118,25 +121,44 @@ __device__ __forceinline__ void tf_pf_load_col(const uint8_t* blk, int g, TfPfCo
     }
 }
 
-// A operand (4 integers as bf16) of K step st (values 16 st + 4g .. +3).
-template <bool Q6>
-__device__ __forceinline__ tf_bf16x4 tf_pf_a(const TfPfCol<Q6>& c, int st) {
-    tf_bf16x4 a;
-    if constexpr (!Q6) {
-        const int s = st >> 1;
-        const uint32_t wd = c.w[(st >> 2) * 2 + (st & 1)] >> (4 * (s & 1));
+// Q4_K A operand of sub-block s: 8 codes as bf16.
+__device__ __forceinline__ tf_s16x8 tf_pf_a4(const TfPfCol<false>& c, int s) {
+    tf_s16x8 a;
+    const int sh = 4 * (s & 1);
+    const uint32_t lo = c.w[2 * (s >> 1)] >> sh, hi = c.w[2 * (s >> 1) + 1] >> sh;
 #pragma unroll
-        for (int i = 0; i < 4; i++) a[i] = tf_bf16_int((wd >> (8 * i)) & 15);
-    } else {
-        const int n = st >> 3, qd = (st & 7) >> 1, half = st & 1;
-        const uint32_t ql = c.w[n * 4 + (qd & 1) * 2 + half] >> (4 * (qd >> 1));
-        const uint32_t qh = c.w[8 + n * 2 + half] >> (2 * qd);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            a[i] = tf_bf16_int((int)(((ql >> (8 * i)) & 15) | (((qh >> (8 * i)) & 3) << 4)) - 32);
+    for (int i = 0; i < 4; i++) {
+        a[i] = tf_bf16_int((lo >> (8 * i)) & 15);
+        a[4 + i] = tf_bf16_int((hi >> (8 * i)) & 15);
     }
     return a;
 }
+
+// Q6_K A operand of sub-block st: 4 signed codes as bf16.
+__device__ __forceinline__ tf_bf16x4 tf_pf_a6(const TfPfCol<true>& c, int st) {
+    tf_bf16x4 a;
+    const int n = st >> 3, qd = (st & 7) >> 1, half = st & 1;
+    const uint32_t ql = c.w[n * 4 + (qd & 1) * 2 + half] >> (4 * (qd >> 1));
+    const uint32_t qh = c.w[8 + n * 2 + half] >> (2 * qd);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        a[i] = tf_bf16_int((int)(((ql >> (8 * i)) & 15) | (((qh >> (8 * i)) & 3) << 4)) - 32);
+    return a;
+}
+
+__device__ __forceinline__ tf_f32x4 tf_mfma32(tf_s16x8 a, tf_s16x8 b, tf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(tf_bf16x8, a),
+                                                   __builtin_bit_cast(tf_bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ tf_f32x4 tf_mfma16(tf_bf16x4 a, tf_bf16x4 b, tf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// LDS image of x for one super-block: 3 bf16 planes x 32 tokens x 256
+// values, rows of TF_PF_ROW bytes (16 bytes of padding: the 16 rows a
+// fragment read touches start on distinct banks).
+#define TF_PF_ROW 528
+#define TF_PF_XBYTES (3 * TF_PF_TOKS * TF_PF_ROW)
 
 template <bool Q6>
 __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restrict__ w,
@@ -145,7 +167,7 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
                                                           int n_cols, int col_bytes, int n_tok) {
     constexpr int NSUB = Q6 ? 16 : 8;
     constexpr int BLK = Q6 ? 210 : 144;
-    __shared__ __align__(16) float xs[TF_PF_TOKS * TF_PF_XSTRIDE];
+    __shared__ __align__(16) uint8_t xp[TF_PF_XBYTES];
     __shared__ float xsum[Q6 ? 1 : TF_PF_TOKS * 8];
     __shared__ __align__(16) float scl[NSUB * TF_PF_COLS];
     __shared__ __align__(16) float mnl[Q6 ? 1 : 8 * TF_PF_COLS];
@@ -170,13 +192,25 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
         for (int ct = 0; ct < 2; ct++)
             tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)sb * BLK, g, wc[ct]);
         __syncthreads();  // the previous super-block's LDS reads are done
-        // stage x: 32 tokens x 256 floats, 8 float4 per thread
-        for (int i = tid; i < TF_PF_TOKS * 64; i += 256) {
-            const int t = i >> 6, v4 = i & 63;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t0 + t < n_tok)
-                v = *reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * n_rows + sb * 256 + 4 * v4);
-            *reinterpret_cast<float4*>(xs + t * TF_PF_XSTRIDE + 4 * v4) = v;
+        {
+            // thread (token t, group s of 32 values): split into the three
+            // bf16 planes once for the whole workgroup, and sum the group
+            const int t = tid >> 3, s = tid & 7;
+            const bool live = t0 + t < n_tok;
+            const float* src = x + (size_t)(live ? t0 + t : 0) * n_rows + sb * 256 + 32 * s;
+            float gs = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                float4 v = *reinterpret_cast<const float4*>(src + 4 * k);
+                if (!live) v = make_float4(0.f, 0.f, 0.f, 0.f);
+                gs += (v.x + v.y) + (v.z + v.w);
+                const TfSplit3 sp = tf_split3(v);
+#pragma unroll
+                for (int pl = 0; pl < 3; pl++)
+                    *reinterpret_cast<tf_bf16x4*>(xp + (pl * TF_PF_TOKS + t) * TF_PF_ROW +
+                                                  2 * (32 * s + 4 * k)) = sp.p[pl];
+            }
+            if constexpr (!Q6) xsum[t * 8 + s] = gs;
         }
         // scales of the workgroup's columns
         if (tid < TF_PF_COLS) {
@@ -200,47 +234,53 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
             }
         }
         __syncthreads();
-        if constexpr (!Q6) {
-            // sum of x over each 32-value group, per token
-            const int t = tid >> 3, s = tid & 7;
-            float a = 0.f;
-            for (int i = 0; i < 32; i++) a += xs[t * TF_PF_XSTRIDE + 32 * s + ((i + 4 * s) & 31)];
-            xsum[t * 8 + s] = a;
-            __syncthreads();
-        }
-        tf_f32x4 part[2][2];
-        for (int st = 0; st < 16; st++) {
-            const bool first = Q6 || (st & 1) == 0;
-            TfSplit3 b[2];
-            for (int tt = 0; tt < 2; tt++)
-                b[tt] = tf_split3(*reinterpret_cast<const float4*>(
-                    xs + (16 * tt + l16) * TF_PF_XSTRIDE + 16 * st + 4 * g));
-            for (int ct = 0; ct < 2; ct++) {
-                const tf_bf16x4 a = tf_pf_a<Q6>(wc[ct], st);
+        for (int s = 0; s < NSUB; s++) {
+            tf_f32x4 part[2][2];
+            if constexpr (!Q6) {
+                tf_s16x8 b[2][3];
                 for (int tt = 0; tt < 2; tt++)
-                    part[ct][tt] = tf_mfma3(a, b[tt], first ? tf_f32x4{0.f, 0.f, 0.f, 0.f}
-                                                            : part[ct][tt]);
-            }
-            const bool last = Q6 || (st & 1) == 1;
-            if (last) {
-                const int s = Q6 ? st : (st >> 1);
+                    for (int pl = 0; pl < 3; pl++)
+                        b[tt][pl] = *reinterpret_cast<const tf_s16x8*>(
+                            xp + (pl * TF_PF_TOKS + 16 * tt + l16) * TF_PF_ROW + 2 * (32 * s + 8 * g));
                 for (int ct = 0; ct < 2; ct++) {
-                    // scales of C rows 4g..4g+3 = columns 16 ct + 4g + r of this wave
-                    const float4 sc4 = *reinterpret_cast<const float4*>(
-                        scl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
-                    float4 mn4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if constexpr (!Q6)
-                        mn4 = *reinterpret_cast<const float4*>(
-                            mnl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
-                    const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-                    const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+                    const tf_s16x8 a = tf_pf_a4(wc[ct], s);
                     for (int tt = 0; tt < 2; tt++) {
-                        const float xs_s = Q6 ? 0.f : xsum[(16 * tt + l16) * 8 + (s & 7)];
-                        for (int r = 0; r < 4; r++) {
-                            float v = acc[ct][tt][r] + scv[r] * part[ct][tt][r];
-                            if constexpr (!Q6) v -= mnv[r] * xs_s;
-                            acc[ct][tt][r] = v;
-                        }
+                        tf_f32x4 c = tf_mfma32(a, b[tt][0], tf_f32x4{0.f, 0.f, 0.f, 0.f});
+                        c = tf_mfma32(a, b[tt][1], c);
+                        part[ct][tt] = tf_mfma32(a, b[tt][2], c);
+                    }
+                }
+            } else {
+                tf_bf16x4 b[2][3];
+                for (int tt = 0; tt < 2; tt++)
+                    for (int pl = 0; pl < 3; pl++)
+                        b[tt][pl] = *reinterpret_cast<const tf_bf16x4*>(
+                            xp + (pl * TF_PF_TOKS + 16 * tt + l16) * TF_PF_ROW + 2 * (16 * s + 4 * g));
+                for (int ct = 0; ct < 2; ct++) {
+                    const tf_bf16x4 a = tf_pf_a6(wc[ct], s);
+                    for (int tt = 0; tt < 2; tt++) {
+                        tf_f32x4 c = tf_mfma16(a, b[tt][0], tf_f32x4{0.f, 0.f, 0.f, 0.f});
+                        c = tf_mfma16(a, b[tt][1], c);
+                        part[ct][tt] = tf_mfma16(a, b[tt][2], c);
+                    }
+                }
+            }
+            for (int ct = 0; ct < 2; ct++) {
+                // scales of C rows 4g..4g+3 = columns 16 ct + 4g + r of this wave
+                const float4 sc4 = *reinterpret_cast<const float4*>(
+                    scl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
+                float4 mn4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (!Q6)
+                    mn4 = *reinterpret_cast<const float4*>(
+                        mnl + s * TF_PF_COLS + 32 * wave + 16 * ct + 4 * g);
+                const float scv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+                const float mnv[4] = {mn4.x, mn4.y, mn4.z, mn4.w};
+                for (int tt = 0; tt < 2; tt++) {
+                    const float xs_s = Q6 ? 0.f : xsum[(16 * tt + l16) * 8 + (s & 7)];
+                    for (int r = 0; r < 4; r++) {
+                        float v = acc[ct][tt][r] + scv[r] * part[ct][tt][r];
+                        if constexpr (!Q6) v -= mnv[r] * xs_s;
+                        acc[ct][tt][r] = v;
                     }
                 }
             }
