@@ -85,6 +85,25 @@ def decode_throughput(m, cfg, warmup, steps, seed):
     return dt, toks, e0.elapsed_time(e1) * 1e-3
 
 
+def prefill_throughput(m, cfg, n_tok, reps=3):
+    """Prompt tokens/s of the runtime's batched prefill (tf_model_prefill:
+    n_tok tokens from position 0, K/V written, last-token logits), median of
+    reps after one warm-up; host-timed, the call blocks on its stream."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, cfg["n_vocab"], n_tok).tolist()
+    m.prefill(toks, 0)
+    times = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill(toks, 0)
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    return {"prompt_tokens": n_tok, "ms": round(dt * 1e3, 2), "tok_s": round(n_tok / dt, 1)}
+
+
 def kernel_roofline(iters):
     """Config 1a: fused gate+up 2048 -> 2 x 11008 with the Q8 activation
     prepared by tf_quantize_q8 (the decode runtime's path)."""
@@ -269,6 +288,8 @@ def main():
     log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
     wbytes = synth.weight_bytes(cfg)
     path = m.path()
+    pf = prefill_throughput(m, cfg, 512)
+    log(f"[bench] prefill: {pf}")
     m.close()
     del m
     torch.cuda.empty_cache()
@@ -321,6 +342,7 @@ def main():
         "roofline": roof,
         "roofline_q4k_gemv": roof_gemv,
         "cpu_baseline": cpu,
+        "prefill": pf,
         "kernels": table,
         "greedy_tokens_head": [int(t) for t in toks[:8]],
     }

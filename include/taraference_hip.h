@@ -487,6 +487,16 @@ int tf_model_forward(tf_model *m, int token, int pos, int *next_token,
  * synchronized once, at the end. */
 int tf_model_generate(tf_model *m, const int *forced, int n_forced, int pos0,
                       int n_gen, int *tokens, int use_graph, tf_stream_t stream);
+/* cuda/forward.rs:42-71 forward_greedy for n_tok > 1 (the prompt): the
+ * tokens at positions pos0 .. pos0+n_tok-1 go through the n_tok-row forward
+ * in chunks of 256 (the prefill GEMMs and attention, f32 activations, as the
+ * reference's prefill), their K/V rows are written to the cache, and
+ * *next_token receives the argmax of the last token's logits (left on the
+ * device as after a decode step).  Continue with tf_model_generate(forced =
+ * {*next_token}, pos0 + n_tok, ...).  Weights must be Q4_K / Q6_K.  Blocks on
+ * the stream. */
+int tf_model_prefill(tf_model *m, const int *tokens, int n_tok, int pos0,
+                     int *next_token, tf_stream_t stream);
 /* Select the kernel sequence of a step (all compute the same step):
  *   0  the reference's sequence through the operator API (cuda/layer.rs
  *      order, one launch per reference kernel);

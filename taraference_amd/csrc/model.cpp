@@ -30,6 +30,7 @@
 #include "argmax_key.hpp"
 #include "decode_persistent.hpp"
 #include "op_api.hpp"
+#include "prefill.hpp"
 #include "taraference_hip.h"
 
 namespace {
@@ -123,6 +124,11 @@ struct tf_model {
     TfPArgs* d_pargs = nullptr;
     unsigned* d_flash_cnt = nullptr;  // per-kv-head tickets of tf_flash_decode
     int *d_forced = nullptr, *d_nforced = nullptr, *d_log = nullptr;
+    // prefill workspace (n_tok-row activations of one chunk), allocated on
+    // the first prefill
+    float *pf_x = nullptr, *pf_xb = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr,
+          *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr;
+    int* pf_tok = nullptr;
     std::vector<void*> allocs;
 
     hipGraph_t graph = nullptr;
@@ -547,6 +553,90 @@ struct tf_model {
         if (path == 4 && d_trace) dump_trace();
     }
 
+    // Prompt chunk size of the prefill (types.rs MAX_BATCH).
+    static constexpr int kPrefillChunk = 256;
+
+    static bool gemm_ok(const GpuMat& w) {
+        return w.wtype == tf::WType::Q4K || w.wtype == tf::WType::Q6K;
+    }
+
+    // x[t] (+)= W xin[t] for n rows on the matrix cores (raw GGUF bytes).
+    static void gemm(hipStream_t s, const GpuMat& w, const float* xin, float* out, int n,
+                     bool accumulate) {
+        tf::check(tf_gemm_kq(w.wtype == tf::WType::Q6K, w.data, xin, out, (int)w.n_rows,
+                             (int)w.n_cols, (int)w.col_bytes, n, accumulate ? 1 : 0,
+                             reinterpret_cast<tf_stream_t>(s)),
+                  "prefill gemm");
+    }
+
+    // The prompt forward of forward.rs:42-71 forward_greedy / :360-404
+    // forward_chunk: chunks of up to kPrefillChunk tokens through the
+    // n_tok-row layer (layer.rs attn_block / ffn_block_dense with
+    // n_tok > 1: rms_norm rows, GEMMs, add_bias, rope, copy_kv, prefill
+    // attention, GEMM + add for wo and down, silu_mul), K/V appended at
+    // positions pos0 .. pos0+n-1; then the last row's logits and argmax
+    // (logits_from_last), as the decode step computes them.
+    void prefill(hipStream_t s, const int* tokens, int n, int pos0) {
+        const tf_model_config& c = cfg;
+        if (n < 1 || pos0 < 0 || pos0 + n > c.max_seq)
+            throw tf::HipError((int)hipErrorInvalidValue, "prefill range outside the KV cache");
+        for (const Layer& L : layers)
+            if (!gemm_ok(L.wq) || !gemm_ok(L.wk) || !gemm_ok(L.wv) || !gemm_ok(L.wo) ||
+                !gemm_ok(L.gate) || !gemm_ok(L.up) || !gemm_ok(L.down))
+                throw tf::HipError((int)hipErrorNotSupported, "prefill needs Q4_K/Q6_K weights");
+        const int CH = kPrefillChunk, E = c.n_embd, F = c.n_ff;
+        const int kvd = c.n_kv * c.head_dim;
+        if (!pf_x) {
+            pf_x = alloc<float>((size_t)CH * E);
+            pf_xb = alloc<float>((size_t)CH * E);
+            pf_q = alloc<float>((size_t)CH * E);
+            pf_att = alloc<float>((size_t)CH * E);
+            pf_k = alloc<float>((size_t)CH * kvd);
+            pf_v = alloc<float>((size_t)CH * kvd);
+            pf_g = alloc<float>((size_t)CH * F);
+            pf_u = alloc<float>((size_t)CH * F);
+            pf_tok = alloc<int>(CH);
+        }
+        const tf_stream_t ts = reinterpret_cast<tf_stream_t>(s);
+        int last = 0;
+        for (int off = 0; off < n; off += CH) {
+            const int nt = n - off < CH ? n - off : CH;
+            const int p0 = pos0 + off;
+            tf::check((int)hipMemcpyAsync(pf_tok, tokens + off, sizeof(int) * nt,
+                                          hipMemcpyHostToDevice, s), "copy tokens");
+            tf::check(tf_pf_embed(token_embd.data, embd_block_bytes, pf_tok, pf_x, E,
+                                  (int)token_embd.col_bytes, nt, ts), "embed");
+            for (size_t li = 0; li < layers.size(); li++) {
+                const Layer& L = layers[li];
+                tf::check(tf_pf_rms_norm(pf_x, L.attn_norm, pf_xb, E, nt, c.rms_eps, ts), "rms");
+                gemm(s, L.wq, pf_xb, pf_q, nt, false);
+                gemm(s, L.wk, pf_xb, pf_k, nt, false);
+                gemm(s, L.wv, pf_xb, pf_v, nt, false);
+                tf::check(tf_pf_qkv_post(pf_q, pf_k, pf_v, L.bq, L.bk, L.bv, kc[li], vc[li],
+                                         c.n_head, c.n_kv, c.head_dim, p0, nt, c.rope_theta, ts),
+                          "qkv post");
+                tf::check(tf_attn_prefill_any(pf_q, kc[li], vc[li], pf_att, c.n_head, c.n_kv,
+                                              c.head_dim, p0, nullptr, nt, fd.scale, ts),
+                          "prefill attention");
+                gemm(s, L.wo, pf_att, pf_x, nt, true);
+                tf::check(tf_pf_rms_norm(pf_x, L.ffn_norm, pf_xb, E, nt, c.rms_eps, ts), "rms");
+                gemm(s, L.gate, pf_xb, pf_g, nt, false);
+                gemm(s, L.up, pf_xb, pf_u, nt, false);
+                tf::check(tf_pf_silu_mul(pf_g, pf_u, (long long)nt * F, ts), "silu_mul");
+                gemm(s, L.down, pf_g, pf_x, nt, true);
+            }
+            last = nt - 1;
+        }
+        // logits of the last prompt token (the decode step's head)
+        const float* xl = pf_x + (size_t)last * E;
+        tf::check(tf_rms_norm(xl, output_norm, xb, E, c.rms_eps, s), "rms_norm");
+        if (!tf::try_gemv_global_q8(s, output, xb, logits, nullptr, GemvResidual::none(), q8_x,
+                                    q8_d, gemv_partial, partial_stride))
+            tf::gemv(s, output, xb, logits, nullptr, GemvResidual::none(), gemv_partial,
+                     partial_stride);
+        tf::check(tf_argmax(logits, c.n_vocab, d_argmax, s), "argmax");
+    }
+
     void dump_trace() {
         std::vector<unsigned long long> h(trace_words);
         tf::check((int)hipMemcpy(h.data(), d_trace, trace_words * sizeof(unsigned long long),
@@ -679,6 +769,26 @@ extern "C" int tf_model_generate(tf_model* m, const int* forced, int n_forced, i
         return 0;
     } catch (const tf::HipError& e) {
         return e.code;
+    }
+}
+
+extern "C" int tf_model_prefill(tf_model* m, const int* tokens, int n_tok, int pos0,
+                                int* next_token, tf_stream_t stream) {
+    if (!m || !tokens || n_tok < 1 || pos0 < 0) return (int)hipErrorInvalidValue;
+    for (int i = 0; i < n_tok; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.n_vocab) return (int)hipErrorInvalidValue;
+    try {
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        m->prefill(s, tokens, n_tok, pos0);
+        if (next_token)
+            tf::check((int)hipMemcpyAsync(next_token, m->d_argmax, sizeof(int),
+                                          hipMemcpyDeviceToHost, s), "copy");
+        tf::check((int)hipStreamSynchronize(s), "sync");
+        return 0;
+    } catch (const tf::HipError& e) {
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        return (int)hipErrorOutOfMemory;
     }
 }
 

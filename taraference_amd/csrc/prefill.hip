@@ -34,6 +34,8 @@
 // B columns = tokens, C[i][j] with j = l % 16, i = 4g .. 4g+3:
 //   16x16x16: A[l % 16][4g .. 4g+3], B[4g .. 4g+3][l % 16];
 //   16x16x32: A[l % 16][8g .. 8g+7], B[8g .. 8g+7][l % 16].
+#include "dequant.hpp"
+#include "prefill.hpp"
 #include "tf_common.hpp"
 #include "tf_host.hpp"
 
@@ -164,7 +166,8 @@ template <bool Q6>
 __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restrict__ w,
                                                           const float* __restrict__ x,
                                                           float* __restrict__ out, int n_rows,
-                                                          int n_cols, int col_bytes, int n_tok) {
+                                                          int n_cols, int col_bytes, int n_tok,
+                                                          int accumulate) {
     constexpr int NSUB = Q6 ? 16 : 8;
     constexpr int BLK = Q6 ? 210 : 144;
     __shared__ __align__(16) uint8_t xp[TF_PF_XBYTES];
@@ -293,12 +296,18 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
             const int t = t0 + 16 * tt + l16;
             if (t >= n_tok) continue;
             float* o = out + (size_t)t * n_cols + cb;
+            // accumulate: out += W x (the residual stream), one rounding
             if (cb + 3 < n_cols && ((n_cols & 3) == 0)) {
-                *reinterpret_cast<float4*>(o) = make_float4(acc[ct][tt][0], acc[ct][tt][1],
-                                                            acc[ct][tt][2], acc[ct][tt][3]);
+                float4 v = make_float4(acc[ct][tt][0], acc[ct][tt][1], acc[ct][tt][2],
+                                       acc[ct][tt][3]);
+                if (accumulate) {
+                    const float4 o0 = *reinterpret_cast<const float4*>(o);
+                    v = make_float4(o0.x + v.x, o0.y + v.y, o0.z + v.z, o0.w + v.w);
+                }
+                *reinterpret_cast<float4*>(o) = v;
             } else {
                 for (int r = 0; r < 4; r++)
-                    if (cb + r < n_cols) o[r] = acc[ct][tt][r];
+                    if (cb + r < n_cols) o[r] = accumulate ? o[r] + acc[ct][tt][r] : acc[ct][tt][r];
             }
         }
     }
@@ -425,10 +434,160 @@ __global__ __launch_bounds__(256) void tf_attn_prefill_kernel(
     }
 }
 
+// ------------------------------------------------- batched prefill glue
+//
+// The n_tok-row forms of the decode glue (kernels/ops.cu rms_norm_f32 with
+// n_tok rows :4-34, add_bias_f32 :340, rope_neox_f32 :348, copy_kv_f16
+// :471, silu_mul_f32 :202; kernels/embed.cu embed_q{4,6}_k :1-50), used by
+// the runtime's prefill step.
+
+template <int BB>
+__global__ __launch_bounds__(256) void tf_pf_embed_kernel(const uint8_t* __restrict__ table,
+                                                          const int* __restrict__ tokens,
+                                                          float* __restrict__ out, int n_rows,
+                                                          int col_bytes) {
+    const int t = blockIdx.y;
+    const uint8_t* col = table + (size_t)tokens[t] * col_bytes;
+    const int nb = n_rows / 256;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nb * 256; i += gridDim.x * blockDim.x) {
+        const uint8_t* blk = col + (size_t)(i >> 8) * BB;
+        out[(size_t)t * n_rows + i] = BB == 144 ? tf_q4k_value(blk, i & 255) : tf_q6k_value(blk, i & 255);
+    }
+}
+
+// One row per workgroup, the decode RMSNorm's order (256 strided fused
+// square sums, halving tree).
+__global__ __launch_bounds__(256) void tf_pf_rms_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        float* __restrict__ out, int n, float eps) {
+    __shared__ float buf[256];
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* orow = out + (size_t)blockIdx.x * n;
+    float local = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        local = fmaf(v, v, local);
+    }
+    buf[threadIdx.x] = local;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) buf[threadIdx.x] += buf[threadIdx.x + s];
+        __syncthreads();
+    }
+    const float scale = 1.0f / sqrtf(buf[0] / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) orow[i] = xr[i] * scale * w[i];
+}
+
+// q/k/v rows of token t (position pos0 + t): add the biases, rotate q and k
+// (NeoX pairs (i, i + hd/2) by (pos0+t) theta^(-2i/hd)), append k and v to
+// the f16 cache.  Grid (n_head + 2 n_kv, n_tok): head blocks of q, then k,
+// then v.
+__global__ __launch_bounds__(64) void tf_pf_qkv_post_kernel(
+    float* __restrict__ q, float* __restrict__ k, float* __restrict__ v,
+    const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int n_head, int n_kv, int hd, int pos0,
+    float theta) {
+    const int t = blockIdx.y, hb = blockIdx.x;
+    const int kvd = n_kv * hd, pos = pos0 + t;
+    float* base;
+    const float* b;
+    uint16_t* cache = nullptr;
+    bool rot = true;
+    if (hb < n_head) {
+        base = q + (size_t)t * n_head * hd + hb * hd;
+        b = bq ? bq + hb * hd : nullptr;
+    } else if (hb < n_head + n_kv) {
+        const int h = hb - n_head;
+        base = k + (size_t)t * kvd + h * hd;
+        b = bk ? bk + h * hd : nullptr;
+        cache = kc + (size_t)pos * kvd + h * hd;
+    } else {
+        const int h = hb - n_head - n_kv;
+        base = v + (size_t)t * kvd + h * hd;
+        b = bv ? bv + h * hd : nullptr;
+        cache = vc + (size_t)pos * kvd + h * hd;
+        rot = false;
+    }
+    const int half = hd / 2;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        float x0 = base[i], x1 = base[i + half];
+        if (b) {
+            x0 += b[i];
+            x1 += b[i + half];
+        }
+        if (rot) {
+            const float freq = powf(theta, -2.f * (float)i / (float)hd);
+            const float ang = (float)pos * freq;
+            float sn, cs;
+            sincosf(ang, &sn, &cs);
+            const float r0 = x0 * cs - x1 * sn, r1 = x0 * sn + x1 * cs;
+            x0 = r0;
+            x1 = r1;
+        }
+        base[i] = x0;
+        base[i + half] = x1;
+        if (cache) {
+            cache[i] = tf_f2h_halfup(x0);
+            cache[i + half] = tf_f2h_halfup(x1);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void tf_pf_silu_mul_kernel(float* __restrict__ g,
+                                                             const float* __restrict__ u,
+                                                             long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float v = g[i];
+        g[i] = (v / (1.f + __expf(-v))) * u[i];
+    }
+}
+
+int tf_pf_embed(const uint8_t* table, int block_bytes, const int* tokens_dev, float* out,
+                int n_rows, int col_bytes, int n_tok, tf_stream_t stream) {
+    const int nb = n_rows / 256;
+    TF_CHECK_ARG(table && tokens_dev && out && nb > 0 && n_tok > 0);
+    TF_CHECK_ARG((block_bytes == 144 || block_bytes == 210) && col_bytes >= nb * block_bytes);
+    const dim3 grid((nb * 256 + 255) / 256, n_tok);
+    if (block_bytes == 144)
+        hipLaunchKernelGGL(tf_pf_embed_kernel<144>, grid, dim3(256), 0, tf_stream(stream), table,
+                           tokens_dev, out, n_rows, col_bytes);
+    else
+        hipLaunchKernelGGL(tf_pf_embed_kernel<210>, grid, dim3(256), 0, tf_stream(stream), table,
+                           tokens_dev, out, n_rows, col_bytes);
+    return TF_LAUNCH_RESULT();
+}
+
+int tf_pf_rms_norm(const float* x, const float* w, float* out, int n, int n_tok, float eps,
+                   tf_stream_t stream) {
+    TF_CHECK_ARG(x && w && out && n > 0 && n_tok > 0);
+    hipLaunchKernelGGL(tf_pf_rms_kernel, dim3(n_tok), dim3(256), 0, tf_stream(stream), x, w, out,
+                       n, eps);
+    return TF_LAUNCH_RESULT();
+}
+
+int tf_pf_qkv_post(float* q, float* k, float* v, const float* bq, const float* bk,
+                   const float* bv, uint16_t* k_cache, uint16_t* v_cache, int n_head, int n_kv,
+                   int head_dim, int pos0, int n_tok, float theta, tf_stream_t stream) {
+    TF_CHECK_ARG(q && k && v && k_cache && v_cache && n_head > 0 && n_kv > 0 && n_tok > 0);
+    TF_CHECK_ARG(head_dim > 0 && (head_dim & 1) == 0 && pos0 >= 0);
+    hipLaunchKernelGGL(tf_pf_qkv_post_kernel, dim3(n_head + 2 * n_kv, n_tok), dim3(64), 0,
+                       tf_stream(stream), q, k, v, bq, bk, bv, k_cache, v_cache, n_head, n_kv,
+                       head_dim, pos0, theta);
+    return TF_LAUNCH_RESULT();
+}
+
+int tf_pf_silu_mul(float* g, const float* u, long long n, tf_stream_t stream) {
+    TF_CHECK_ARG(g && u && n > 0);
+    hipLaunchKernelGGL(tf_pf_silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       tf_stream(stream), g, u, n);
+    return TF_LAUNCH_RESULT();
+}
+
 // ---------------------------------------------------------------- C ABI
 
-static int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows,
-                      int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
+int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows, int n_cols,
+               int col_bytes, int n_tok, int accumulate, tf_stream_t stream) {
     const int nb = n_rows / 256;
     const int blk = q6 ? 210 : 144;
     TF_CHECK_ARG(w && x && out && nb > 0 && n_cols > 0 && n_tok > 0);
@@ -440,24 +599,24 @@ static int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int
     TF_CHECK_ARG(grid.y <= 65535);
     if (q6)
         hipLaunchKernelGGL(tf_gemm_kq_kernel<true>, grid, dim3(256), 0, tf_stream(stream), w, x,
-                           out, n_rows, n_cols, col_bytes, n_tok);
+                           out, n_rows, n_cols, col_bytes, n_tok, accumulate);
     else
         hipLaunchKernelGGL(tf_gemm_kq_kernel<false>, grid, dim3(256), 0, tf_stream(stream), w, x,
-                           out, n_rows, n_cols, col_bytes, n_tok);
+                           out, n_rows, n_cols, col_bytes, n_tok, accumulate);
     return TF_LAUNCH_RESULT();
 }
 
 extern "C" int tf_gemm_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
                                int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
-    return tf_gemm_kq(false, w, x, out, n_rows, n_cols, col_bytes, n_tok, stream);
+    return tf_gemm_kq(false, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream);
 }
 
 extern "C" int tf_gemm_q6k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
                                int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
-    return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, stream);
+    return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream);
 }
 
-static int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                float* out, int n_head, int n_kv, int head_dim, int pos0,
                                const int* pos0_dev, int n_q, float scale, tf_stream_t stream) {
     TF_CHECK_ARG(q && k_cache && v_cache && out && n_head > 0 && n_kv > 0 && n_q > 0);

@@ -157,6 +157,7 @@ static const char* const k_symbols[] = {
     "tf_model_destroy",
     "tf_model_forward",
     "tf_model_generate",
+    "tf_model_prefill",
     "tf_model_set_path",
     "tf_model_get_path",
     "tf_model_logits",

@@ -49,6 +49,9 @@ def _bind(lib):
     lib.tf_model_generate.argtypes = [C.c_void_p, C.POINTER(C.c_int), C.c_int, C.c_int,
                                       C.c_int, C.POINTER(C.c_int), C.c_int, C.c_void_p]
     lib.tf_model_generate.restype = C.c_int
+    lib.tf_model_prefill.argtypes = [C.c_void_p, C.POINTER(C.c_int), C.c_int, C.c_int,
+                                     C.POINTER(C.c_int), C.c_void_p]
+    lib.tf_model_prefill.restype = C.c_int
     lib.tf_model_set_path.argtypes = [C.c_void_p, C.c_int]
     lib.tf_model_set_path.restype = C.c_int
     lib.tf_model_get_path.argtypes = [C.c_void_p]
@@ -274,6 +277,28 @@ class DecodeModel:
         if rc != 0:
             raise capi.HipError(f"tf_model_generate returned {rc}")
         return np.array(out[:n_gen], np.int32)
+
+    def prefill(self, tokens, pos0: int = 0) -> int:
+        """Run the prompt `tokens` (positions pos0 ..) through the batched
+        prefill forward; their K/V rows land in the cache and the argmax of
+        the last token's logits is returned (the first generated token)."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        arr = (C.c_int * len(tokens))(*tokens.tolist())
+        nxt = C.c_int()
+        rc = self.lib.tf_model_prefill(self.h, arr, len(tokens), pos0, C.byref(nxt), self.stream)
+        if rc != 0:
+            raise capi.HipError(f"tf_model_prefill returned {rc}")
+        return nxt.value
+
+    def generate_prefilled(self, prompt, n_gen: int, use_graph: bool = True):
+        """Greedy continuation of `prompt` with the prompt run through
+        prefill(): the first token is prefill's argmax, the rest decode
+        steps (forward.rs forward_greedy, then single-token decode)."""
+        first = self.prefill(prompt, 0)
+        if n_gen <= 1:
+            return np.array([first][:n_gen], np.int32)
+        rest = self.generate([first], n_gen - 1, pos0=len(prompt), use_graph=use_graph)
+        return np.concatenate([[first], rest]).astype(np.int32)
 
     def close(self):
         if getattr(self, "h", None):

@@ -77,3 +77,51 @@ class RefModel:
         xb = oracle.rms_norm(x, np.ones(e, np.float32), c["rms_eps"])
         logits = self._global_q8((self.E, self.ecb), e, xb, True)
         return logits, oracle.argmax(logits)
+
+    def prefill(self, tokens, pos0=0):
+        """The n_tok-row prompt forward (forward.rs:42-71, layer.rs with
+        n_tok > 1): f32 GEMMs (kernels/gemm.cu), add_bias, rope, copy_kv,
+        prefill attention (attn/fast_v2.cu), GEMM + add for wo and down,
+        silu_mul; then the decode head on the last row.  Fills the K/V rows
+        pos0 .. pos0+n-1; returns (logits, argmax) of the last token."""
+        c = self.c
+        e, hd, F = c["n_embd"], c["head_dim"], c["n_ff"]
+        nq, nkv = c["n_head"] * hd, c["n_kv"] * hd
+        T = len(tokens)
+        scale = float(np.float32(1.0 / np.sqrt(hd)))
+        x = np.stack([oracle.embed_row(self.E, 210, int(t), e, self.ecb) for t in tokens])
+
+        def rows_norm(a, w):
+            return np.stack([oracle.rms_norm(r, w, c["rms_eps"]) for r in a])
+
+        def gemm(wm, a, n_rows, q6k):
+            w, cb = wm
+            fn = oracle.gemm_q6k if q6k else oracle.gemm_q4k
+            return fn(w, np.ascontiguousarray(a, np.float32), n_rows, w.shape[0], cb, a.shape[0])
+
+        for li, L in enumerate(self.L):
+            xb = rows_norm(x, L["attn_norm"])
+            q = gemm(L["wq"], xb, e, False)
+            k = gemm(L["wk"], xb, e, False)
+            v = gemm(L["wv"], xb, e, True)
+            if L.get("bq") is not None:
+                q = q + L["bq"]
+                k = k + L["bk"]
+                v = v + L["bv"]
+            for t in range(T):
+                q[t] = oracle.rope_neox(q[t], c["n_head"], hd, pos0 + t, c["rope_theta"])
+                k[t] = oracle.rope_neox(k[t], c["n_kv"], hd, pos0 + t, c["rope_theta"])
+                self.K[li][pos0 + t] = oracle.f32_to_f16(k[t])
+                self.V[li][pos0 + t] = oracle.f32_to_f16(v[t])
+            att = oracle.attn_prefill(q, self.K[li], self.V[li], c["n_head"], c["n_kv"], hd,
+                                      pos0, T, scale)
+            x = (x + gemm(L["wo"], att, nq, False)).astype(np.float32)
+            xb = rows_norm(x, L["ffn_norm"])
+            g = gemm(L["gate"], xb, e, False)
+            u = gemm(L["up"], xb, e, False)
+            with np.errstate(over="ignore"):  # exp(-g) = inf -> silu 0, as __expf
+                h = ((g / (np.float32(1) + np.exp(-g))) * u).astype(np.float32)
+            x = (x + gemm(L["down"], h, F, L["down_q6k"])).astype(np.float32)
+        xb = oracle.rms_norm(x[-1], np.ones(e, np.float32), c["rms_eps"])
+        logits = self._global_q8((self.E, self.ecb), e, xb, True)
+        return logits, oracle.argmax(logits)
