@@ -85,6 +85,43 @@ def decode_throughput(m, cfg, warmup, steps, seed):
     return dt, toks, e0.elapsed_time(e1) * 1e-3
 
 
+def config4(ctx=32768, n_gen=128):
+    """Config 4: a random-init Qwen2.5-7B-shape Q4_K_M model, the context
+    written by tf_model_prefill (timed once), then n_gen greedy decode steps
+    timed as in decode_throughput (HIP events on the replay stream)."""
+    import torch
+
+    from taraference_amd import synth
+
+    cfg = dict(synth.QWEN25_7B)
+    m = build_model(cfg, 0x7A7A0004, ctx + n_gen + 8)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, cfg["n_vocab"], ctx).tolist()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    first = m.prefill(prompt, 0)
+    t_pf = time.perf_counter() - t0
+    m.generate([first], 2, pos0=ctx, use_graph=True)  # graph capture, untimed
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    toks = m.generate([first], n_gen, pos0=ctx, use_graph=True)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out = {"config": "4: Qwen2.5-7B-shape Q4_K_M, 32768-token context, 128 greedy tokens",
+           "path": m.path(), "prefill_tokens": ctx, "prefill_s": round(t_pf, 3),
+           "prefill_tok_s": round(ctx / t_pf, 1), "decode_tokens": n_gen,
+           "decode_tok_s": round(n_gen / dt, 2), "ms_per_token": round(dt * 1e3 / n_gen, 3),
+           "ms_per_token_events": round(e0.elapsed_time(e1) / n_gen, 3),
+           "weight_bytes_per_token": synth.weight_bytes(cfg),
+           "greedy_tokens_head": [int(t) for t in toks[:8]]}
+    m.close()
+    return out
+
+
 def prefill_throughput(m, cfg, n_tok, reps=3):
     """Prompt tokens/s of the runtime's batched prefill (tf_model_prefill:
     n_tok tokens from position 0, K/V written, last-token logits), median of
@@ -253,6 +290,9 @@ def main():
                     help="decode kernel sequence (tf_model_set_path); default: the library's")
     ap.add_argument("--only-roofline", action="store_true",
                     help="run only the copy calibration and the roofline kernel (for counter runs)")
+    ap.add_argument("--config4", action="store_true",
+                    help="BASELINE config 4 instead: Qwen2.5-7B shape, 32768-token context "
+                         "filled by prefill, then 128 timed greedy tokens")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     args = ap.parse_args()
@@ -272,6 +312,9 @@ def main():
         r = kernel_roofline(args.kernel_iters)
         print(json.dumps({"kernel": ROOFLINE_KERNEL, "bytes": int(r["bytes"]),
                           "us_b2b": round(r["b2b_us"], 3), "us_single": round(r["per_us"], 3)}))
+        return
+    if args.config4:
+        print(json.dumps(config4()), flush=True)
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
