@@ -18,6 +18,7 @@
 //            LDS, V row from LDS.
 // Each wave owns whole heads, so (m, l, O) is written without a merge.
 #include <math.h>
+#include <stdlib.h>
 
 #include "tf_common.hpp"
 #include "tf_host.hpp"
@@ -307,10 +308,318 @@ __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
     if (tid == 0) counters[kv_h] = 0u;
 }
 
-// Log-sum-exp merge of the partitions of one head per workgroup: the
-// partition weights e^(m_s - M) go to LDS once; each thread then owns one
-// dimension and a strided subset of partitions, and the subsets are summed
-// through LDS.
+// ------------------------------------------------ matrix-core partial
+//
+// head_dim 128, G <= 16 query heads per kv head.  For one kv head the
+// scores of a 64-token tile are a small GEMM, S[16 heads][64 tokens] =
+// Q[16][128] K^T, and the output update is another, O[16][128] += P V, so
+// both run on v_mfma_f32_16x16x16_f16 (heads padded to 16 rows):
+//   QK: wave w takes tokens 16w .. 16w+15 (8 K steps of 16 dims); K is f16
+//       (exact), q is split into three f16 parts after a power-of-two scale
+//       that keeps it inside the f16 range, so the products are exact and
+//       the dot is fp32-accurate;
+//   softmax: in the QK result a 16-lane DPP row holds one head's 16 tokens
+//       of the wave, so the tile max and sum of a head are a DPP row
+//       reduction per wave plus four per-wave values through LDS; every
+//       lane keeps the running (m, l) of its heads 4g .. 4g+3 (the rows it
+//       also holds in the PV result), alpha = e^(m - m_new), and writes
+//       p = e^(s - m_new) to LDS for the PV A operand;
+//   PV: wave w takes dims 32w .. 32w+31; p is split into two f16 parts
+//       (2^-22 relative), V is f16; its B fragment (4 tokens of one dim) is
+//       gathered with four 2-byte LDS reads from the row-major tile, which
+//       the 16 lanes of a row read as one contiguous 32-byte run.
+// Every K/V byte is read from LDS by one wave only (the VALU kernel reads
+// the tile once per wave).  MFMA 16x16x16 layout (lane l, g = l / 16):
+// A[l % 16][4g .. 4g+3], B[4g .. 4g+3][l % 16], C[4g + r][l % 16].
+
+typedef _Float16 tf_h16x4 __attribute__((ext_vector_type(4)));
+typedef float tf_f32x4m __attribute__((ext_vector_type(4)));
+
+#define TF_FM_KROW 136  // halves per K row (128 dims + 8)
+#define TF_FM_VROW 136  // halves per V row (128 dims + 8)
+#define TF_FM_SROW 68   // floats per score / weight row (64 tokens + 4)
+#define TF_FM_LDS (64 * TF_FM_KROW * 2 + 64 * TF_FM_VROW * 2 + 16 * TF_FM_SROW * 4 + 128 * 4)
+
+#ifdef TF_FLASH_STAMPS
+__device__ unsigned long long tf_flash_stamps[512];
+#define TF_FSTAMP(k)                                                                        \
+    do {                                                                                   \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && (k) < 512)           \
+            tf_flash_stamps[(k)] = __builtin_amdgcn_s_memrealtime();                        \
+    } while (0)
+extern "C" int tf_flash_debug_stamps(unsigned long long* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tf_flash_stamps), sizeof(tf_flash_stamps));
+}
+#else
+#define TF_FSTAMP(k) \
+    do {             \
+    } while (0)
+#endif
+
+__device__ __forceinline__ tf_f32x4m tf_mfma_h16(tf_h16x4 a, tf_h16x4 b, tf_f32x4m c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void tf_flash_partial_mfma_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, float* __restrict__ partial, int n_head, int n_kv,
+    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale,
+    unsigned* __restrict__ counters, float* __restrict__ out, int8_t* __restrict__ q8,
+    float* __restrict__ d8) {
+    constexpr int HD = 128;
+    constexpr int PER_THREAD = 64 * HD / 8 / 256;  // 16-byte chunks of a tile per thread
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    uint16_t* k_lds = reinterpret_cast<uint16_t*>(lds_raw);   // [64][KROW]
+    uint16_t* v_lds = k_lds + 64 * TF_FM_KROW;                 // [64][VROW]
+    float* s_lds = reinterpret_cast<float*>(v_lds + 64 * TF_FM_VROW);  // [16][SROW]
+    float* mx_lds = s_lds + 16 * TF_FM_SROW;                   // [4 waves][16 heads]
+    float* sm_lds = mx_lds + 64;                               // [4 waves][16 heads]
+
+    TF_FSTAMP(0);
+    const int kv_h = blockIdx.x, s = blockIdx.y;
+    const int G = n_head / n_kv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int stride = n_kv * HD;
+    if (pos0_dev) pos0 = pos0_dev[0];
+    const int seq_len = pos0 + 1;
+    const int chunk = (seq_len + n_split - 1) / n_split;
+    const int t_begin = s * chunk;
+    const int t_end = min(t_begin + chunk, seq_len);
+    const uint16_t* kbase = k_cache + (size_t)kv_h * HD;
+    const uint16_t* vbase = v_cache + (size_t)kv_h * HD;
+
+    // two tiles in flight: buffer b holds tile t_begin + 64 (it + 2j) for
+    // it % 2 == b; loads are unconditional from a clamped row (rows past
+    // the split are zeroed when staged)
+    tf_u32x4 kr[2][PER_THREAD], vr[2][PER_THREAD];
+    auto load_tile = [&](int t0, tf_u32x4 (&kb)[PER_THREAD], tf_u32x4 (&vb)[PER_THREAD]) {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; i++) {
+            const int c = tid + 256 * i;
+            const int r = c / (HD / 8), col = 8 * (c % (HD / 8));
+            const int t = t0 + r;
+            const size_t off = (size_t)(t < t_end ? t : 0) * stride + col;
+            kb[i] = tf_ld16(kbase + off);
+            vb[i] = tf_ld16(vbase + off);
+        }
+    };
+    if (t_begin < t_end) load_tile(t_begin, kr[0], vr[0]);
+    if (t_begin + 64 < t_end) load_tile(t_begin + 64, kr[1], vr[1]);
+
+    // q fragments: head l16, dims 16 st + 4g .. +3, as three f16 parts of
+    // q * 2^-e (|q| 2^-e < 2^15)
+    float qv[8][4];
+    float qmax = 0.f;
+    {
+        const bool hv = l16 < G;
+        const float* qh = q + (size_t)(kv_h * G + (hv ? l16 : 0)) * HD;
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            float4 v = *reinterpret_cast<const float4*>(qh + 16 * st + 4 * g);
+            if (!hv) v = make_float4(0.f, 0.f, 0.f, 0.f);
+            qv[st][0] = v.x;
+            qv[st][1] = v.y;
+            qv[st][2] = v.z;
+            qv[st][3] = v.w;
+            qmax = fmaxf(qmax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    }
+    qmax = tf_wave_max(qmax);
+    const int e = qmax >= 16384.f ? ilogbf(qmax) - 13 : 0;
+    tf_h16x4 qa[8][3];
+#pragma unroll
+    for (int st = 0; st < 8; st++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x = ldexpf(qv[st][i], -e);
+            const _Float16 p0 = (_Float16)x;
+            x -= (float)p0;
+            const _Float16 p1 = (_Float16)x;
+            x -= (float)p1;
+            qa[st][0][i] = p0;
+            qa[st][1][i] = p1;
+            qa[st][2][i] = (_Float16)x;
+        }
+    const float sc = ldexpf(scale, e);
+    TF_FSTAMP(1);
+
+    float m[4], l[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+        m[hh] = TF_NEG_BIG;
+        l[hh] = 0.f;
+    }
+    // O of dims 32 wave + 16 b + l16, kept as the hi- and lo-weight sums
+    tf_f32x4m o[2] = {tf_f32x4m{0.f, 0.f, 0.f, 0.f}, tf_f32x4m{0.f, 0.f, 0.f, 0.f}};
+    tf_f32x4m olo[2] = {tf_f32x4m{0.f, 0.f, 0.f, 0.f}, tf_f32x4m{0.f, 0.f, 0.f, 0.f}};
+
+    auto tile = [&](int t0, tf_u32x4 (&kb)[PER_THREAD], tf_u32x4 (&vb)[PER_THREAD]) {
+        const int sk = 2 + 5 * ((t0 - t_begin) >> 6);
+        __syncthreads();  // the previous tile is consumed
+        TF_FSTAMP(sk);
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; i++) {
+            const int c = tid + 256 * i;
+            const int r = c / (HD / 8), col = 8 * (c % (HD / 8));
+            const bool live = t0 + r < t_end;
+            const tf_u32x4 kw = live ? kb[i] : tf_u32x4{0, 0, 0, 0};
+            const tf_u32x4 vv = live ? vb[i] : tf_u32x4{0, 0, 0, 0};
+            *reinterpret_cast<tf_u32x4*>(k_lds + r * TF_FM_KROW + col) = kw;
+            *reinterpret_cast<tf_u32x4*>(v_lds + r * TF_FM_VROW + col) = vv;
+        }
+        if (t0 + 128 < t_end) load_tile(t0 + 128, kb, vb);  // two tiles ahead
+        __syncthreads();
+        TF_FSTAMP(sk + 1);
+        // ---- scores S[h = 4g + r][t = 16 wave + l16] (C layout of the QK MFMA)
+        float sv[4];
+        {
+            // three independent accumulator chains (one per q part)
+            tf_f32x4m c0 = tf_f32x4m{0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
+            const uint16_t* kp = k_lds + (16 * wave + l16) * TF_FM_KROW + 4 * g;
+            // every K fragment read is issued before the first MFMA waits on one
+            tf_h16x4 kf[8];
+#pragma unroll
+            for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const tf_h16x4*>(kp + 16 * st);
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                c0 = tf_mfma_h16(qa[st][0], kf[st], c0);
+                c1 = tf_mfma_h16(qa[st][1], kf[st], c1);
+                c2 = tf_mfma_h16(qa[st][2], kf[st], c2);
+            }
+            const tf_f32x4m c = c0 + (c1 + c2);
+            const bool tv = t0 + 16 * wave + l16 < t_end;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sv[r] = tv ? c[r] * sc : TF_NEG_BIG;
+                // a 16-lane DPP row holds one head's 16 tokens of this wave
+                const float wm = tf_row16_max(sv[r]);
+                if (l16 == 0) mx_lds[wave * 16 + 4 * g + r] = wm;
+            }
+        }
+        __syncthreads();
+        TF_FSTAMP(sk + 2);
+        // ---- online softmax: every lane keeps (m, l) of its heads 4g .. 4g+3
+        float alpha[4];
+        {
+            const bool tv = t0 + 16 * wave + l16 < t_end;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int h = 4 * g + r;
+                const float tm = fmaxf(fmaxf(mx_lds[h], mx_lds[16 + h]),
+                                       fmaxf(mx_lds[32 + h], mx_lds[48 + h]));
+                const float m_new = fmaxf(m[r], tm);
+                alpha[r] = __expf(m[r] - m_new);
+                const float p = tv ? __expf(sv[r] - m_new) : 0.f;
+                m[r] = m_new;
+                s_lds[h * TF_FM_SROW + 16 * wave + l16] = p;
+                const float ws = tf_row16_sum(p);
+                if (l16 == 0) sm_lds[wave * 16 + h] = ws;
+            }
+        }
+        __syncthreads();
+        TF_FSTAMP(sk + 3);
+        // ---- l and O: O[h][d] = alpha_h O[h][d] + sum_t p[h][t] V[t][d]
+        // for dims 32 wave .. +31 (the PV C rows are the same heads 4g + r)
+        {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int h = 4 * g + r;
+                l[r] = l[r] * alpha[r] +
+                       ((sm_lds[h] + sm_lds[16 + h]) + (sm_lds[32 + h] + sm_lds[48 + h]));
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    o[b][r] *= alpha[r];
+                    olo[b][r] *= alpha[r];
+                }
+            }
+            // all P and V fragment reads first, then the MFMAs
+            float4 pf[4];
+            uint16_t vf[4][2][4];
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                pf[ts] = *reinterpret_cast<const float4*>(s_lds + l16 * TF_FM_SROW + 16 * ts + 4 * g);
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    const uint16_t* vp = v_lds + (16 * ts + 4 * g) * TF_FM_VROW + 32 * wave +
+                                         16 * b + l16;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) vf[ts][b][i] = vp[i * TF_FM_VROW];
+                }
+            }
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                const float pp[4] = {pf[ts].x, pf[ts].y, pf[ts].z, pf[ts].w};
+                tf_h16x4 ahi, alo;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const _Float16 h0 = (_Float16)pp[i];
+                    ahi[i] = h0;
+                    alo[i] = (_Float16)(pp[i] - (float)h0);
+                }
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    tf_h16x4 bv;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) bv[i] = __builtin_bit_cast(_Float16, vf[ts][b][i]);
+                    o[b] = tf_mfma_h16(ahi, bv, o[b]);
+                    olo[b] = tf_mfma_h16(alo, bv, olo[b]);
+                }
+            }
+            TF_FSTAMP(sk + 4);
+        }
+    };
+    for (int t0 = t_begin; t0 < t_end; t0 += 128) {
+        tile(t0, kr[0], vr[0]);
+        if (t0 + 64 < t_end) tile(t0 + 64, kr[1], vr[1]);
+    }
+
+    // ---- (m, l, O) of the kv head's G heads
+    const int po = 2 + HD;
+    if (wave == 0 && l16 == 0) {  // lanes 0, 16, 32, 48 hold heads 4g .. 4g+3
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = 4 * g + r;
+            if (h < G) {
+                float* base = partial + ((size_t)(kv_h * G + h) * n_split + s) * po;
+                base[0] = m[r];
+                base[1] = l[r];
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = 4 * g + r;
+            if (h < G)
+                partial[((size_t)(kv_h * G + h) * n_split + s) * po + 2 + 32 * wave + 16 * b + l16] =
+                    o[b][r] + olo[b][r];
+        }
+    if (counters == nullptr) return;
+    // fused merge, as the VALU kernel
+    __shared__ int s_last_m;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(counters + kv_h, 1u, __ATOMIC_ACQ_REL,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        s_last_m = prev == (unsigned)(n_split - 1);
+    }
+    __syncthreads();
+    if (!s_last_m) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    tf_flash_merge_group<(16 * HD + 255) / 256>(partial, out, q8, d8, kv_h * G, G, HD, n_split,
+                                                reinterpret_cast<float*>(lds_raw));
+    if (tid == 0) counters[kv_h] = 0u;
+}
+
+// Log-sum-exp merge of the partitions (flash.cu:222-255).  Workgroup
+// (head h, dim chunk c) produces dims 32c .. 32c+31 of head h: every
+// workgroup forms the partition weights e^(m_s - M) (in LDS) and
+// L = sum_s e^(m_s - M) l_s; thread (sub, d) sums partitions
+// sub, sub + 8, ... of dim d, and the eight subset sums are added in order.
+// With q8, the chunk's 32 outputs are one Q8 group.
 __global__ __launch_bounds__(256) void tf_flash_reduce_kernel(const float* __restrict__ partial,
                                                               float* __restrict__ out,
                                                               int8_t* __restrict__ q8,
@@ -342,38 +651,44 @@ __global__ __launch_bounds__(256) void tf_flash_reduce_kernel(const float* __res
     if (tid == 0) stat[0] = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
     const float L = stat[0];
-    const int subsets = 256 / head_dim;  // head_dim <= 256
-    const int d = tid % head_dim, sub = tid / head_dim;
+    const int dl = tid & 31, sub = tid >> 5;
+    const int d = 32 * blockIdx.y + dl;
     float acc = 0.f;
-    if (sub < subsets) {
+    if (d < head_dim) {
 #pragma unroll 8
-        for (int s = sub; s < n_split; s += subsets) acc += wts[s] * ph[(size_t)s * po + 2 + d];
+        for (int s = sub; s < n_split; s += 8) acc += wts[s] * ph[(size_t)s * po + 2 + d];
     }
     red[tid] = acc;
     __syncthreads();
-    // waves that hold output dims (head_dim is a multiple of 64 when q8 is
-    // requested, so the test below is wave-uniform)
-    if (tid < head_dim || (q8 && (tid >> 6) * 64 < head_dim)) {
-        float v = 0.f;
-        if (tid < head_dim) {
-            float tot = 0.f;
-            for (int k = 0; k < subsets; k++) tot += red[k * head_dim + tid];
-            v = tot / fmaxf(L, 1e-20f);
-            out[(size_t)h * head_dim + tid] = v;
-        }
-        if (q8) {  // quantize_q8 of the attention output: 32-value groups
+    if (tid < 32) {  // wave 0, lanes 0..31: the chunk's outputs
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) tot += red[32 * k + tid];
+        const float v = d < head_dim ? tot / fmaxf(L, 1e-20f) : 0.f;
+        const size_t i = (size_t)h * head_dim + d;
+        if (d < head_dim) out[i] = v;
+        if (q8) {  // quantize_q8 of the attention output: this 32-value group
             const float amax = tf_group32_max(fabsf(v));
-            const float d = amax * (1.0f / 127.0f);
-            const size_t i = (size_t)h * head_dim + tid;
-            if (tid < head_dim) {
-                q8[i] = (int8_t)tf_q8_value(v, amax, d);
-                if ((tid & 31) == 0) d8[i >> 5] = d;
+            const float dq = amax * (1.0f / 127.0f);
+            if (d < head_dim) {
+                q8[i] = (int8_t)tf_q8_value(v, amax, dq);
+                if (dl == 0) d8[i >> 5] = dq;
             }
         }
     }
 }
 
 // ---------------------------------------------------------------- dispatch
+
+// The matrix-core partial serves head_dim 128 (set TF_FLASH_VALU=1 in the
+// environment to use the vector-ALU kernel for every head_dim).
+static bool tf_flash_use_mfma() {
+    static const bool on = [] {
+        const char* e = getenv("TF_FLASH_VALU");
+        return !(e && e[0] == '1');
+    }();
+    return on;
+}
 
 template <int HD>
 static int tf_flash_lds_bytes(int hpw) {
@@ -389,6 +704,12 @@ static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t*
                               float* out, int8_t* q8, float* d8, tf_stream_t stream) {
     const int G = n_head / n_kv;
     const dim3 grid(n_kv, n_split);
+    if (HD == 128 && G <= 16 && tf_flash_use_mfma()) {
+        hipLaunchKernelGGL(tf_flash_partial_mfma_kernel, grid, dim3(256), TF_FM_LDS,
+                           tf_stream(stream), q, k, v, partial, n_head, n_kv, pos0, pos0_dev,
+                           n_split, scale, counters, out, q8, d8);
+        return TF_LAUNCH_RESULT();
+    }
     if (G <= 4)
         hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 1>), grid, dim3(256),
                            tf_flash_lds_bytes<HD>(1), tf_stream(stream), q, k, v, partial, n_head,
@@ -452,7 +773,8 @@ extern "C" int tf_flash_decode_reduce(const float* partial, float* out, int n_he
                                       int head_dim, int n_split, int n_q, tf_stream_t stream) {
     TF_CHECK_ARG(partial && out && n_head > 0 && head_dim > 0 && n_split >= 1 && n_q == 1);
     TF_CHECK_ARG(head_dim <= 256 && n_split <= 1024);
-    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream), partial, out, nullptr, nullptr, head_dim, n_split);
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head, (head_dim + 31) / 32), dim3(256), 0,
+                       tf_stream(stream), partial, out, nullptr, nullptr, head_dim, n_split);
     return TF_LAUNCH_RESULT();
 }
 
@@ -461,7 +783,8 @@ extern "C" int tf_flash_decode_reduce_q8(const float* partial, float* out, int8_
                                          tf_stream_t stream) {
     TF_CHECK_ARG(partial && out && q8 && d8 && n_head > 0 && n_split >= 1 && n_split <= 1024);
     TF_CHECK_ARG(head_dim > 0 && head_dim <= 256 && (head_dim % 64) == 0);
-    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream),
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head, (head_dim + 31) / 32), dim3(256), 0,
+                       tf_stream(stream),
                        partial, out, q8, d8, head_dim, n_split);
     return TF_LAUNCH_RESULT();
 }
@@ -481,7 +804,8 @@ extern "C" int tf_flash_decode(const float* q, const uint16_t* k_cache, const ui
                                         pos0, pos0_dev, 1, n_split, scale, stream);
     if (rc) return rc;
     TF_CHECK_ARG(head_dim <= 256 && n_split <= 1024);
-    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head), dim3(256), 0, tf_stream(stream),
+    hipLaunchKernelGGL(tf_flash_reduce_kernel, dim3(n_head, (head_dim + 31) / 32), dim3(256), 0,
+                       tf_stream(stream),
                        partial, out, q8, d8, head_dim, n_split);
     return TF_LAUNCH_RESULT();
 }
