@@ -1300,6 +1300,25 @@ __device__ __forceinline__ unsigned long long* tf_p_part(TfPA& a, int kh, int g,
     return a.fpart + ((size_t)(kh * G + g) * TF_P_MAX_SPLIT + s) * (2 + TF_P_HD);
 }
 
+// Long contexts (one head group: all G <= 8 query heads of the kv head in
+// one workgroup, one wave per head) run the tile on the matrix cores, as
+// tf_flash_partial_mfma_kernel: S[16][64] = Q K^T by waves 0-3 (16 tokens
+// each; q split into three f16 parts after a power-of-two scale, K f16),
+// the softmax from DPP row reductions of the MFMA layout plus four per-wave
+// values through LDS, O[16][128] += P V by the eight waves (16 dims each;
+// p split into two f16 parts).  Every lane keeps (m, l) of heads
+// 4g .. 4g+3 (g = lane / 16).  After the tiles, O, m and l of head h go
+// through LDS to wave h, which then publishes them as the vector-ALU path
+// does.
+typedef _Float16 tf_p_h16x4 __attribute__((ext_vector_type(4)));
+typedef float tf_p_f32x4 __attribute__((ext_vector_type(4)));
+#define TF_P_SROW 68  // floats per weight row in LDS (64 tokens + 4)
+
+__device__ __forceinline__ tf_p_f32x4 tf_p_mfma16(tf_p_h16x4 a, tf_p_h16x4 b, tf_p_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+template <bool MM>
 __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo& g, int pos,
                                               TfPAttnRegs& r, uint8_t* lds,
                                               const unsigned long long* fq,
@@ -1330,6 +1349,47 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
             return false;
     }
     tf_p_stamp(a, sk, 1);
+
+    // matrix-core tiles for a single head group with one wave per head
+    const bool mm = MM && g.n_hg == 1 && g.wph == 1;
+    const int l16 = lane & 15, gq = lane >> 4;
+    float* mx_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES);
+    float* sm_lds = mx_lds + 64;  // [4 waves][16 heads] each, in the P area
+    float* pm_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES +
+                                             LA::P_BYTES);  // weights [8][SROW], in the C area
+    tf_p_h16x4 qa[8][3];
+    float msc = 0.f, m4[4], l4[4];
+    tf_p_f32x4 om = tf_p_f32x4{0.f, 0.f, 0.f, 0.f}, oml = om;
+    if (mm) {
+        float qmax = 0.f;
+        const bool hv = l16 < G;
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                qmax = fmaxf(qmax, hv ? fabsf(q_lds[l16 * HD + 16 * st + 4 * gq + i]) : 0.f);
+        qmax = tf_wave_max(qmax);
+        const int e = qmax >= 16384.f ? ilogbf(qmax) - 13 : 0;
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float x = hv ? ldexpf(q_lds[l16 * HD + 16 * st + 4 * gq + i], -e) : 0.f;
+                const _Float16 p0 = (_Float16)x;
+                x -= (float)p0;
+                const _Float16 p1 = (_Float16)x;
+                x -= (float)p1;
+                qa[st][0][i] = p0;
+                qa[st][1][i] = p1;
+                qa[st][2][i] = (_Float16)x;
+            }
+        msc = ldexpf(a.scale, e);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            m4[r] = TF_P_NEG_BIG;
+            l4[r] = 0.f;
+        }
+    }
 
     // this wave: head hd (valid if hh < hpw and hd < G), token slice sl
     const int hh = wave / g.wph, sl = wave % g.wph;
@@ -1362,6 +1422,83 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         if (it + 1 < g.tpw) tf_p_attn_load(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
         __syncthreads();
+        if (mm) {
+            const bool tv = t0 + 16 * wave + l16 < g.t_end;
+            float sv[4];
+            if (wave < 4) {
+                tf_p_f32x4 c0 = tf_p_f32x4{0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
+                const uint16_t* kp = k_lds + (16 * wave + l16) * TF_P_KROW + 4 * gq;
+                tf_p_h16x4 kf[8];
+#pragma unroll
+                for (int st = 0; st < 8; st++)
+                    kf[st] = *reinterpret_cast<const tf_p_h16x4*>(kp + 16 * st);
+#pragma unroll
+                for (int st = 0; st < 8; st++) {
+                    c0 = tf_p_mfma16(qa[st][0], kf[st], c0);
+                    c1 = tf_p_mfma16(qa[st][1], kf[st], c1);
+                    c2 = tf_p_mfma16(qa[st][2], kf[st], c2);
+                }
+                const tf_p_f32x4 c = c0 + (c1 + c2);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sv[r] = tv ? c[r] * msc : TF_P_NEG_BIG;
+                    const float wm = tf_row16_max(sv[r]);  // one head's 16 tokens
+                    if (l16 == 0) mx_lds[wave * 16 + 4 * gq + r] = wm;
+                }
+            }
+            __syncthreads();
+            float alpha[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int h = 4 * gq + r;
+                const float tm = fmaxf(fmaxf(mx_lds[h], mx_lds[16 + h]),
+                                       fmaxf(mx_lds[32 + h], mx_lds[48 + h]));
+                const float m_new = fmaxf(m4[r], tm);
+                alpha[r] = __expf(m4[r] - m_new);
+                if (wave < 4) {
+                    const float pr = tv ? __expf(sv[r] - m_new) : 0.f;
+                    if (h < 8) pm_lds[h * TF_P_SROW + 16 * wave + l16] = pr;
+                    const float ws = tf_row16_sum(pr);
+                    if (l16 == 0) sm_lds[wave * 16 + h] = ws;
+                }
+                m4[r] = m_new;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int h = 4 * gq + r;
+                l4[r] = l4[r] * alpha[r] +
+                        ((sm_lds[h] + sm_lds[16 + h]) + (sm_lds[32 + h] + sm_lds[48 + h]));
+                om[r] *= alpha[r];
+                oml[r] *= alpha[r];
+            }
+            // PV for dims 16 wave .. +15
+            float4 pf[4];
+            uint16_t vf[4][4];
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                pf[ts] = l16 < G ? *reinterpret_cast<const float4*>(pm_lds + l16 * TF_P_SROW + 16 * ts + 4 * gq)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    vf[ts][i] = v_lds[(16 * ts + 4 * gq + i) * HD + 16 * wave + l16];
+            }
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                const float pp[4] = {pf[ts].x, pf[ts].y, pf[ts].z, pf[ts].w};
+                tf_p_h16x4 ahi, alo, bv;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const _Float16 h0 = (_Float16)pp[i];
+                    ahi[i] = h0;
+                    alo[i] = (_Float16)(pp[i] - (float)h0);
+                    bv[i] = __builtin_bit_cast(_Float16, vf[ts][i]);
+                }
+                om = tf_p_mfma16(ahi, bv, om);
+                oml = tf_p_mfma16(alo, bv, oml);
+            }
+            continue;
+        }
         if (!valid || t0 >= g.t_end) continue;
         // ---- scores: lane (ti, ds) sums dims ds DS .. + DS of token sl T + ti
         // in four chains; the WPH dim slices are then added across lanes
@@ -1421,6 +1558,28 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
         o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
+    }
+    if (mm) {
+        __syncthreads();  // the last tile's K/V readers are done: reuse the K area
+        float* ol = reinterpret_cast<float*>(lds);  // [8 heads][HD], then (m, l) [8][2]
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = 4 * gq + r;
+            if (h < G) {
+                ol[h * HD + 16 * wave + l16] = om[r] + oml[r];
+                if (wave == 0 && l16 == 0) {
+                    ol[8 * HD + 2 * h] = m4[r];
+                    ol[8 * HD + 2 * h + 1] = l4[r];
+                }
+            }
+        }
+        __syncthreads();
+        if (valid) {  // wave hd: its head's (m, l, O) in the vector-ALU lane layout
+            m = ol[8 * HD + 2 * hd];
+            l = ol[8 * HD + 2 * hd + 1];
+            o0 = ol[hd * HD + 2 * lane];
+            o1 = ol[hd * HD + 2 * lane + 1];
+        }
     }
     // ---- the WPH slices of a head: log-sum-exp merge, in slice order, by slice 0
     if (g.wph > 1) {
@@ -1619,6 +1778,7 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     return true;
 }
 
+template <bool MM>
 __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
@@ -1629,7 +1789,7 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    const bool ok = tf_p_attn_run(
+    const bool ok = tf_p_attn_run<MM>(
         a, L, g, pos, ra, lds, tf_p_vec(a, TF_PK_Q, li), tf_p_vec(a, TF_PK_KV, li),
         tf_p_tag(tb, li, TF_PK_Q), tf_p_tag(tb, li, TF_PK_KV), tf_p_vec(a, TF_PK_O, li),
         tf_p_tag(tb, li, TF_PK_O), tf_p_tag(tb, li, TF_PK_PART), 5 * li + 1);
@@ -1840,7 +2000,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
 
 // ------------------------------------------------------------ the kernel
 
-template <int SPR_E, int IT_E, int SPR_F, int IT_F>
+template <int SPR_E, int IT_E, int SPR_F, int IT_F, bool MM>
 __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     const TfPArgs* args, int host_mode, int token_host, int pos_host) {
     {
@@ -1866,7 +2026,7 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     __syncthreads();
     for (int li = 0; li < a.n_layer; li++) {
         if (!tf_p_stage_qkv<SPR_E, IT_E>(&a, li, tb, pos, token)) return;
-        if (!tf_p_stage_attn(&a, li, tb, pos)) return;
+        if (!tf_p_stage_attn<MM>(&a, li, tb, pos)) return;
         if (!tf_p_stage_wo<SPR_E, IT_E>(&a, li, tb, token)) return;
         if (!tf_p_stage_gu<SPR_E, IT_E>(&a, li, tb)) return;
         if (!tf_p_stage_down<SPR_F, IT_F>(&a, li, tb)) return;
@@ -1893,10 +2053,10 @@ struct TfPLaunch {
     int host_mode, token, pos;
 };
 
-template <int SE, int IE, int SF, int IF>
+template <int SE, int IE, int SF, int IF, bool MM>
 int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid_out,
                   int* lds_out) {
-    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF>;
+    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, MM>;
     const int lds = tf_p_lds(a);
     static int attr_done[64];
     int dev = 0;
@@ -1937,11 +2097,13 @@ int tf_p_dispatch(int E, int F_, int H, int KV, int HD, F&& f) {
     return -1;
 }
 
-template <int V>
+// MM: the instantiation whose attention runs long contexts on the matrix
+// cores (its extra registers would cost the short-context step ~2%).
+template <int V, bool MM>
 int tf_p_call(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid, int* lds) {
-    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1>(a, l, s, grid, lds);
-    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3>(a, l, s, grid, lds);
-    else return tf_p_launch_t<16, 1, 16, 5>(a, l, s, grid, lds);
+    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1, MM>(a, l, s, grid, lds);
+    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3, MM>(a, l, s, grid, lds);
+    else return tf_p_launch_t<16, 1, 16, 5, MM>(a, l, s, grid, lds);
 }
 
 }  // namespace
@@ -1952,20 +2114,30 @@ bool tf_decode_persistent_supported(int n_layer, int E, int F, int H, int KV, in
     return tf_p_dispatch(E, F, H, KV, HD, [](auto) { return 0; }) == 0;
 }
 
+bool tf_decode_persistent_long_ctx(const TfPArgs& a, int grid, int pos) {
+    // tf_p_attn_geo: one head group with one wave per head
+    const int G = a.H / a.KV;
+    const int n_tiles = (pos + 1 + TF_P_TILE - 1) / TF_P_TILE;
+    if (G >= 4 && a.KV * n_tiles * 4 <= grid) return false;
+    if (G >= 2 && a.KV * n_tiles * 2 <= grid) return false;
+    return G > 4;
+}
+
 int tf_decode_persistent_grid(const TfPArgs& a, int* lds_bytes) {
     int grid = 0;
     const int rc = tf_p_dispatch(a.E, a.F, a.H, a.KV, a.HD, [&](auto v) {
-        return tf_p_call<decltype(v)::value>(a, nullptr, nullptr, &grid, lds_bytes);
+        return tf_p_call<decltype(v)::value, false>(a, nullptr, nullptr, &grid, lds_bytes);
     });
     return rc == 0 ? grid : 0;
 }
 
 int tf_decode_persistent_launch(const TfPArgs& a, const TfPArgs* dev, int host_mode, int token,
-                                int pos, hipStream_t stream) {
+                                int pos, hipStream_t stream, bool long_ctx) {
     if (!dev) return (int)hipErrorInvalidValue;
     const TfPLaunch l{dev, host_mode, token, pos};
     const int rc = tf_p_dispatch(a.E, a.F, a.H, a.KV, a.HD, [&](auto v) {
-        return tf_p_call<decltype(v)::value>(a, &l, stream, nullptr, nullptr);
+        return long_ctx ? tf_p_call<decltype(v)::value, true>(a, &l, stream, nullptr, nullptr)
+                        : tf_p_call<decltype(v)::value, false>(a, &l, stream, nullptr, nullptr);
     });
     return rc < 0 ? (int)hipErrorInvalidValue : rc;
 }

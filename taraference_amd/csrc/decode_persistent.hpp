@@ -80,5 +80,12 @@ int tf_decode_persistent_grid(const TfPArgs& a, int* lds_bytes);
 // Enqueue one decode step on `stream`.  `dev` is a device copy of `a` (the
 // kernel reads its tables from there); host_mode != 0 decodes `token` at
 // `pos`, otherwise the device state is used and advanced.
+// long_ctx selects the instantiation that runs long-context attention on
+// the matrix cores (valid at every position; tf_decode_persistent_long_ctx
+// says where it pays).
 int tf_decode_persistent_launch(const TfPArgs& a, const TfPArgs* dev, int host_mode, int token,
-                                int pos, hipStream_t stream);
+                                int pos, hipStream_t stream, bool long_ctx);
+// True when the attention of a step at `pos` runs as one head group with
+// one wave per query head on a `grid`-workgroup launch (the regime of the
+// matrix-core tiles).
+bool tf_decode_persistent_long_ctx(const TfPArgs& a, int grid, int pos);

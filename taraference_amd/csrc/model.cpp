@@ -490,9 +490,21 @@ struct tf_model {
         a.log = d_log;
     }
 
+    // the long-context instantiation of the persistent step (graph runs:
+    // chosen in run() for the last position of the run)
+    bool p_long = false;
+
+    bool long_ctx(int pos) {
+        ensure_persistent();
+        const int grid = tf_decode_persistent_grid(pargs, nullptr);
+        return tf_decode_persistent_long_ctx(pargs, grid, pos);
+    }
+
     void step_persistent(hipStream_t s, int token, int pos, bool device_state) {
         ensure_persistent();
-        tf::check(tf_decode_persistent_launch(pargs, d_pargs, device_state ? 0 : 1, token, pos, s),
+        const bool lc = device_state ? p_long : long_ctx(pos);
+        tf::check(tf_decode_persistent_launch(pargs, d_pargs, device_state ? 0 : 1, token, pos, s,
+                                              lc),
                   "persistent step");
     }
 
@@ -500,6 +512,13 @@ struct tf_model {
         if (path == 0) step(s, token, pos, device_state);
         else if (path == 4) step_persistent(s, token, pos, device_state);
         else step_fused(s, token, pos, device_state, path >= 2, path == 3);
+    }
+
+    void drop_graph() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        graph_exec = nullptr;
+        graph = nullptr;
     }
 
     void capture() {
@@ -539,6 +558,11 @@ struct tf_model {
         if (path == 4) {
             ensure_persistent();
             reset_persistent(s);
+            const bool lc = long_ctx(pos0 + total - 1);
+            if (lc != p_long) {  // the captured step launches the other instantiation
+                p_long = lc;
+                drop_graph();
+            }
         }
         if (use_graph) capture();
         for (int i = 0; i < total; i++) {
