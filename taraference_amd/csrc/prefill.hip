@@ -26,8 +26,8 @@
 // Per 256-value super-block the workgroup stages x in LDS already split into
 // its three bf16 planes (once per workgroup, with the per-group sums of x)
 // and the per-sub-block scales of its columns; each wave reads its own
-// columns' quant bytes straight from global memory, issued before the
-// staging barrier.  Consecutive workgroups share columns (token tiles are
+// columns' quant bytes straight from global memory.  All global loads of
+// super-block sb + 1 are issued before the MFMAs of super-block sb.  Consecutive workgroups share columns (token tiles are
 // the fast grid dimension), so a column's bytes are re-read from L2.
 //
 // MFMA operand layouts (lane l, g = l / 16), A rows = output columns,
@@ -156,6 +156,22 @@ __device__ __forceinline__ tf_f32x4 tf_mfma16(tf_bf16x4 a, tf_bf16x4 b, tf_f32x4
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+#ifdef TF_GEMM_STAMPS
+__device__ unsigned long long tf_gemm_stamps[256];
+#define TF_GSTAMP(k)                                                                    \
+    do {                                                                               \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && (k) < 256)       \
+            tf_gemm_stamps[(k)] = __builtin_amdgcn_s_memrealtime();                    \
+    } while (0)
+extern "C" int tf_gemm_debug_stamps(unsigned long long* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tf_gemm_stamps), sizeof(tf_gemm_stamps));
+}
+#else
+#define TF_GSTAMP(k) \
+    do {             \
+    } while (0)
+#endif
+
 // LDS image of x for one super-block: 3 bf16 planes x 32 tokens x 256
 // values, rows of TF_PF_ROW bytes (16 bytes of padding: the 16 rows a
 // fragment read touches start on distinct banks).
@@ -190,53 +206,96 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
     for (int ct = 0; ct < 2; ct++)
         for (int tt = 0; tt < 2; tt++) acc[ct][tt] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // Software pipeline over super-blocks: the global loads of super-block
+    // sb + 1 (this lane's quant bytes, this thread's x values, the scale
+    // header of one column) are issued before the MFMAs of super-block sb,
+    // and written to LDS after them.
+    const int xt = tid >> 3, xs = tid & 7;  // staging: token xt, 32-value group xs
+    const bool xlive = t0 + xt < n_tok;
+    const float* xrow = x + (size_t)(xlive ? t0 + xt : 0) * n_rows + 32 * xs;
+    const int hc = c0 + tid < n_cols ? c0 + tid : n_cols - 1;  // header column (tid < 128)
+    const uint8_t* hcol = w + (size_t)hc * col_bytes;
+    auto load_x = [&](int sb, float4 (&xr)[8]) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) xr[k] = *reinterpret_cast<const float4*>(xrow + sb * 256 + 4 * k);
+    };
+    // Q4_K header: d | dmin, 12 scale bytes (4-byte aligned 144-byte blocks);
+    // Q6_K: 16 int8 scales and d (2-byte aligned raw blocks)
+    auto load_hdr = [&](int sb, uint32_t (&hd)[5]) {
+        const uint8_t* blk = hcol + (size_t)sb * BLK;
+        if (tid >= TF_PF_COLS) return;
+        if constexpr (!Q6) {
+            const tf_u32x4 v = tf_ld16_a4(blk);
+            hd[0] = v.x;
+            hd[1] = v.y;
+            hd[2] = v.z;
+            hd[3] = v.w;
+            hd[4] = 0;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) hd[i] = tf_pf_u16x2(blk + 192 + 4 * i);
+            hd[4] = tf_gld(reinterpret_cast<const uint16_t*>(blk + 208));
+        }
+    };
+    auto store_x = [&](const float4 (&xr)[8]) {
+        float gs = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 v = xlive ? xr[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+            gs += (v.x + v.y) + (v.z + v.w);
+            const TfSplit3 sp = tf_split3(v);
+#pragma unroll
+            for (int pl = 0; pl < 3; pl++)
+                *reinterpret_cast<tf_bf16x4*>(xp + (pl * TF_PF_TOKS + xt) * TF_PF_ROW +
+                                              2 * (32 * xs + 4 * k)) = sp.p[pl];
+        }
+        if constexpr (!Q6) xsum[xt * 8 + xs] = gs;
+    };
+    auto store_hdr = [&](const uint32_t (&hd)[5]) {
+        if (tid >= TF_PF_COLS) return;
+        if constexpr (!Q6) {
+            const float d = tf_h2f(hd[0]), dmin = tf_h2f(hd[0] >> 16);
+            uint8_t s12[12];
+#pragma unroll
+            for (int i = 0; i < 12; i++) s12[i] = (uint8_t)(hd[1 + i / 4] >> (8 * (i % 4)));
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                int sc, m;
+                tf_pf_scale_min(s12, s, sc, m);
+                scl[s * TF_PF_COLS + tid] = d * (float)sc;
+                mnl[s * TF_PF_COLS + tid] = dmin * (float)m;
+            }
+        } else {
+            const float d = tf_h2f(hd[4]);
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+                scl[s * TF_PF_COLS + tid] = d * (float)(int8_t)(hd[s / 4] >> (8 * (s % 4)));
+        }
+    };
+
+    TfPfCol<Q6> wc[2], wn[2];
+    float4 xr[8];
+    uint32_t hd[5];
+    for (int ct = 0; ct < 2; ct++)
+        tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes, g, wc[ct]);
+    load_x(0, xr);
+    load_hdr(0, hd);
+    TF_GSTAMP(0);
     for (int sb = 0; sb < nb; sb++) {
-        TfPfCol<Q6> wc[2];
-        for (int ct = 0; ct < 2; ct++)
-            tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)sb * BLK, g, wc[ct]);
+        TF_GSTAMP(1 + 4 * sb);
         __syncthreads();  // the previous super-block's LDS reads are done
-        {
-            // thread (token t, group s of 32 values): split into the three
-            // bf16 planes once for the whole workgroup, and sum the group
-            const int t = tid >> 3, s = tid & 7;
-            const bool live = t0 + t < n_tok;
-            const float* src = x + (size_t)(live ? t0 + t : 0) * n_rows + sb * 256 + 32 * s;
-            float gs = 0.f;
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                float4 v = *reinterpret_cast<const float4*>(src + 4 * k);
-                if (!live) v = make_float4(0.f, 0.f, 0.f, 0.f);
-                gs += (v.x + v.y) + (v.z + v.w);
-                const TfSplit3 sp = tf_split3(v);
-#pragma unroll
-                for (int pl = 0; pl < 3; pl++)
-                    *reinterpret_cast<tf_bf16x4*>(xp + (pl * TF_PF_TOKS + t) * TF_PF_ROW +
-                                                  2 * (32 * s + 4 * k)) = sp.p[pl];
-            }
-            if constexpr (!Q6) xsum[t * 8 + s] = gs;
-        }
-        // scales of the workgroup's columns
-        if (tid < TF_PF_COLS) {
-            const int c = c0 + tid < n_cols ? c0 + tid : n_cols - 1;
-            const uint8_t* blk = w + (size_t)c * col_bytes + (size_t)sb * BLK;
-            if constexpr (!Q6) {
-                const float d = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk)));
-                const float dmin = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk + 2)));
-                uint8_t s12[12];
-                for (int i = 0; i < 12; i++) s12[i] = blk[4 + i];
-                for (int s = 0; s < 8; s++) {
-                    int sc, m;
-                    tf_pf_scale_min(s12, s, sc, m);
-                    scl[s * TF_PF_COLS + tid] = d * (float)sc;
-                    mnl[s * TF_PF_COLS + tid] = dmin * (float)m;
-                }
-            } else {
-                const float d = tf_h2f(tf_gld(reinterpret_cast<const uint16_t*>(blk + 208)));
-                for (int s = 0; s < 16; s++)
-                    scl[s * TF_PF_COLS + tid] = d * (float)(int8_t)blk[192 + s];
-            }
-        }
+        TF_GSTAMP(2 + 4 * sb);
+        store_x(xr);
+        store_hdr(hd);
         __syncthreads();
+        TF_GSTAMP(3 + 4 * sb);
+        if (sb + 1 < nb) {  // workgroup-uniform
+            for (int ct = 0; ct < 2; ct++)
+                tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)(sb + 1) * BLK, g,
+                                   wn[ct]);
+            load_x(sb + 1, xr);
+            load_hdr(sb + 1, hd);
+        }
         for (int s = 0; s < NSUB; s++) {
             tf_f32x4 part[2][2];
             if constexpr (!Q6) {
@@ -288,7 +347,9 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
                 }
             }
         }
+        for (int ct = 0; ct < 2; ct++) wc[ct] = wn[ct];
     }
+    TF_GSTAMP(4 * nb + 1);
     // C rows 4g..4g+3 -> columns, C column l16 -> token
     for (int ct = 0; ct < 2; ct++) {
         const int cb = c0 + 32 * wave + 16 * ct + 4 * g;
