@@ -333,9 +333,10 @@ int tf_flash_decode_n_split(int n_kv, int max_seq);
 
 /* ------------------------------------------------------- decode-step glue */
 
-/* kernels/embed.cu:51-131 embed_q{4,6}_k_one[_d]: dequantize row `token`
- * (or *token_dev when token_dev != NULL) of a Q4_K (block_bytes 144) or raw
- * Q6_K (210) table into out[n_rows]. */
+/* kernels/embed.cu:51-131 embed_q{4,6}_k_one[_d] and embed_q{5,8}_0_one[_d]:
+ * dequantize row `token` (or *token_dev when token_dev != NULL) of a Q4_K
+ * (block_bytes 144), raw Q6_K (210), Q8_0 (34) or Q5_0 (22) table into
+ * out[n_rows]. */
 int tf_embed_row(const uint8_t *table, int block_bytes, float *out, int token,
                  const int *token_dev, int n_rows, int col_bytes,
                  tf_stream_t stream);
@@ -436,6 +437,8 @@ int tf_argmax_key_finalize(unsigned long long *amax_key, int *out_idx,
 
 #define TF_TYPE_Q4_K 12 /* GGML type ids */
 #define TF_TYPE_Q6_K 14
+#define TF_TYPE_Q5_0 6  /* K = 896 tensors of Qwen2.5-0.5B files (path 0 only) */
+#define TF_TYPE_Q8_0 8
 
 /* cuda/types.rs:212-225 GpuMat: data = GGUF bytes; compact = 212-byte Q6_K
  * repack (NULL for Q4_K). */

@@ -18,14 +18,11 @@ template <int BLOCK_BYTES>
 __global__ __launch_bounds__(256) void tf_embed_kernel(const uint8_t* __restrict__ table,
                                                        float* __restrict__ out, int token,
                                                        const int* __restrict__ token_dev,
-                                                       int n_rows, int col_bytes) {
+                                                       int n, int col_bytes) {
     if (token_dev) token = token_dev[0];
     const uint8_t* col = table + (size_t)token * col_bytes;
-    const int nb = n_rows / 256;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nb * 256; i += gridDim.x * blockDim.x) {
-        const uint8_t* blk = col + (size_t)(i >> 8) * BLOCK_BYTES;
-        out[i] = BLOCK_BYTES == 144 ? tf_q4k_value(blk, i & 255) : tf_q6k_value(blk, i & 255);
-    }
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = tf_row_value<BLOCK_BYTES>(col, i);
 }
 
 // ------------------------------------------------------------ RMSNorm
@@ -207,16 +204,26 @@ __global__ __launch_bounds__(1024) void tf_argmax_kernel(const float* __restrict
 extern "C" int tf_embed_row(const uint8_t* table, int block_bytes, float* out, int token,
                             const int* token_dev, int n_rows, int col_bytes,
                             tf_stream_t stream) {
-    const int nb = n_rows / 256;
+    // 256-value K-quant blocks cover floor(n_rows / 256) * 256 values (as
+    // the reference); 32-value blocks cover n_rows (a multiple of 32)
+    const bool k256 = block_bytes == 144 || block_bytes == 210;
+    TF_CHECK_ARG(k256 || block_bytes == 34 || block_bytes == 22);
+    const int per = k256 ? 256 : 32;
+    const int nb = n_rows / per;
     TF_CHECK_ARG(table && out && nb > 0 && (token_dev || token >= 0));
-    TF_CHECK_ARG((block_bytes == 144 || block_bytes == 210) && col_bytes >= nb * block_bytes);
-    const int blocks = (nb * 256 + 255) / 256;
-    if (block_bytes == 144)
-        hipLaunchKernelGGL(tf_embed_kernel<144>, dim3(blocks), dim3(256), 0, tf_stream(stream),
-                           table, out, token, token_dev, n_rows, col_bytes);
-    else
-        hipLaunchKernelGGL(tf_embed_kernel<210>, dim3(blocks), dim3(256), 0, tf_stream(stream),
-                           table, out, token, token_dev, n_rows, col_bytes);
+    TF_CHECK_ARG(col_bytes >= nb * block_bytes);
+    const int n = nb * per;
+    const dim3 grid((n + 255) / 256);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, tf_stream(stream), table, out, token,
+                           token_dev, n, col_bytes);
+    };
+    switch (block_bytes) {
+    case 144: go(tf_embed_kernel<144>); break;
+    case 210: go(tf_embed_kernel<210>); break;
+    case 34: go(tf_embed_kernel<34>); break;
+    default: go(tf_embed_kernel<22>); break;
+    }
     return TF_LAUNCH_RESULT();
 }
 

@@ -44,3 +44,30 @@ __device__ __forceinline__ float tf_q6k_value(const uint8_t* blk_, int v) {
     const int8_t sc = (int8_t)blk[192 + (v >> 4)];
     return d * (float)sc * (float)q;
 }
+
+// Q8_0 (34-byte blocks of 32): d * qs[v]; Q5_0 (22-byte blocks of 32):
+// d * (code - 16) (kernels/embed.cu embed_q8_0 / embed_q5_0).  Value v of
+// the block at blk.
+__device__ __forceinline__ float tf_q8_0_value(const uint8_t* blk_, int v) {
+    const TF_GAS uint8_t* blk = (const TF_GAS uint8_t*)blk_;
+    return tf_h2f(blk[0] | (blk[1] << 8)) * (float)(int8_t)blk[2 + v];
+}
+
+__device__ __forceinline__ float tf_q5_0_value(const uint8_t* blk_, int v) {
+    const TF_GAS uint8_t* blk = (const TF_GAS uint8_t*)blk_;
+    const uint32_t qh = blk[2] | (blk[3] << 8) | (blk[4] << 16) | ((uint32_t)blk[5] << 24);
+    const int t = v & 15;
+    const int nib = v < 16 ? (blk[6 + t] & 0xF) : (blk[6 + t] >> 4);
+    const int code = nib | (int)(((qh >> v) & 1u) << 4);
+    return tf_h2f(blk[0] | (blk[1] << 8)) * (float)(code - 16);
+}
+
+// Value i of a row stored in blocks of block_bytes (144 / 210: 256 values,
+// 34 / 22: 32 values).
+template <int BB>
+__device__ __forceinline__ float tf_row_value(const uint8_t* row, int i) {
+    if constexpr (BB == 144) return tf_q4k_value(row + (size_t)(i >> 8) * 144, i & 255);
+    else if constexpr (BB == 210) return tf_q6k_value(row + (size_t)(i >> 8) * 210, i & 255);
+    else if constexpr (BB == 34) return tf_q8_0_value(row + (size_t)(i >> 5) * 34, i & 31);
+    else return tf_q5_0_value(row + (size_t)(i >> 5) * 22, i & 31);
+}

@@ -46,7 +46,10 @@ GpuMat to_mat(const tf_mat& m) {
     g.n_cols = (size_t)m.n_cols;
     g.col_bytes = (size_t)m.col_bytes;
     g.compact_col_bytes = (size_t)m.compact_col_bytes;
-    g.wtype = m.type == TF_TYPE_Q6_K ? tf::WType::Q6K : tf::WType::Q4K;
+    g.wtype = m.type == TF_TYPE_Q6_K   ? tf::WType::Q6K
+              : m.type == TF_TYPE_Q5_0 ? tf::WType::Q5_0
+              : m.type == TF_TYPE_Q8_0 ? tf::WType::Q8_0
+                                       : tf::WType::Q4K;
     return g;
 }
 
@@ -93,6 +96,7 @@ struct tf_model {
 
     // workspace (cuda/load.rs:502-607)
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr;
+    float* hb2 = nullptr;  // up projection when gate/up are not fused
     float *logits = nullptr, *flash_partial = nullptr, *gemv_partial = nullptr;
     int8_t* q8_x = nullptr;
     float* q8_d = nullptr;
@@ -164,7 +168,8 @@ struct tf_model {
             // ---- attention block
             tf::check(tf_rms_norm(x, L.attn_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
             if (!tf::try_gemv_qkv(s, L.wq, L.wk, L.wv, xb, q, k, v, L.bq, L.bk, L.bv, q8_x, q8_d)) {
-                if (tf::try_gemv_pair(s, L.wq, L.wk, xb, q, k, L.bq, L.bk, q8_x, q8_d)) {
+                if (tf::try_gemv_pair(s, L.wq, L.wk, xb, q, k, L.bq, L.bk, q8_x, q8_d) ||
+                    tf::try_gemv_q5_dual(s, L.wq, L.wk, xb, q, k, L.bq, L.bk)) {
                     tf::gemv(s, L.wv, xb, v, L.bv, GemvResidual::none(), gemv_partial,
                              partial_stride);
                 } else {
@@ -184,8 +189,18 @@ struct tf_model {
                          partial_stride);
             // ---- FFN block
             tf::check(tf_rms_norm(x, L.ffn_norm, xb, c.n_embd, c.rms_eps, s), "rms_norm");
-            if (!tf::try_gemv_q4_ffn(s, L.gate, L.up, xb, hb, q8_x, q8_d))
-                throw tf::HipError(1, "ffn gate/up must be Q4_K");
+            if (!tf::try_gemv_q4_ffn(s, L.gate, L.up, xb, hb, q8_x, q8_d)) {
+                // layer.rs:1267-1390: gate and up (one dual launch when both
+                // are Q5_0), then silu_mul
+                if (!tf::try_gemv_q5_dual(s, L.gate, L.up, xb, hb, hb2, nullptr, nullptr)) {
+                    tf::gemv(s, L.gate, xb, hb, nullptr, GemvResidual::none(), gemv_partial,
+                             partial_stride);
+                    tf::gemv(s, L.up, xb, hb2, nullptr, GemvResidual::none(), gemv_partial,
+                             partial_stride);
+                }
+                tf::check(tf_pf_silu_mul(hb, hb2, c.n_ff, reinterpret_cast<tf_stream_t>(s)),
+                          "silu_mul");
+            }
             if (!tf::try_gemv_global_q8(s, L.down, hb, x, nullptr, GemvResidual::in_place(), q8_x,
                                         q8_d, gemv_partial, partial_stride))
                 tf::gemv(s, L.down, hb, x, nullptr, GemvResidual::in_place(), gemv_partial,
@@ -354,7 +369,25 @@ struct tf_model {
     // Whether path 4 can serve this model: Q4_K q/k/wo/gate/up, Q6_K or
     // Q4_K v and down (Q6_K down and the lm_head with their compact copy), and
     // a shape the persistent kernel is instantiated for.
+    // Paths 1-4 are written for the Q4_K_M K-quant placement: every matrix
+    // Q4_K or Q6_K, widths multiples of 256.  Other models (Q5_0 / Q8_0
+    // tensors, e.g. the 896-wide Qwen2.5-0.5B) run the reference sequence.
+    bool kquant_ok() const {
+        const tf_model_config& c = cfg;
+        if (c.n_embd % 256 || c.n_ff % 256) return false;
+        auto kq = [](const GpuMat& w) {
+            return w.wtype == tf::WType::Q4K || w.wtype == tf::WType::Q6K;
+        };
+        if (!kq(token_embd) || !kq(output)) return false;
+        for (const Layer& L : layers)
+            if (!kq(L.wq) || !kq(L.wk) || !kq(L.wv) || !kq(L.wo) || !kq(L.gate) || !kq(L.up) ||
+                !kq(L.down))
+                return false;
+        return true;
+    }
+
     bool persistent_ok() const {
+        if (!kquant_ok()) return false;
         const tf_model_config& c = cfg;
         if (!tf_decode_persistent_supported(c.n_layer, c.n_embd, c.n_ff, c.n_head, c.n_kv,
                                             c.head_dim))
@@ -580,10 +613,6 @@ struct tf_model {
     // Prompt chunk size of the prefill (types.rs MAX_BATCH).
     static constexpr int kPrefillChunk = 256;
 
-    static bool gemm_ok(const GpuMat& w) {
-        return w.wtype == tf::WType::Q4K || w.wtype == tf::WType::Q6K;
-    }
-
     // x[t] (+)= W xin[t] for n rows on the matrix cores (raw GGUF bytes).
     static void gemm(hipStream_t s, const GpuMat& w, const float* xin, float* out, int n,
                      bool accumulate) {
@@ -604,10 +633,8 @@ struct tf_model {
         const tf_model_config& c = cfg;
         if (n < 1 || pos0 < 0 || pos0 + n > c.max_seq)
             throw tf::HipError((int)hipErrorInvalidValue, "prefill range outside the KV cache");
-        for (const Layer& L : layers)
-            if (!gemm_ok(L.wq) || !gemm_ok(L.wk) || !gemm_ok(L.wv) || !gemm_ok(L.wo) ||
-                !gemm_ok(L.gate) || !gemm_ok(L.up) || !gemm_ok(L.down))
-                throw tf::HipError((int)hipErrorNotSupported, "prefill needs Q4_K/Q6_K weights");
+        if (!kquant_ok())
+            throw tf::HipError((int)hipErrorNotSupported, "prefill needs Q4_K/Q6_K weights");
         const int CH = kPrefillChunk, E = c.n_embd, F = c.n_ff;
         const int kvd = c.n_kv * c.head_dim;
         if (!pf_x) {
@@ -690,7 +717,7 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
                                const float* output_norm, tf_model** out) {
     if (!cfg || !layers || !token_embd || !output || !output_norm || !out) return (int)hipErrorInvalidValue;
     const tf_model_config& c = *cfg;
-    if (c.n_layer <= 0 || c.n_embd % 256 || c.n_ff % 256 || c.n_head <= 0 || c.n_kv <= 0 ||
+    if (c.n_layer <= 0 || c.n_embd % 32 || c.n_ff % 32 || c.n_head <= 0 || c.n_kv <= 0 ||
         c.n_head % c.n_kv || c.n_head * c.head_dim != c.n_embd || c.max_seq <= 0 || c.n_vocab <= 0)
         return (int)hipErrorInvalidValue;
     try {
@@ -714,7 +741,10 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
             m->layers.push_back(l);
         }
         m->token_embd = to_mat(*token_embd);
-        m->embd_block_bytes = token_embd->type == TF_TYPE_Q6_K ? 210 : 144;
+        m->embd_block_bytes = token_embd->type == TF_TYPE_Q6_K   ? 210
+                              : token_embd->type == TF_TYPE_Q8_0 ? 34
+                              : token_embd->type == TF_TYPE_Q5_0 ? 22
+                                                                 : 144;
         m->output = to_mat(*output);
         m->output_norm = output_norm;
         const int n_split = tf_flash_decode_n_split(c.n_kv, c.max_seq);
@@ -726,6 +756,7 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->k = m->alloc<float>(c.n_kv * c.head_dim);
         m->v = m->alloc<float>(c.n_kv * c.head_dim);
         m->hb = m->alloc<float>(c.n_ff);
+        m->hb2 = m->alloc<float>(c.n_ff);
         m->logits = m->alloc<float>(c.n_vocab);
         m->q8_x = m->alloc<int8_t>(std::max(c.n_ff, c.n_embd));
         m->q8_d = m->alloc<float>(std::max(c.n_ff, c.n_embd) / 32);
@@ -751,7 +782,7 @@ extern "C" int tf_model_create(const tf_model_config* cfg, const tf_layer* layer
         m->d_log = m->alloc<int>(c.max_seq);
         // the persistent step where the kernel serves this model, else the
         // fused multi-launch step
-        m->path = m->persistent_ok() ? 4 : 3;
+        m->path = m->persistent_ok() ? 4 : (m->kquant_ok() ? 3 : 0);
         *out = m.release();
         return 0;
     } catch (const tf::HipError& e) {
@@ -821,6 +852,7 @@ extern "C" int tf_model_get_path(const tf_model* m) { return m ? m->path : -1; }
 extern "C" int tf_model_set_path(tf_model* m, int path) {
     if (!m || path < 0 || path > 4) return (int)hipErrorInvalidValue;
     if (path == 4 && !m->persistent_ok()) return (int)hipErrorNotSupported;
+    if (path >= 1 && !m->kquant_ok()) return (int)hipErrorNotSupported;
     if (m->path != path) {
         m->path = path;
         if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);

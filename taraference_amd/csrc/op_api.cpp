@@ -28,7 +28,15 @@ uint32_t gemv_n_split(size_t n_rows) {
 void gemv(hipStream_t s, const GpuMat& w, const float* x, float* y, const float* bias,
           GemvResidual res, float* /*partial*/, size_t /*partial_stride*/) {
     const int use_bias = bias ? 1 : 0;
-    if (w.wtype == WType::Q6K) {
+    if (w.wtype == WType::Q5_0) {
+        check(tf_gemv_q5_0_f32(w.data, x, y, I(w.n_rows), I(w.n_cols), I(w.col_bytes), use_bias,
+                               bias, res.use_res(), res.add, S(s)),
+              "gemv_q5_0");
+    } else if (w.wtype == WType::Q8_0) {  // x quantized per workgroup (gemv_q8_0)
+        check(tf_gemv_q8_0_f32(w.data, x, y, I(w.n_rows), I(w.n_cols), I(w.col_bytes), use_bias,
+                               bias, res.use_res(), res.add, S(s)),
+              "gemv_q8_0");
+    } else if (w.wtype == WType::Q6K) {
         check(tf_gemv_q6k_f32(w.data, x, y, I(w.n_rows), I(w.n_cols), I(w.col_bytes), use_bias,
                               bias, res.use_res(), res.add, S(s)),
               "gemv_q6_k");
@@ -43,8 +51,15 @@ bool try_gemv_global_q8(hipStream_t s, const GpuMat& w, const float* x, float* y
                         const float* bias, GemvResidual res, int8_t* q8_x, float* q8_d,
                         float* /*partial*/, size_t /*partial_stride*/) {
     if (w.wtype == WType::Q6K && !w.compact_data) return false;
+    if (w.wtype == WType::Q5_0) return false;  // no global-Q8 Q5_0 kernel (matmul.rs:160-176)
     const int use_bias = bias ? 1 : 0;
     quantize_q8(s, x, q8_x, q8_d, I(w.n_rows));
+    if (w.wtype == WType::Q8_0) {
+        check(tf_gemv_q8_0_q8(w.data, q8_x, q8_d, y, I(w.n_rows), I(w.n_cols), I(w.col_bytes),
+                              use_bias, bias, res.use_res(), res.add, S(s)),
+              "gemv_q8_0_global");
+        return true;
+    }
     if (w.wtype == WType::Q4K) {
         check(tf_gemv_q4k_q8(w.data, q8_x, q8_d, y, I(w.n_rows), I(w.n_cols), I(w.col_bytes),
                              use_bias, bias, res.use_res(), res.add, S(s)),
@@ -95,6 +110,19 @@ bool try_gemv_q4_dual(hipStream_t s, const GpuMat& wa, const GpuMat& wb, const f
     return true;
 }
 
+bool try_gemv_q5_dual(hipStream_t s, const GpuMat& wa, const GpuMat& wb, const float* x,
+                      float* out_a, float* out_b, const float* ba, const float* bb) {
+    if (wa.wtype != WType::Q5_0 || wb.wtype != WType::Q5_0 || wa.n_rows != wb.n_rows ||
+        wa.col_bytes != wb.col_bytes)
+        return false;
+    const bool both = ba && bb, none = !ba && !bb;
+    if (!both && !none) return false;
+    check(tf_gemv_q5_0_qk(wa.data, wb.data, x, out_a, out_b, I(wa.n_rows), I(wa.n_cols),
+                          I(wb.n_cols), I(wa.col_bytes), both ? 1 : 0, ba, bb, S(s)),
+          "gemv_q5_0_qk");
+    return true;
+}
+
 bool try_gemv_q4_ffn(hipStream_t s, const GpuMat& gate, const GpuMat& up, const float* x,
                      float* out, int8_t* q8_x, float* q8_d) {
     if (gate.wtype != WType::Q4K || up.wtype != WType::Q4K || gate.n_rows != up.n_rows ||
@@ -115,8 +143,24 @@ bool try_gemv_qkv(hipStream_t s, const GpuMat& wq, const GpuMat& wk, const GpuMa
     const bool same = wq.n_rows == wk.n_rows && wq.n_rows == wv.n_rows &&
                       wq.col_bytes == wk.col_bytes && wq.col_bytes == wv.col_bytes;
     const bool all = bq && bk && bv, none = !bq && !bk && !bv;
-    if (wq.wtype != WType::Q4K || wk.wtype != WType::Q4K || wv.wtype != WType::Q4K || !same ||
-        !(all || none))
+    if (!same || !(all || none)) return false;
+    // matmul.rs:1003-1130: all three Q8_0 (x quantized in the kernel), or all
+    // three Q5_0 (f32 x)
+    if (wq.wtype == WType::Q8_0 && wk.wtype == WType::Q8_0 && wv.wtype == WType::Q8_0) {
+        check(tf_gemv_q8_0_qkv(wq.data, wk.data, wv.data, x, q, k, v, I(wq.n_rows), I(wq.n_cols),
+                               I(wk.n_cols), I(wv.n_cols), I(wq.col_bytes), all ? 1 : 0, bq, bk,
+                               bv, S(s)),
+              "gemv_q8_0_qkv");
+        return true;
+    }
+    if (wq.wtype == WType::Q5_0 && wk.wtype == WType::Q5_0 && wv.wtype == WType::Q5_0) {
+        check(tf_gemv_q5_0_qkv(wq.data, wk.data, wv.data, x, q, k, v, I(wq.n_rows), I(wq.n_cols),
+                               I(wk.n_cols), I(wv.n_cols), I(wq.col_bytes), all ? 1 : 0, bq, bk,
+                               bv, S(s)),
+              "gemv_q5_0_qkv");
+        return true;
+    }
+    if (wq.wtype != WType::Q4K || wk.wtype != WType::Q4K || wv.wtype != WType::Q4K)
         return false;
     quantize_q8(s, x, q8_x, q8_d, I(wq.n_rows));
     check(tf_gemv_q4k_qkv(wq.data, wk.data, wv.data, q8_x, q8_d, q, k, v, I(wq.n_rows),

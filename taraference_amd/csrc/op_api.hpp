@@ -22,7 +22,7 @@
 
 namespace tf {
 
-enum class WType { Q4K, Q6K };
+enum class WType { Q4K, Q6K, Q5_0, Q8_0 };
 
 // cuda/types.rs:212-225
 struct GpuMat {
@@ -76,6 +76,10 @@ bool try_gemv_pair(hipStream_t s, const GpuMat& wa, const GpuMat& wb, const floa
 // matmul.rs:582 try_gemv_q4_dual
 bool try_gemv_q4_dual(hipStream_t s, const GpuMat& wa, const GpuMat& wb, const float* x,
                       float* out_a, float* out_b, int8_t* q8_x, float* q8_d);
+
+// matmul.rs:786 try_gemv_q5_dual (Q+K or gate+up, both Q5_0, f32 x)
+bool try_gemv_q5_dual(hipStream_t s, const GpuMat& wa, const GpuMat& wb, const float* x,
+                      float* out_a, float* out_b, const float* ba, const float* bb);
 
 // matmul.rs:627 try_gemv_q4_ffn: out = silu(gate x) * (up x)
 bool try_gemv_q4_ffn(hipStream_t s, const GpuMat& gate, const GpuMat& up, const float* x,

@@ -15,6 +15,8 @@ from . import capi, synth
 
 TYPE_Q4_K = 12
 TYPE_Q6_K = 14
+TYPE_Q5_0 = 6   # 32-value block formats: run on path 0 (the reference sequence)
+TYPE_Q8_0 = 8
 
 
 class TfMat(C.Structure):
@@ -92,9 +94,9 @@ class DecodeModel:
                 t = f.tensor(name)
                 if t is None:
                     raise ValueError(f"{path}: missing tensor {name}")
-                if t.type not in (GGML_Q4_K, GGML_Q6_K):
+                if t.type not in (GGML_Q4_K, GGML_Q6_K, TYPE_Q5_0, TYPE_Q8_0):
                     raise ValueError(f"{name}: ggml type {t.type} is not on the decode path "
-                                     "(Q4_K and Q6_K are)")
+                                     "(Q4_K, Q6_K, Q5_0 and Q8_0 are)")
                 if t.n_dims != 2 or t.dims[0] != n_rows:
                     raise ValueError(f"{name}: dims {list(t.dims[:t.n_dims])}, expected "
                                      f"[{n_rows}, n]")
@@ -209,6 +211,8 @@ class DecodeModel:
             return self._q4(w, n_rows)
         if typ == TYPE_Q6_K:
             return self._q6(w, n_rows, compact)
+        if typ in (TYPE_Q5_0, TYPE_Q8_0):
+            return TfMat(self._dev(w[0]).data_ptr(), None, typ, n_rows, w[0].shape[0], w[1], 0)
         raise ValueError(f"ggml type {typ} is not supported on the decode path")
 
     def _q4(self, wm, n_rows) -> TfMat:

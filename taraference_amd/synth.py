@@ -203,3 +203,42 @@ def weight_bytes(cfg: dict) -> int:
         tot += q6(f, e) if down_is_q6k(li) else q4(f, e)
     tot += q6(e, cfg["n_vocab"])
     return tot
+
+
+QWEN25_05B = dict(n_layer=24, n_embd=896, n_ff=4864, n_head=14, n_kv=2, head_dim=64,
+                  n_vocab=151936, rope_theta=1e6, rms_eps=1e-6)
+
+
+def qwen05_layer(rng, cfg: dict, layer: int) -> dict:
+    """Random-init weights of one Qwen2.5-0.5B-layout layer as a Q4_K_M file
+    stores them when the hidden width (896) is not a multiple of 256: the
+    896-row matrices fall back to Q5_0 (q/k/o/gate/up) and Q8_0 (v); down
+    (4864 rows) stays Q4_K / Q6_K.  Matrices are (bytes, col_bytes, ggml type)."""
+    e, f = cfg["n_embd"], cfg["n_ff"]
+    nq = cfg["n_head"] * cfg["head_dim"]
+    nkv = cfg["n_kv"] * cfg["head_dim"]
+
+    def t(m, typ):
+        return (m[0], m[1], typ)
+
+    L = {}
+    L["attn_norm"] = np.ones(e, np.float32)
+    L["ffn_norm"] = np.ones(e, np.float32)
+    L["wq"] = t(q5_0_matrix(rng, e, nq), 6)
+    L["wk"] = t(q5_0_matrix(rng, e, nkv), 6)
+    L["wv"] = t(q8_0_matrix(rng, e, nkv), 8)
+    L["bq"] = (rng.standard_normal(nq) * 0.02).astype(np.float32)
+    L["bk"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
+    L["bv"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
+    L["wo"] = t(q5_0_matrix(rng, nq, e), 6)
+    L["gate"] = t(q5_0_matrix(rng, e, f), 6)
+    L["up"] = t(q5_0_matrix(rng, e, f), 6)
+    L["down_q6k"] = down_is_q6k(layer)
+    L["down"] = t(q6k_matrix(rng, f, e), 14) if L["down_q6k"] else t(q4k_matrix(rng, f, e), 12)
+    return L
+
+
+def qwen05_embedding(rng, cfg: dict):
+    """Tied token embedding / lm_head of the 0.5B layout: Q8_0 [n_vocab, n_embd]."""
+    w, cb = q8_0_matrix(rng, cfg["n_embd"], cfg["n_vocab"])
+    return (w, cb, 8)

@@ -21,7 +21,7 @@ _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f
         BOOL: "<B", U64: "<Q", I64: "<q", F64: "<d"}
 
 # ggml (block elements, bytes per block) of the types the fixtures use
-TYPES = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+TYPES = {0: (1, 4), 1: (1, 2), 6: (32, 22), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
 
 
 def _string(s) -> bytes:
@@ -93,6 +93,15 @@ def model_tensors(cfg: dict, layers, embedding, output=None, output_norm=None,
     """(meta, tensors) of a dense decoder in the reference's GGUF names
     (cuda/load.rs:280-420) from synth.qwen_layer() dicts: matrices are
     [n_cols, col_bytes] byte arrays stored with dims [n_rows, n_cols]."""
+    meta = model_meta(cfg, arch)
+    c = cfg
+    qd, kvd = c["n_head"] * c["head_dim"], c["n_kv"] * c["head_dim"]
+    t = []
+    return _model_tensor_list(cfg, layers, embedding, output, output_norm, meta, t, qd, kvd)
+
+
+def model_meta(cfg: dict, arch: str = "qwen2"):
+    """The metadata of a dense decoder (config.rs:107-175 keys)."""
     c = cfg
     meta = [
         ("general.architecture", STRING, arch),
@@ -106,8 +115,11 @@ def model_tensors(cfg: dict, layers, embedding, output=None, output_norm=None,
         (f"{arch}.rope.freq_base", F32, c["rope_theta"]),
         (f"{arch}.attention.layer_norm_rms_epsilon", F32, c["rms_eps"]),
     ]
-    qd, kvd = c["n_head"] * c["head_dim"], c["n_kv"] * c["head_dim"]
-    t = []
+    return meta
+
+
+def _model_tensor_list(cfg, layers, embedding, output, output_norm, meta, t, qd, kvd):
+    c = cfg
 
     def mat(name, wm, ty, n_rows):
         w, cb = wm[0], wm[1]
