@@ -122,6 +122,32 @@ def config4(ctx=32768, n_gen=128):
     return out
 
 
+def q05_decode(context, steps):
+    """Decode tok/s of a random-init Qwen2.5-0.5B-layout model: the 896-row
+    matrices Q5_0 (q/k/o/gate/up) and Q8_0 (v, tied embedding), ffn_down
+    Q4_K/Q6_K; the runtime's reference operator sequence (path 0) replayed
+    from a HIP graph; timed as decode_throughput."""
+    from taraference_amd import synth
+    from taraference_amd.model import DecodeModel
+
+    cfg = dict(synth.QWEN25_05B)
+    rng = np.random.default_rng(0x7A7A0005)
+    t0 = time.time()
+    layers = [synth.qwen05_layer(rng, cfg, li) for li in range(cfg["n_layer"])]
+    emb = synth.qwen05_embedding(rng, cfg)
+    m = DecodeModel(dict(cfg, max_seq=context + steps + 8), layers, emb)
+    log(f"[bench] 0.5B-layout model built in {time.time() - t0:.1f}s, path {m.path()}")
+    dt, toks, dt_ev = decode_throughput(m, cfg, context, steps, 5)
+    wbytes = sum(int(v[0].nbytes) for L in layers for k, v in L.items()
+                 if isinstance(v, tuple)) + int(emb[0].nbytes)
+    out = {"model": "Qwen2.5-0.5B layout (Q5_0/Q8_0 896-wide, Q4_K/Q6_K down, Q8_0 tied "
+                    "embedding)", "path": m.path(), "context": context, "decode_tokens": steps,
+           "tok_s": round(steps / dt, 1), "ms_per_token_events": round(dt_ev * 1e3 / steps, 3),
+           "weight_bytes_per_token": wbytes}
+    m.close()
+    return out
+
+
 def prefill_throughput(m, cfg, n_tok, reps=3):
     """Prompt tokens/s of the runtime's batched prefill (tf_model_prefill:
     n_tok tokens from position 0, K/V written, last-token logits), median of
@@ -293,6 +319,9 @@ def main():
     ap.add_argument("--config4", action="store_true",
                     help="BASELINE config 4 instead: Qwen2.5-7B shape, 32768-token context "
                          "filled by prefill, then 128 timed greedy tokens")
+    ap.add_argument("--q05", action="store_true",
+                    help="instead: a Qwen2.5-0.5B-layout model (Q5_0/Q8_0 896-wide matrices, "
+                         "path 0), 512-token context, 256 timed greedy tokens")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     args = ap.parse_args()
@@ -315,6 +344,9 @@ def main():
         return
     if args.config4:
         print(json.dumps(config4()), flush=True)
+        return
+    if args.q05:
+        print(json.dumps(q05_decode(args.warmup, max(2, args.steps))), flush=True)
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
