@@ -131,7 +131,7 @@ struct tf_model {
     // prefill workspace (n_tok-row activations of one chunk), allocated on
     // the first prefill
     float *pf_x = nullptr, *pf_xb = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr,
-          *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr;
+          *pf_att = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_ws = nullptr;
     int* pf_tok = nullptr;
     std::vector<void*> allocs;
 
@@ -614,11 +614,11 @@ struct tf_model {
     static constexpr int kPrefillChunk = 256;
 
     // x[t] (+)= W xin[t] for n rows on the matrix cores (raw GGUF bytes).
-    static void gemm(hipStream_t s, const GpuMat& w, const float* xin, float* out, int n,
-                     bool accumulate) {
+    void gemm(hipStream_t s, const GpuMat& w, const float* xin, float* out, int n,
+              bool accumulate) {
         tf::check(tf_gemm_kq(w.wtype == tf::WType::Q6K, w.data, xin, out, (int)w.n_rows,
                              (int)w.n_cols, (int)w.col_bytes, n, accumulate ? 1 : 0,
-                             reinterpret_cast<tf_stream_t>(s)),
+                             reinterpret_cast<tf_stream_t>(s), pf_ws, kGemmWsFloats),
                   "prefill gemm");
     }
 
@@ -647,6 +647,7 @@ struct tf_model {
             pf_g = alloc<float>((size_t)CH * F);
             pf_u = alloc<float>((size_t)CH * F);
             pf_tok = alloc<int>(CH);
+            pf_ws = alloc<float>(kGemmWsFloats);
         }
         const tf_stream_t ts = reinterpret_cast<tf_stream_t>(s);
         int last = 0;

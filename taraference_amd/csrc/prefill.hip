@@ -183,7 +183,8 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
                                                           const float* __restrict__ x,
                                                           float* __restrict__ out, int n_rows,
                                                           int n_cols, int col_bytes, int n_tok,
-                                                          int accumulate) {
+                                                          int accumulate, int n_split,
+                                                          long long split_stride) {
     constexpr int NSUB = Q6 ? 16 : 8;
     constexpr int BLK = Q6 ? 210 : 144;
     __shared__ __align__(16) uint8_t xp[TF_PF_XBYTES];
@@ -196,6 +197,11 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
     const int t0 = blockIdx.x * TF_PF_TOKS;
     const int c0 = blockIdx.y * TF_PF_COLS;
     const int nb = n_rows / 256;
+    // split z of n_split takes super-blocks [sb_lo, sb_hi) into its own slice
+    const int z = blockIdx.z;
+    const int sb_lo = (int)((long long)z * nb / n_split);
+    const int sb_hi = (int)((long long)(z + 1) * nb / n_split);
+    out += (size_t)z * (size_t)split_stride;
     // this lane's A columns (one per 16-column tile), clamped for loads
     int colA[2];
     for (int ct = 0; ct < 2; ct++) {
@@ -277,11 +283,11 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
     float4 xr[8];
     uint32_t hd[5];
     for (int ct = 0; ct < 2; ct++)
-        tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes, g, wc[ct]);
-    load_x(0, xr);
-    load_hdr(0, hd);
+        tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)sb_lo * BLK, g, wc[ct]);
+    load_x(sb_lo, xr);
+    load_hdr(sb_lo, hd);
     TF_GSTAMP(0);
-    for (int sb = 0; sb < nb; sb++) {
+    for (int sb = sb_lo; sb < sb_hi; sb++) {
         TF_GSTAMP(1 + 4 * sb);
         __syncthreads();  // the previous super-block's LDS reads are done
         TF_GSTAMP(2 + 4 * sb);
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
         store_hdr(hd);
         __syncthreads();
         TF_GSTAMP(3 + 4 * sb);
-        if (sb + 1 < nb) {  // workgroup-uniform
+        if (sb + 1 < sb_hi) {  // workgroup-uniform
             for (int ct = 0; ct < 2; ct++)
                 tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)(sb + 1) * BLK, g,
                                    wn[ct]);
@@ -358,6 +364,284 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
             if (t >= n_tok) continue;
             float* o = out + (size_t)t * n_cols + cb;
             // accumulate: out += W x (the residual stream), one rounding
+            if (cb + 3 < n_cols && ((n_cols & 3) == 0)) {
+                float4 v = make_float4(acc[ct][tt][0], acc[ct][tt][1], acc[ct][tt][2],
+                                       acc[ct][tt][3]);
+                if (accumulate) {
+                    const float4 o0 = *reinterpret_cast<const float4*>(o);
+                    v = make_float4(o0.x + v.x, o0.y + v.y, o0.z + v.z, o0.w + v.w);
+                }
+                *reinterpret_cast<float4*>(o) = v;
+            } else {
+                for (int r = 0; r < 4; r++)
+                    if (cb + r < n_cols) o[r] = accumulate ? o[r] + acc[ct][tt][r] : acc[ct][tt][r];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- Q4_K GEMM, f16 operands
+//
+// The Q4_K GEMM on v_mfma_f32_16x16x32_f16 with the sub-block scale folded
+// into the A operand, so a whole super-block accumulates in the matrix
+// cores and the scales are applied once per super-block:
+//   A = sc_s * q   (integer <= 63 * 15 = 945: exact in f16),
+//   x = 2^-e (h0 + h1), h0 = f16(x 2^e), h1 = f16(x 2^e - h0), with e per
+//       (token, super-block) chosen so max |x 2^e| lies in [2^14, 2^15);
+//       the split keeps 22 bits (|x - 2^-e (h0 + h1)| <= 2^-23 |x|, plus
+//       2^-25 absolute in the subnormal range of h1),
+//   P = sum_k A h (two MFMAs per K step, exact products, fp32 sums),
+//   M = sum_s m_s S_s with S_s = 2^(e-5) sum(x over sub-block s) split into
+//       two f16 parts (one v_mfma_f32_16x16x16_f16 pair, K = 8 padded to 16),
+//   acc += d 2^-e P - dmin 2^(5-e) M.
+// Against the reference's fp32 product the difference is the split error
+// (2^-23 relative per term) and the fp32 summation order.
+//
+// A is built from the packed nibbles without conversions: (b & 0x000F000F)
+// | 0x64006400 holds 1024 + q of bytes 0 and 2 as two f16, and one packed
+// fma with (sc, -1024 sc) gives sc q (fused: the product is not rounded).
+// A lane's 8 K values therefore come in the byte order 0 2 1 3 4 6 5 7, and
+// x is staged in LDS in that same order within each group of 8.
+
+typedef _Float16 tf_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 tf_h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 tf_h8 __attribute__((ext_vector_type(8)));
+
+#define TF_PH_ROW 528  // 256 f16 + 16 bytes of padding
+#define TF_PH_XBYTES (2 * TF_PF_TOKS * TF_PH_ROW)
+#ifndef TF_PH_WAVES
+#define TF_PH_WAVES __attribute__((amdgpu_waves_per_eu(3)))
+#endif
+
+__device__ __forceinline__ uint32_t tf_ph_pk(float a, float b) {
+    const tf_h2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// A operand (8 values sc q) from two qs dwords, nibble shift sh (0 or 4).
+// (v & mask) | magic in one instruction; gfx9 VOP3 takes no literal, so the
+// mask comes in a VGPR and the magic in an SGPR.
+__device__ __forceinline__ uint32_t tf_ph_and_or(uint32_t v, uint32_t mask_v) {
+    uint32_t r;
+    asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(mask_v), "s"(0x64006400u));
+    return r;
+}
+__device__ __forceinline__ tf_h8 tf_ph_a(uint32_t lo, uint32_t hi, int sh, uint2 scn,
+                                         uint32_t mask_v) {
+    const tf_h2 s2 = __builtin_bit_cast(tf_h2, scn.x), n2 = __builtin_bit_cast(tf_h2, scn.y);
+    const uint32_t t[4] = {tf_ph_and_or(lo >> sh, mask_v), tf_ph_and_or(lo >> (sh + 8), mask_v),
+                           tf_ph_and_or(hi >> sh, mask_v), tf_ph_and_or(hi >> (sh + 8), mask_v)};
+    tf_h8 a;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const tf_h2 v = __builtin_elementwise_fma(__builtin_bit_cast(tf_h2, t[i]), s2, n2);
+        a[2 * i] = v[0];
+        a[2 * i + 1] = v[1];
+    }
+    return a;
+}
+
+__global__ __launch_bounds__(256) TF_PH_WAVES void tf_gemm_q4k_h_kernel(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x,
+                                                            float* __restrict__ out, int n_rows,
+                                                            int n_cols, int col_bytes, int n_tok,
+                                                            int accumulate, int n_split,
+                                                            long long split_stride) {
+    __shared__ __align__(16) uint8_t xp[TF_PH_XBYTES];      // [part][token][256] f16
+    __shared__ __align__(16) _Float16 xsm[2 * TF_PF_TOKS * 8];  // [part][token][sub-block]
+    __shared__ float xinv[TF_PF_TOKS];                       // 2^-e per token
+    __shared__ __align__(16) uint2 scn[8 * TF_PF_COLS];      // [sub-block][column] (sc, -1024 sc)
+    __shared__ __align__(16) _Float16 mh[TF_PF_COLS * 8];    // [column][sub-block] m
+    __shared__ __align__(16) float dd[TF_PF_COLS], dm[TF_PF_COLS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int t0 = blockIdx.x * TF_PF_TOKS;
+    const int c0 = blockIdx.y * TF_PF_COLS;
+    const int nb = n_rows / 256;
+    const int z = blockIdx.z;
+    const int sb_lo = (int)((long long)z * nb / n_split);
+    const int sb_hi = (int)((long long)(z + 1) * nb / n_split);
+    out += (size_t)z * (size_t)split_stride;
+    int colA[2];
+    for (int ct = 0; ct < 2; ct++) {
+        const int c = c0 + 32 * wave + 16 * ct + l16;
+        colA[ct] = c < n_cols ? c : n_cols - 1;
+    }
+    tf_f32x4 acc[2][2];
+    for (int ct = 0; ct < 2; ct++)
+        for (int tt = 0; tt < 2; tt++) acc[ct][tt] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int xt = tid >> 3, xs = tid & 7;  // staging: token xt, sub-block xs
+    const bool xlive = t0 + xt < n_tok;
+    const float* xrow = x + (size_t)(xlive ? t0 + xt : 0) * n_rows + 32 * xs;
+    const int hc = c0 + tid < n_cols ? c0 + tid : n_cols - 1;
+    const uint8_t* hcol = w + (size_t)hc * col_bytes;
+    auto load_x = [&](int sb, float4 (&xr)[8]) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) xr[k] = *reinterpret_cast<const float4*>(xrow + sb * 256 + 4 * k);
+    };
+    auto load_hdr = [&](int sb, tf_u32x4& hd) {
+        if (tid >= TF_PF_COLS) return;
+        hd = tf_ld16_a4(hcol + (size_t)sb * 144);
+    };
+    auto store_x = [&](const float4 (&xr)[8]) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = xlive ? xr[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[4 * k] = q.x;
+            v[4 * k + 1] = q.y;
+            v[4 * k + 2] = q.z;
+            v[4 * k + 3] = q.w;
+        }
+        float gs = 0.f, amax = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            gs += (v[4 * k] + v[4 * k + 1]) + (v[4 * k + 2] + v[4 * k + 3]);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[4 * k]), fabsf(v[4 * k + 1])),
+                                     fmaxf(fabsf(v[4 * k + 2]), fabsf(v[4 * k + 3]))));
+        }
+        // max over the token's 8 staging threads (consecutive lanes)
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        // f = 2^fe with fe = 14 - floor(log2 amax); fe <= 126 keeps 2^-fe a
+        // normal float (amax below 2^-112 then scales to below 2^14)
+        const int eb = (int)((__float_as_uint(amax) >> 23) & 0xff);
+        int fe = amax > 0.f ? 141 - eb : 0;
+        fe = fe > 126 ? 126 : fe;
+        const float f = __uint_as_float((uint32_t)(fe + 127) << 23);
+        if (xs == 0) xinv[xt] = __uint_as_float((uint32_t)(127 - fe) << 23);
+        const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+            uint32_t h0[4], h1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a = v[8 * gg + perm[2 * i]] * f, b = v[8 * gg + perm[2 * i + 1]] * f;
+                const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+                h0[i] = __builtin_bit_cast(uint32_t, tf_h2{ah, bh});
+                h1[i] = tf_ph_pk(a - (float)ah, b - (float)bh);
+            }
+            *reinterpret_cast<tf_u32x4*>(xp + xt * TF_PH_ROW + 2 * (32 * xs + 8 * gg)) =
+                tf_u32x4{h0[0], h0[1], h0[2], h0[3]};
+            *reinterpret_cast<tf_u32x4*>(xp + (TF_PF_TOKS + xt) * TF_PH_ROW +
+                                         2 * (32 * xs + 8 * gg)) =
+                tf_u32x4{h1[0], h1[1], h1[2], h1[3]};
+        }
+        const float sv = gs * f * 0.03125f;  // |sv| <= 2^15
+        const _Float16 s0 = (_Float16)sv;
+        xsm[xt * 8 + xs] = s0;
+        xsm[(TF_PF_TOKS + xt) * 8 + xs] = (_Float16)(sv - (float)s0);
+    };
+    auto store_hdr = [&](const tf_u32x4& hd) {
+        if (tid >= TF_PF_COLS) return;
+        dd[tid] = tf_h2f(hd.x);
+        dm[tid] = tf_h2f(hd.x >> 16);
+        uint8_t s12[12];
+        const uint32_t hw[3] = {hd.y, hd.z, hd.w};
+#pragma unroll
+        for (int i = 0; i < 12; i++) s12[i] = (uint8_t)(hw[i / 4] >> (8 * (i % 4)));
+        _Float16 mv[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            int sc, m;
+            tf_pf_scale_min(s12, s, sc, m);
+            const float scf = (float)sc;
+            scn[s * TF_PF_COLS + tid] = make_uint2(tf_ph_pk(scf, scf),
+                                                   tf_ph_pk(-1024.f * scf, -1024.f * scf));
+            mv[s] = (_Float16)m;
+        }
+        *reinterpret_cast<tf_h8*>(mh + 8 * tid) =
+            tf_h8{mv[0], mv[1], mv[2], mv[3], mv[4], mv[5], mv[6], mv[7]};
+    };
+
+    TfPfCol<false> wc[2], wn[2];
+    float4 xr[8];
+    tf_u32x4 hd = {0, 0, 0, 0};
+    uint32_t mask_v = 0x000F000Fu;
+    asm volatile("" : "+v"(mask_v));  // keep the mask in a VGPR
+    for (int ct = 0; ct < 2; ct++)
+        tf_pf_load_col<false>(w + (size_t)colA[ct] * col_bytes + (size_t)sb_lo * 144, g, wc[ct]);
+    load_x(sb_lo, xr);
+    load_hdr(sb_lo, hd);
+    for (int sb = sb_lo; sb < sb_hi; sb++) {
+        __syncthreads();  // the previous super-block's LDS reads are done
+        store_x(xr);
+        store_hdr(hd);
+        __syncthreads();
+        if (sb + 1 < sb_hi) {  // workgroup-uniform
+            for (int ct = 0; ct < 2; ct++)
+                tf_pf_load_col<false>(w + (size_t)colA[ct] * col_bytes + (size_t)(sb + 1) * 144,
+                                      g, wn[ct]);
+            load_x(sb + 1, xr);
+            load_hdr(sb + 1, hd);
+        }
+        tf_f32x4 P[2][2], M[2][2];
+        for (int ct = 0; ct < 2; ct++)
+            for (int tt = 0; tt < 2; tt++) {
+                P[ct][tt] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
+                M[ct][tt] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            tf_h8 b[2][2];
+            for (int tt = 0; tt < 2; tt++)
+                for (int pl = 0; pl < 2; pl++)
+                    b[tt][pl] = *reinterpret_cast<const tf_h8*>(
+                        xp + (pl * TF_PF_TOKS + 16 * tt + l16) * TF_PH_ROW + 2 * (32 * s + 8 * g));
+            for (int ct = 0; ct < 2; ct++) {
+                const uint2 sn = scn[s * TF_PF_COLS + 32 * wave + 16 * ct + l16];
+                const tf_h8 a = tf_ph_a(wc[ct].w[2 * (s >> 1)], wc[ct].w[2 * (s >> 1) + 1],
+                                        4 * (s & 1), sn, mask_v);
+                for (int tt = 0; tt < 2; tt++) {
+                    P[ct][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[tt][0], P[ct][tt], 0, 0, 0);
+                    P[ct][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[tt][1], P[ct][tt], 0, 0, 0);
+                }
+            }
+        }
+        // min term: K = the 8 sub-blocks (lanes g < 2), zero-padded to 16
+        {
+            tf_h4v bm[2][2], am[2];
+            const tf_h4v z = {0, 0, 0, 0};
+            for (int tt = 0; tt < 2; tt++)
+                for (int pl = 0; pl < 2; pl++)
+                    bm[tt][pl] = g < 2 ? *reinterpret_cast<const tf_h4v*>(
+                                             xsm + (pl * TF_PF_TOKS + 16 * tt + l16) * 8 + 4 * g)
+                                       : z;
+            for (int ct = 0; ct < 2; ct++)
+                am[ct] = g < 2 ? *reinterpret_cast<const tf_h4v*>(
+                                     mh + 8 * (32 * wave + 16 * ct + l16) + 4 * g)
+                               : z;
+            for (int ct = 0; ct < 2; ct++)
+                for (int tt = 0; tt < 2; tt++) {
+                    M[ct][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(am[ct], bm[tt][0], M[ct][tt], 0, 0, 0);
+                    M[ct][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(am[ct], bm[tt][1], M[ct][tt], 0, 0, 0);
+                }
+        }
+        // acc += d 2^-e P - dmin 2^(5-e) M; C rows 4g+r = columns, C column l16 = token
+        for (int ct = 0; ct < 2; ct++) {
+            const int cl = 32 * wave + 16 * ct + 4 * g;
+            const float4 d4 = *reinterpret_cast<const float4*>(dd + cl);
+            const float4 m4 = *reinterpret_cast<const float4*>(dm + cl);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, mv[4] = {m4.x, m4.y, m4.z, m4.w};
+            for (int tt = 0; tt < 2; tt++) {
+                const float fi = xinv[16 * tt + l16];
+                for (int r = 0; r < 4; r++) {
+                    float v = acc[ct][tt][r] + (dv[r] * fi) * P[ct][tt][r];
+                    acc[ct][tt][r] = v - (mv[r] * (32.f * fi)) * M[ct][tt][r];
+                }
+            }
+        }
+        for (int ct = 0; ct < 2; ct++) wc[ct] = wn[ct];
+    }
+    for (int ct = 0; ct < 2; ct++) {
+        const int cb = c0 + 32 * wave + 16 * ct + 4 * g;
+        for (int tt = 0; tt < 2; tt++) {
+            const int t = t0 + 16 * tt + l16;
+            if (t >= n_tok) continue;
+            float* o = out + (size_t)t * n_cols + cb;
             if (cb + 3 < n_cols && ((n_cols & 3) == 0)) {
                 float4 v = make_float4(acc[ct][tt][0], acc[ct][tt][1], acc[ct][tt][2],
                                        acc[ct][tt][3]);
@@ -645,10 +929,41 @@ int tf_pf_silu_mul(float* g, const float* u, long long n, tf_stream_t stream) {
     return TF_LAUNCH_RESULT();
 }
 
+// out[i] (+)= sum over z of part[z][i], z in order (split-K of the GEMM).
+__global__ __launch_bounds__(256) void tf_gemm_split_reduce_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ out,
+                                                                   long long n4, int n_split,
+                                                                   int accumulate) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4* p = reinterpret_cast<const float4*>(part) + i;
+    float4 v = p[0];
+    for (int z = 1; z < n_split; z++) {
+        const float4 q = p[(size_t)z * (size_t)n4];
+        v = make_float4(v.x + q.x, v.y + q.y, v.z + q.z, v.w + q.w);
+    }
+    float4* o = reinterpret_cast<float4*>(out) + i;
+    if (accumulate) {
+        const float4 r = *o;
+        v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+    }
+    *o = v;
+}
+
 // ---------------------------------------------------------------- C ABI
 
+// TF_GEMM_BF16=1 selects the three-part bf16 Q4_K kernel (A/B measurements).
+static bool tf_gemm_bf16_q4k() {
+    static const bool on = [] {
+        const char* e = getenv("TF_GEMM_BF16");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
+
 int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows, int n_cols,
-               int col_bytes, int n_tok, int accumulate, tf_stream_t stream) {
+               int col_bytes, int n_tok, int accumulate, tf_stream_t stream, float* ws,
+               size_t ws_floats) {
     const int nb = n_rows / 256;
     const int blk = q6 ? 210 : 144;
     TF_CHECK_ARG(w && x && out && nb > 0 && n_cols > 0 && n_tok > 0);
@@ -656,25 +971,46 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
     if (q6) TF_CHECK_ARG(((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
     else TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0);
     TF_CHECK_ARG(((uintptr_t)out & 15) == 0);
-    const dim3 grid((n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS, (n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
+    dim3 grid((n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS, (n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
     TF_CHECK_ARG(grid.y <= 65535);
+    // Split-K when the tile grid leaves the chip short of workgroups (about
+    // three per CU resident): partial slices into ws, then a fixed-order sum.
+    const size_t tiles = (size_t)grid.x * grid.y;
+    const size_t slice = (size_t)n_tok * n_cols;
+    int n_split = 1;
+    if (ws && tiles < 384 && (n_cols & 3) == 0 && ((uintptr_t)ws & 15) == 0) {
+        n_split = (int)((768 + tiles - 1) / tiles);
+        if (n_split > nb) n_split = nb;
+        while (n_split > 1 && (size_t)n_split * slice > ws_floats) n_split--;
+    }
+    grid.z = n_split;
+    float* dst = n_split > 1 ? ws : out;
+    const int acc = n_split > 1 ? 0 : accumulate;
     if (q6)
         hipLaunchKernelGGL(tf_gemm_kq_kernel<true>, grid, dim3(256), 0, tf_stream(stream), w, x,
-                           out, n_rows, n_cols, col_bytes, n_tok, accumulate);
-    else
+                           dst, n_rows, n_cols, col_bytes, n_tok, acc, n_split, (long long)slice);
+    else if (tf_gemm_bf16_q4k())
         hipLaunchKernelGGL(tf_gemm_kq_kernel<false>, grid, dim3(256), 0, tf_stream(stream), w, x,
-                           out, n_rows, n_cols, col_bytes, n_tok, accumulate);
+                           dst, n_rows, n_cols, col_bytes, n_tok, acc, n_split, (long long)slice);
+    else
+        hipLaunchKernelGGL(tf_gemm_q4k_h_kernel, grid, dim3(256), 0, tf_stream(stream), w, x,
+                           dst, n_rows, n_cols, col_bytes, n_tok, acc, n_split, (long long)slice);
+    if (n_split > 1) {
+        const long long n4 = (long long)(slice / 4);
+        hipLaunchKernelGGL(tf_gemm_split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)),
+                           dim3(256), 0, tf_stream(stream), ws, out, n4, n_split, accumulate);
+    }
     return TF_LAUNCH_RESULT();
 }
 
 extern "C" int tf_gemm_q4k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
                                int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
-    return tf_gemm_kq(false, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream);
+    return tf_gemm_kq(false, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream, nullptr, 0);
 }
 
 extern "C" int tf_gemm_q6k_f32(const uint8_t* w, const float* x, float* out, int n_rows,
                                int n_cols, int col_bytes, int n_tok, tf_stream_t stream) {
-    return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream);
+    return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream, nullptr, 0);
 }
 
 int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,

@@ -7,8 +7,15 @@
 #include "taraference_hip.h"
 
 // out[t][j] (+)= sum_k W[k][j] x[t][k]; q6: raw 210-byte Q6_K, else Q4_K.
+// ws (ws_floats, 16-byte aligned, may be null) lets a GEMM with few output
+// tiles split K into slices summed in a fixed order afterwards;
+// kGemmWsFloats covers every shape.
 int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows, int n_cols,
-               int col_bytes, int n_tok, int accumulate, tf_stream_t stream);
+               int col_bytes, int n_tok, int accumulate, tf_stream_t stream, float* ws,
+               size_t ws_floats);
+// split-K workspace that serves any shape: n_split * n_tok * n_cols with
+// n_split = ceil(768 / tiles) and tiles < 384 of 32 x 128 outputs.
+static const size_t kGemmWsFloats = (size_t)1152 * 32 * 128;
 int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                         float* out, int n_head, int n_kv, int head_dim, int pos0,
                         const int* pos0_dev, int n_q, float scale, tf_stream_t stream);
