@@ -779,6 +779,206 @@ __global__ __launch_bounds__(256) void tf_attn_prefill_kernel(
     }
 }
 
+// Matrix-core form for head_dim 128.  A workgroup (4 waves) owns one head
+// and 16 queries; the waves split the 32-key tiles round-robin, each staging
+// its own tiles in LDS, and merge their (m, l, O) with the log-sum-exp rule
+// at the end (a wave with no keys for a query contributes e^(-1e30 - M) = 0).
+// Per tile, on v_mfma_f32_16x16x32_f16:
+//   S^T = K q^T: A = K rows (A row i of key block b is key
+//       8 (i / 4) + 4 b + i % 4, so the C values a lane holds, key rows
+//       4g .. 4g+3 of blocks 0 and 1, are the tile's keys 8g .. 8g+7), B =
+//       q^T, q split into two f16 parts after a power-of-two scale (2^-22
+//       relative per product; K is f16, the products are exact);
+//   O += P V: A = P (query l16, keys 8g .. 8g+7: the lane's own S values
+//       after the softmax, split into two f16 parts), B = V gathered from
+//       the row-major f16 tile (8 u16 reads per fragment).
+// Softmax per query: the lane's 8 values, then the 4 lanes of the query
+// (xor 16, 32).  Keys past the workgroup's last query are staged as zeros.
+
+#define TF_PM_T 32              // keys per tile
+#define TF_PM_KROW 272          // K tile row bytes (128 f16 + 16)
+#define TF_PM_VROW 264          // V tile row bytes (128 f16 + 8): 8-row gathers on distinct banks
+#define TF_PM_WAVE_BYTES (TF_PM_T * TF_PM_KROW + TF_PM_T * TF_PM_VROW)
+
+__global__ __launch_bounds__(256) void tf_attn_prefill_mfma_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ out, int n_head, int n_kv, int pos0_arg, const int* __restrict__ pos0_ptr,
+    int n_q, float scale) {
+    constexpr int HD = 128;
+    __shared__ __align__(16) uint8_t lds[4 * TF_PM_WAVE_BYTES];
+    __shared__ float ml[2][4][16];
+    const int pos0 = pos0_ptr ? pos0_ptr[0] : pos0_arg;
+    const int h = blockIdx.y, q0 = blockIdx.x * 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int kv_h = h / (n_head / n_kv), stride = n_kv * HD;
+    const int last_q = (q0 + 16 < n_q ? q0 + 16 : n_q) - 1;
+    const int kv_len = pos0 + last_q + 1;  // keys the workgroup reads
+    const int n_t = (kv_len + TF_PM_T - 1) / TF_PM_T;
+    uint8_t* kt = lds + wave * TF_PM_WAVE_BYTES;
+    uint8_t* vt = kt + TF_PM_T * TF_PM_KROW;
+
+    // q^T fragments: query l16, dims 32 st + 8 g .. +7, two f16 parts
+    const int my_q = q0 + l16 < n_q ? q0 + l16 : last_q;
+    const int qpos = pos0 + my_q;
+    float qv[32];
+    {
+        const float* qr = q + (size_t)my_q * n_head * HD + (size_t)h * HD;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 32 * st + 8 * g);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 32 * st + 8 * g + 4);
+            qv[8 * st] = a.x; qv[8 * st + 1] = a.y; qv[8 * st + 2] = a.z; qv[8 * st + 3] = a.w;
+            qv[8 * st + 4] = b.x; qv[8 * st + 5] = b.y; qv[8 * st + 6] = b.z; qv[8 * st + 7] = b.w;
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(qv[i]));
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const int eb = (int)((__float_as_uint(amax) >> 23) & 0xff);
+    int fe = amax > 0.f ? 141 - eb : 0;
+    fe = fe > 126 ? 126 : fe;
+    const float f = __uint_as_float((uint32_t)(fe + 127) << 23);
+    const float sscale = scale * __uint_as_float((uint32_t)(127 - fe) << 23);
+    tf_h8 qb[4][2];
+#pragma unroll
+    for (int st = 0; st < 4; st++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float a = qv[8 * st + i] * f;
+            const _Float16 hi = (_Float16)a;
+            qb[st][0][i] = hi;
+            qb[st][1][i] = (_Float16)(a - (float)hi);
+        }
+
+    float mx = -1e30f, l = 0.f;
+    tf_f32x4 o[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; nb++) o[nb] = tf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int ti = wave; ti < n_t; ti += 4) {
+        const int t0 = ti * TF_PM_T;
+        // stage K and V rows t0 .. t0+31 (zeros past kv_len)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int idx = lane + 64 * j, r = idx >> 4, c = idx & 15;
+            tf_u32x4 kb = {0, 0, 0, 0}, vb = {0, 0, 0, 0};
+            if (t0 + r < kv_len) {
+                const size_t off = (size_t)(t0 + r) * stride + (size_t)kv_h * HD + 8 * c;
+                kb = *reinterpret_cast<const tf_u32x4*>(kc + off);
+                vb = *reinterpret_cast<const tf_u32x4*>(vc + off);
+            }
+            *reinterpret_cast<tf_u32x4*>(kt + r * TF_PM_KROW + 16 * c) = kb;
+            uint32_t* vw = reinterpret_cast<uint32_t*>(vt + r * TF_PM_VROW + 16 * c);
+            vw[0] = vb.x; vw[1] = vb.y; vw[2] = vb.z; vw[3] = vb.w;  // 8-byte aligned rows
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // LDS stores of the wave done (lgkmcnt 0)
+        __builtin_amdgcn_wave_barrier();
+        // S^T: two key blocks, 4 K steps, 2 parts
+        tf_f32x4 sc[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int key = 8 * (l16 >> 2) + 4 * b + (l16 & 3);
+            tf_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const tf_h8 ka = *reinterpret_cast<const tf_h8*>(kt + key * TF_PM_KROW +
+                                                                 2 * (32 * st + 8 * g));
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[st][0], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[st][1], c, 0, 0, 0);
+            }
+            sc[b] = c;
+        }
+        // lane values: keys t0 + 8g + 4b + r of query my_q
+        float sv[8];
+        float tmax = -1e30f;
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int kp = t0 + 8 * g + 4 * b + r;
+                const float v = kp <= qpos ? sc[b][r] * sscale : -1e30f;
+                sv[4 * b + r] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(mx, tmax);
+        const float alpha = __expf(mx - m_new);
+        float ls = 0.f;
+        tf_h8 pa[2];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float e = sv[i] > -1e29f ? __expf(sv[i] - m_new) : 0.f;
+            ls += e;
+            const _Float16 hi = (_Float16)e;
+            pa[0][i] = hi;
+            pa[1][i] = (_Float16)(e - (float)hi);
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l = l * alpha + ls;
+        mx = m_new;
+        // O rows are queries 4g .. 4g+3: their alpha from lanes 4g + r
+        float al[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) al[r] = __shfl(alpha, 4 * g + r);
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[nb][r] *= al[r];
+            // V fragment: keys 8g .. 8g+7, dim 16 nb + l16
+            const uint8_t* vp = vt + (8 * g) * TF_PM_VROW + 2 * (16 * nb + l16);
+            tf_h8 vf;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                vf[i] = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(vp + i * TF_PM_VROW));
+            o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[0], vf, o[nb], 0, 0, 0);
+            o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1], vf, o[nb], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();  // tile reads done before the next staging
+    }
+    // merge the 4 waves: (m, l) per query, O through LDS
+    if (g == 0) {
+        ml[0][wave][l16] = mx;
+        ml[1][wave][l16] = l;
+    }
+    __syncthreads();  // every wave's tiles consumed; ml visible
+    float* ow = reinterpret_cast<float*>(lds + wave * TF_PM_WAVE_BYTES);  // [16][128]
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int qi = 4 * g + r;
+        float mall = ml[0][0][qi];
+        for (int w = 1; w < 4; w++) mall = fmaxf(mall, ml[0][w][qi]);
+        const float sc_w = __expf(ml[0][wave][qi] - mall);
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) ow[qi * HD + 16 * nb + l16] = o[nb][r] * sc_w;
+    }
+    __syncthreads();
+    {
+        const int qi = tid >> 4, d0 = 8 * (tid & 15);
+        if (q0 + qi < n_q) {
+            float mall = ml[0][0][qi];
+            for (int w = 1; w < 4; w++) mall = fmaxf(mall, ml[0][w][qi]);
+            float L = 0.f;
+            for (int w = 0; w < 4; w++) L += ml[1][w][qi] * __expf(ml[0][w][qi] - mall);
+            const float inv = 1.f / fmaxf(L, 1e-20f);
+            float acc[8];
+            for (int i = 0; i < 8; i++) acc[i] = 0.f;
+            for (int w = 0; w < 4; w++) {
+                const float* src = reinterpret_cast<const float*>(lds + w * TF_PM_WAVE_BYTES) + qi * HD + d0;
+                for (int i = 0; i < 8; i++) acc[i] += src[i];
+            }
+            float* dst = out + (size_t)(q0 + qi) * n_head * HD + (size_t)h * HD + d0;
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
+        }
+    }
+}
+
 // ------------------------------------------------- batched prefill glue
 //
 // The n_tok-row forms of the decode glue (kernels/ops.cu rms_norm_f32 with
@@ -1013,6 +1213,15 @@ extern "C" int tf_gemm_q6k_f32(const uint8_t* w, const float* x, float* out, int
     return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream, nullptr, 0);
 }
 
+// TF_ATTN_PREFILL_VALU=1 selects the vector-ALU attention for head_dim 128.
+static bool tf_attn_prefill_valu() {
+    static const bool on = [] {
+        const char* e = getenv("TF_ATTN_PREFILL_VALU");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
+
 int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                float* out, int n_head, int n_kv, int head_dim, int pos0,
                                const int* pos0_dev, int n_q, float scale, tf_stream_t stream) {
@@ -1027,7 +1236,11 @@ int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t*
                            n_head, n_kv, pos0, pos0_dev, n_q, scale);
     };
     if (head_dim == 64) go(tf_attn_prefill_kernel<64>);
-    else if (head_dim == 128) go(tf_attn_prefill_kernel<128>);
+    else if (head_dim == 128 && !tf_attn_prefill_valu()) {
+        const dim3 g16((n_q + 15) / 16, n_head);
+        hipLaunchKernelGGL(tf_attn_prefill_mfma_kernel, g16, dim3(256), 0, tf_stream(stream), q,
+                           k_cache, v_cache, out, n_head, n_kv, pos0, pos0_dev, n_q, scale);
+    } else if (head_dim == 128) go(tf_attn_prefill_kernel<128>);
     else go(tf_attn_prefill_kernel<256>);
     return TF_LAUNCH_RESULT();
 }

@@ -58,13 +58,20 @@ def test_gemm(gpu, fmt, n_rows, n_cols, n_tok):
     (14, 2, 64, 0, 200),    # Qwen2.5-0.5B heads
     (4, 1, 256, 5, 20),
     (28, 4, 128, 0, 1),     # Qwen2.5-7B heads, one query
+    (16, 2, 128, 1000, 50),  # many key tiles per query block
+    (28, 4, 128, 300, 256),  # Qwen2.5-7B heads, a full prompt chunk after 300 positions
 ])
-def test_attn_prefill(gpu, n_head, n_kv, hd, pos0, n_q):
-    print(f"attn prefill h={n_head} kv={n_kv} hd={hd} pos0={pos0} n_q={n_q}", flush=True)
+@pytest.mark.parametrize("junk", ["finite", "nan"])
+def test_attn_prefill(gpu, n_head, n_kv, hd, pos0, n_q, junk):
+    print(f"attn prefill h={n_head} kv={n_kv} hd={hd} pos0={pos0} n_q={n_q} junk={junk}",
+          flush=True)
     rng = np.random.default_rng(n_q * 3 + pos0)
     L = pos0 + n_q
-    K = synth.kv_cache(rng, L + 3, n_kv, hd)  # rows past the last query hold junk
-    V = synth.kv_cache(rng, L + 3, n_kv, hd)
+    K = synth.kv_cache(rng, L + 40, n_kv, hd)  # rows past the last query hold junk
+    V = synth.kv_cache(rng, L + 40, n_kv, hd)
+    if junk == "nan":  # f16 NaN past the last query: must never reach the output
+        K[L:] = 0x7E00
+        V[L:] = 0x7E00
     q = rng.standard_normal((n_q, n_head * hd)).astype(np.float32)
     scale = float(np.float32(1 / np.sqrt(hd)))
     kd, vd, qd = dev(K), dev(V), dev(q)
