@@ -322,6 +322,8 @@ def main():
     ap.add_argument("--q05", action="store_true",
                     help="instead: a Qwen2.5-0.5B-layout model (Q5_0/Q8_0 896-wide matrices, "
                          "path 0), 512-token context, 256 timed greedy tokens")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="only the runtime's 512-token prefill of the 3B-shape model")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     args = ap.parse_args()
@@ -350,6 +352,12 @@ def main():
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
+        return
+    if args.only_prefill:
+        cfg = dict(synth.QWEN25_3B)
+        m = build_model(cfg, 0x7A7A0003, 1024)
+        print(json.dumps({"prefill": prefill_throughput(m, cfg, 512)}), flush=True)
+        m.close()
         return
     cfg = dict(synth.QWEN25_3B)
     steps = max(2, args.steps)

@@ -43,6 +43,8 @@ typedef short tf_bf16x4 __attribute__((ext_vector_type(4)));
 typedef float tf_f32x4 __attribute__((ext_vector_type(4)));
 
 #define TF_PF_COLS 128  // output columns per workgroup
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt unchanged
+#define TF_VMCNT0 0x0F70
 #define TF_PF_TOKS 32   // tokens per workgroup
 
 // Three-part bf16 split of four floats (truncation; every remainder exact).
@@ -194,8 +196,17 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, l16 = lane & 15;
-    const int t0 = blockIdx.x * TF_PF_TOKS;
-    const int c0 = blockIdx.y * TF_PF_COLS;
+    // XCD-aware tile order: workgroups go round-robin to the 8 XCDs, so XCD
+    // k = blockIdx.x % 8 takes the contiguous tile range [k per, (k+1) per)
+    // (token tiles fastest): a column tile's weights are fetched into one
+    // XCD's L2 and reused there by all its token tiles.
+    const int ntx = (n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS;
+    const int n_tiles = ntx * ((n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
+    const int per = (n_tiles + 7) >> 3;
+    const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (tile >= n_tiles) return;  // workgroup-uniform, before any barrier
+    const int t0 = (tile % ntx) * TF_PF_TOKS;
+    const int c0 = (tile / ntx) * TF_PF_COLS;
     const int nb = n_rows / 256;
     // split z of n_split takes super-blocks [sb_lo, sb_hi) into its own slice
     const int z = blockIdx.z;
@@ -286,6 +297,11 @@ __global__ __launch_bounds__(256) void tf_gemm_kq_kernel(const uint8_t* __restri
         tf_pf_load_col<Q6>(w + (size_t)colA[ct] * col_bytes + (size_t)sb_lo * BLK, g, wc[ct]);
     load_x(sb_lo, xr);
     load_hdr(sb_lo, hd);
+    // Nothing may be pending at loop entry: the wait-count insertion merges
+    // the loop header's state over both edges, and a prologue load still in
+    // flight into wc would make every iteration wait for its own prefetch
+    // of the next super-block before the first use of wc.
+    __builtin_amdgcn_s_waitcnt(TF_VMCNT0);
     TF_GSTAMP(0);
     for (int sb = sb_lo; sb < sb_hi; sb++) {
         TF_GSTAMP(1 + 4 * sb);
@@ -456,8 +472,17 @@ __global__ __launch_bounds__(256) TF_PH_WAVES void tf_gemm_q4k_h_kernel(const ui
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, l16 = lane & 15;
-    const int t0 = blockIdx.x * TF_PF_TOKS;
-    const int c0 = blockIdx.y * TF_PF_COLS;
+    // XCD-aware tile order: workgroups go round-robin to the 8 XCDs, so XCD
+    // k = blockIdx.x % 8 takes the contiguous tile range [k per, (k+1) per)
+    // (token tiles fastest): a column tile's weights are fetched into one
+    // XCD's L2 and reused there by all its token tiles.
+    const int ntx = (n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS;
+    const int n_tiles = ntx * ((n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
+    const int per = (n_tiles + 7) >> 3;
+    const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (tile >= n_tiles) return;  // workgroup-uniform, before any barrier
+    const int t0 = (tile % ntx) * TF_PF_TOKS;
+    const int c0 = (tile / ntx) * TF_PF_COLS;
     const int nb = n_rows / 256;
     const int z = blockIdx.z;
     const int sb_lo = (int)((long long)z * nb / n_split);
@@ -566,6 +591,7 @@ __global__ __launch_bounds__(256) TF_PH_WAVES void tf_gemm_q4k_h_kernel(const ui
         tf_pf_load_col<false>(w + (size_t)colA[ct] * col_bytes + (size_t)sb_lo * 144, g, wc[ct]);
     load_x(sb_lo, xr);
     load_hdr(sb_lo, hd);
+    __builtin_amdgcn_s_waitcnt(TF_VMCNT0);  // nothing pending at loop entry (as above)
     for (int sb = sb_lo; sb < sb_hi; sb++) {
         __syncthreads();  // the previous super-block's LDS reads are done
         store_x(xr);
@@ -1171,11 +1197,14 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
     if (q6) TF_CHECK_ARG(((uintptr_t)w & 1) == 0 && (col_bytes & 1) == 0);
     else TF_CHECK_ARG(((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0);
     TF_CHECK_ARG(((uintptr_t)out & 15) == 0);
-    dim3 grid((n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS, (n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
-    TF_CHECK_ARG(grid.y <= 65535);
+    const size_t tiles = (size_t)((n_tok + TF_PF_TOKS - 1) / TF_PF_TOKS) *
+                         ((n_cols + TF_PF_COLS - 1) / TF_PF_COLS);
+    TF_CHECK_ARG(tiles <= (size_t)1 << 28);
+    // one-dimensional grid, 8 x ceil(tiles / 8) workgroups (the kernel maps
+    // them XCD by XCD; the padding exits at once)
+    dim3 grid((unsigned)(8 * ((tiles + 7) / 8)), 1);
     // Split-K when the tile grid leaves the chip short of workgroups (about
     // three per CU resident): partial slices into ws, then a fixed-order sum.
-    const size_t tiles = (size_t)grid.x * grid.y;
     const size_t slice = (size_t)n_tok * n_cols;
     int n_split = 1;
     if (ws && tiles < 384 && (n_cols & 3) == 0 && ((uintptr_t)ws & 15) == 0) {
