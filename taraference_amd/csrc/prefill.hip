@@ -1203,12 +1203,18 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
     // one-dimensional grid, 8 x ceil(tiles / 8) workgroups (the kernel maps
     // them XCD by XCD; the padding exits at once)
     dim3 grid((unsigned)(8 * ((tiles + 7) / 8)), 1);
-    // Split-K when the tile grid leaves the chip short of workgroups (about
-    // three per CU resident): partial slices into ws, then a fixed-order sum.
+    // Split-K when the tile grid leaves the chip short of workgroups: about
+    // 512 workgroups in all (TF_GEMM_SPLIT_TARGET overrides; measured on the
+    // 3B prefill against 384, 768, 1024 and 1536), partial slices into ws,
+    // then a fixed-order sum.
     const size_t slice = (size_t)n_tok * n_cols;
     int n_split = 1;
     if (ws && tiles < 384 && (n_cols & 3) == 0 && ((uintptr_t)ws & 15) == 0) {
-        n_split = (int)((768 + tiles - 1) / tiles);
+        static const int target = [] {
+            const char* e = getenv("TF_GEMM_SPLIT_TARGET");
+            return e && atoi(e) > 0 ? atoi(e) : 512;
+        }();
+        n_split = (int)((target + tiles - 1) / tiles);
         if (n_split > nb) n_split = nb;
         while (n_split > 1 && (size_t)n_split * slice > ws_floats) n_split--;
     }

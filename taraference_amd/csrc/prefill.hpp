@@ -14,7 +14,9 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
                int col_bytes, int n_tok, int accumulate, tf_stream_t stream, float* ws,
                size_t ws_floats);
 // split-K workspace that serves any shape: n_split * n_tok * n_cols with
-// n_split = ceil(768 / tiles) and tiles < 384 of 32 x 128 outputs.
+// n_split = ceil(512 / tiles) with tiles < 384 of 32 x 128 outputs needs at
+// most 896 tiles of slices; a larger split (the tuning override) is clamped
+// to what fits.
 static const size_t kGemmWsFloats = (size_t)1152 * 32 * 128;
 int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                         float* out, int n_head, int n_kv, int head_dim, int pos0,
