@@ -5,9 +5,10 @@ dominant kernel (the persistent decode-step kernel, one launch per token),
 the standalone config-1a Q4_K GEMV (fused gate+up) for the metric's GEMV
 part, and the CPU-oracle baseline timed on this host.
 
-Workload: --warmup W forced decode steps build the synthetic context
-(W = 512 by default, the config's context), then --steps K greedy decode
-steps are timed (K = 256 by default).  Each step is one full decode forward
+Workload: 512 forced decode steps build the synthetic context (config 3's
+context, untimed), --warmup W greedy steps run untimed from position 512
+(W = 16 by default), then --steps K greedy decode steps are timed from that
+same position (K = 256 by default).  Each step is one full decode forward
 (36 layers + lm_head + argmax) replayed from a captured HIP graph; the token
 feeds back on the device and the K generated tokens are copied to the host
 once at the end.  value = K / elapsed.
@@ -63,22 +64,26 @@ def build_model(cfg, seed, max_seq):
     return m
 
 
-def decode_throughput(m, cfg, warmup, steps, seed):
+def decode_throughput(m, cfg, context, warmup, steps, seed):
+    """Config-3 decode: `context` forced tokens build the context (untimed,
+    captures the step graph), `warmup` greedy steps from position `context`
+    (untimed), then `steps` greedy steps timed from the same position
+    (rewriting the same K/V rows).  Returns host seconds, the tokens and the
+    HIP-event seconds on the stream the step graph replays on."""
     import torch
 
     rng = np.random.default_rng(seed + 1)
-    prompt = rng.integers(0, cfg["n_vocab"], max(1, warmup)).tolist()
-    # untimed: the forced context (graph capture happens on the first call)
+    prompt = rng.integers(0, cfg["n_vocab"], context).tolist()
     first = m.generate(prompt, 1, pos0=0, use_graph=True)
+    if warmup:
+        m.generate([int(first[0])], warmup, pos0=context, use_graph=True)
     torch.cuda.synchronize()
-    # timed: `steps` decode steps continuing from the greedy token; HIP events
-    # on the stream the step graph is replayed on bracket the same region
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    toks = m.generate([int(first[0])], steps, pos0=len(prompt), use_graph=True)
+    toks = m.generate([int(first[0])], steps, pos0=context, use_graph=True)
     e1.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
@@ -137,7 +142,7 @@ def q05_decode(context, steps):
     emb = synth.qwen05_embedding(rng, cfg)
     m = DecodeModel(dict(cfg, max_seq=context + steps + 8), layers, emb)
     log(f"[bench] 0.5B-layout model built in {time.time() - t0:.1f}s, path {m.path()}")
-    dt, toks, dt_ev = decode_throughput(m, cfg, context, steps, 5)
+    dt, toks, dt_ev = decode_throughput(m, cfg, context, 0, steps, 5)
     wbytes = sum(int(v[0].nbytes) for L in layers for k, v in L.items()
                  if isinstance(v, tuple)) + int(emb[0].nbytes)
     out = {"model": "Qwen2.5-0.5B layout (Q5_0/Q8_0 896-wide, Q4_K/Q6_K down, Q8_0 tied "
@@ -229,93 +234,208 @@ def kernel_table(iters):
     return out
 
 
-def cpu_baseline(cfg, budget_s=20.0):
-    """The oracle's Q4_K/Q6_K x Q8 dequant-and-dot (the reference arithmetic
-    restated in C) on the host cores, on a bounded sample of the decode step:
-    the GEMVs of one even (Q4_K down) and one odd (Q6_K down) layer plus the
-    lm_head, repeated while the budget lasts; tok/s is extrapolated to the 36
-    layers.  Attention is not included (0.1% of the bytes at L = 512)."""
-    import oracle
-    from taraference_amd import synth
-
-    try:
-        avail = len(os.sched_getaffinity(0))
-    except AttributeError:
-        avail = os.cpu_count() or 1
-    threads = max(1, min(16, avail))
-    rng = np.random.default_rng(99)
-    e, f = cfg["n_embd"], cfg["n_ff"]
-    nq, nkv = cfg["n_head"] * cfg["head_dim"], cfg["n_kv"] * cfg["head_dim"]
-    x_e = synth.activation(rng, e)
-    x_f = synth.activation(rng, f)
-    qe, de = oracle.quantize_q8(x_e)
-    qf, df = oracle.quantize_q8(x_f)
-    wq, cb = synth.q4k_matrix(rng, e, nq + 2 * nkv)  # q, k (Q4_K) and v-sized rows
-    wo, _ = synth.q4k_matrix(rng, nq, e)
-    g, _ = synth.q4k_matrix(rng, e, f)
-    u, _ = synth.q4k_matrix(rng, e, f)
-    d4, fcb = synth.q4k_matrix(rng, f, e)
-    d6raw, _ = synth.q6k_matrix(rng, f, e)
-    d6, d6cb = synth.q6k_compact(d6raw, f)
-    del d6raw
-    head_raw, _ = synth.q6k_matrix(rng, e, cfg["n_vocab"])
-    head, hcb = synth.q6k_compact(head_raw, e)
-    del head_raw
-
-    def layer_pair():
-        for down_q6 in (False, True):
-            oracle.gemv_q4k_q8_mt(wq, qe, de, e, nq + 2 * nkv, cb, threads)
-            oracle.gemv_q4k_q8_mt(wo, qe, de, nq, e, cb, threads)
-            oracle.gemv_q4k_ffn_mt(g, u, qe, de, e, f, cb, threads)
-            if down_q6:
-                oracle.gemv_q6k_compact_q8_kway_mt(d6, qf, df, f, e, d6cb, 8, threads)
-            else:
-                oracle.gemv_q4k_q8_mt(d4, qf, df, f, e, fcb, threads)
-
-    def lm_head():
-        oracle.gemv_q6k_compact_q8_kway_mt(head, qe, de, e, cfg["n_vocab"], hcb, 1, threads)
-
-    layer_pair()  # warm caches / threads
-    t_pairs, t_heads = [], []
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(t_pairs) < 2:
-        t0 = time.perf_counter()
-        layer_pair()
-        t_pairs.append(time.perf_counter() - t0)
-        t0 = time.perf_counter()
-        lm_head()
-        t_heads.append(time.perf_counter() - t0)
-        if len(t_pairs) >= 20:
-            break
-    per_token = (cfg["n_layer"] / 2) * float(np.median(t_pairs)) + float(np.median(t_heads))
-    model = ""
+def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"oracle Q4_K/Q6_K x Q8 GEMVs of 2 layers (one Q4_K-down, one Q6_K-down)"
-                       f" + lm_head, {len(t_pairs)} reps, median, extrapolated to "
-                       f"{cfg['n_layer']} layers; attention excluded; CPU: {model}")}
+    return ""
+
+
+def _cpu_threads():
+    """Every core this process may run on (the affinity mask; on the GPU
+    boxes that is the one-GPU share of the host)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _median_us(fn, reps, warm=2):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)) * 1e6
+
+
+def cpu_kernel_table(threads_all, reps=20):
+    """The oracle's (the reference arithmetic restated in C) Q4_K/Q6_K x Q8
+    GEMVs and flash-decode partial at configs 0, 1a, 1b, 1c and 2 on the
+    host cores, single-threaded and on `threads_all` threads with output
+    columns (heads for attention) partitioned; median of `reps` runs after
+    two warm-up runs; GB/s over the same algorithmic bytes as the GPU table."""
+    import oracle
+    from taraference_amd import synth
+
+    rng = np.random.default_rng(98)
+    rows = {}
+
+    def q8(k):
+        return oracle.quantize_q8(synth.activation(rng, k))
+
+    def add(name, nbytes, fn):
+        r = {}
+        for label, th in (("1t", 1), ("mt", threads_all)):
+            us = _median_us(lambda: fn(th), reps)
+            r[f"us_{label}"] = round(us, 1)
+            r[f"GBs_{label}"] = round(nbytes / (us * 1e-6) / 1e9, 2)
+        r["MB"] = round(nbytes / 1e6, 3)
+        rows[name] = r
+        log(f"[bench] cpu {name}: {r}")
+
+    xq, xd = q8(896)
+    w0, cb0 = synth.q4k_matrix(rng, 896, 4864)
+    add("cfg0_q4k_896x4864", 4864 * 3 * 144 + 896 + 112 + 4 * 4864,
+        lambda th: oracle.gemv_q4k_q8_mt(w0, xq, xd, 896, 4864, cb0, th))
+    xq, xd = q8(2048)
+    g, cb = synth.q4k_matrix(rng, 2048, 11008)
+    u, _ = synth.q4k_matrix(rng, 2048, 11008)
+    add("cfg1a_q4k_gate_up_2048x2x11008", 2 * 11008 * 8 * 144 + 2048 + 256 + 4 * 11008,
+        lambda th: oracle.gemv_q4k_ffn_mt(g, u, xq, xd, 2048, 11008, cb, th))
+    del g, u
+    wqkv, cb = synth.q4k_matrix(rng, 2048, 2560)
+    add("cfg1c_q4k_qkv_2048x2560", 2560 * 8 * 144 + 2048 + 256 + 4 * 2560,
+        lambda th: oracle.gemv_q4k_q8_mt(wqkv, xq, xd, 2048, 2560, cb, th))
+    xq, xd = q8(11008)
+    raw, _ = synth.q6k_matrix(rng, 11008, 2048)
+    d6, ccb = synth.q6k_compact(raw, 11008)
+    del raw
+    add("cfg1b_q6k_down_11008x2048", 2048 * 43 * 210 + 11008 + 1376 + 8 * 2048,
+        lambda th: oracle.gemv_q6k_compact_q8_kway_mt(d6, xq, xd, 11008, 2048, ccb, 8, th))
+    del d6
+    n_head, n_kv, hd = 16, 2, 128
+    sc = float(np.float32(1 / np.sqrt(hd)))
+    q = synth.activation(rng, n_head * hd)
+    for L in (512, 4096, 32768):
+        Kc = synth.kv_cache(rng, L, n_kv, hd)
+        Vc = synth.kv_cache(rng, L, n_kv, hd)
+        add(f"cfg2_flash_L{L}_split8", 2 * L * n_kv * hd * 2 + 8 * n_head * hd,
+            lambda th, Kc=Kc, Vc=Vc, L=L: oracle.flash_reduce(
+                oracle.flash_partial_mt(q, Kc, Vc, n_head, n_kv, hd, L - 1, 8, sc, th),
+                n_head, hd, 8))
+    return rows
+
+
+def cpu_decode_step(cfg, threads, context=512, budget_s=12.0):
+    """One full config-3 decode step of the oracle on `threads` host
+    threads: for every one of the 36 layers the Q8 quantize, QKV, split-KV
+    attention over `context` positions (K/V ~ N(0,1) f16), wo, fused gate+up
+    and the Q4_K or Q6_K down, then the lm_head; distinct random weights per
+    layer (1.93 GB, as the GPU streams).  Median over as many steps as fit
+    the budget (at least 3)."""
+    import oracle
+    from taraference_amd import synth
+
+    rng = np.random.default_rng(97)
+    e, f, hd = cfg["n_embd"], cfg["n_ff"], cfg["head_dim"]
+    nh, nkv = cfg["n_head"], cfg["n_kv"]
+    nq, nk = nh * hd, nkv * hd
+    layers = []
+    for li in range(cfg["n_layer"]):
+        L = {"qkv": synth.q4k_matrix(rng, e, nq + 2 * nk), "wo": synth.q4k_matrix(rng, nq, e),
+             "g": synth.q4k_matrix(rng, e, f), "u": synth.q4k_matrix(rng, e, f)}
+        if synth.down_is_q6k(li):
+            raw, _ = synth.q6k_matrix(rng, f, e)
+            L["d6"] = synth.q6k_compact(raw, f)
+        else:
+            L["d4"] = synth.q4k_matrix(rng, f, e)
+        layers.append(L)
+    raw, _ = synth.q6k_matrix(rng, e, cfg["n_vocab"])
+    head, hcb = synth.q6k_compact(raw, e)
+    del raw
+    Kc = synth.kv_cache(rng, context, nkv, hd)
+    Vc = synth.kv_cache(rng, context, nkv, hd)
+    x0 = synth.activation(rng, e)
+    sc = float(np.float32(1 / np.sqrt(hd)))
+
+    def step():
+        x = x0
+        for L in layers:
+            qe, de = oracle.quantize_q8(x)
+            qkv = oracle.gemv_q4k_q8_mt(L["qkv"][0], qe, de, e, nq + 2 * nk, L["qkv"][1], threads)
+            part = oracle.flash_partial_mt(qkv[:nq], Kc, Vc, nh, nkv, hd, context - 1, 8, sc,
+                                           threads)
+            att = oracle.flash_reduce(part, nh, hd, 8)
+            qa, da = oracle.quantize_q8(att)
+            x = x + oracle.gemv_q4k_q8_mt(L["wo"][0], qa, da, nq, e, L["wo"][1], threads)
+            qe, de = oracle.quantize_q8(x)
+            h = oracle.gemv_q4k_ffn_mt(L["g"][0], L["u"][0], qe, de, e, f, L["g"][1], threads)
+            qh, dh = oracle.quantize_q8(h)
+            if "d6" in L:
+                y = oracle.gemv_q6k_compact_q8_kway_mt(L["d6"][0], qh, dh, f, e, L["d6"][1], 8,
+                                                       threads)
+            else:
+                y = oracle.gemv_q4k_q8_mt(L["d4"][0], qh, dh, f, e, L["d4"][1], threads)
+            x = (x + y * np.float32(1e-3)).astype(np.float32)
+        qe, de = oracle.quantize_q8(x)
+        lg = oracle.gemv_q6k_compact_q8_kway_mt(head, qe, de, e, cfg["n_vocab"], hcb, 1, threads)
+        return oracle.argmax(lg)
+
+    step()  # warm-up
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < 3 or (time.perf_counter() - t_start < budget_s and len(ts) < 20):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_baseline(cfg, budget_s=12.0, kernel_reps=20):
+    """The reference's arithmetic (the oracle) on this host: config 3's
+    whole decode step on all usable cores (tok/s = the value), plus the
+    per-kernel table at configs 0-2 single-threaded and on all cores."""
+    threads = _cpu_threads()
+    t_step, n = cpu_decode_step(cfg, threads, budget_s=budget_s)
+    table = cpu_kernel_table(threads, kernel_reps)
+    return {"value": round(1.0 / t_step, 3), "unit": "tok/s", "cores": threads,
+            "hardware_concurrency": os.cpu_count(), "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": (f"oracle (reference arithmetic in C) config-3 decode step: all "
+                       f"{cfg['n_layer']} layers (Q8 quantize, QKV, 8-split flash attention at "
+                       f"context 512, wo, gate+up+SiLU, Q4_K/Q6_K down) + lm_head + argmax on "
+                       f"{threads} threads, median of {n} steps; per-kernel table: median of "
+                       f"{kernel_reps} runs, 1 thread and {threads} threads"),
+            "step_ms": round(t_step * 1e3, 1),
+            "kernels": table,
+            "note": "baseline, not target"}
+
+
+CONTEXT = 512  # config 3: a 512-token context, then the greedy decode steps
+
+
+def _leg(name, fn):
+    """Run an optional bench leg; a failure is recorded, not raised."""
+    try:
+        return fn()
+    except Exception as exc:  # noqa: BLE001
+        log(f"[bench] {name} failed: {exc!r}")
+        return {"error": f"{type(exc).__name__}: {exc}"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=512)
+    ap.add_argument("--steps", type=int, default=256,
+                    help="timed greedy decode steps (config 3: 256)")
+    ap.add_argument("--warmup", type=int, default=16,
+                    help="untimed greedy decode steps before the timed ones (same positions)")
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--path", type=int, default=None,
                     help="decode kernel sequence (tf_model_set_path); default: the library's")
     ap.add_argument("--only-roofline", action="store_true",
                     help="run only the copy calibration and the roofline kernel (for counter runs)")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="run only the config-3 decode leg (for kernel traces and counter runs)")
     ap.add_argument("--config4", action="store_true",
                     help="BASELINE config 4 instead: Qwen2.5-7B shape, 32768-token context "
                          "filled by prefill, then 128 timed greedy tokens")
@@ -326,15 +446,25 @@ def main():
                     help="only the runtime's 512-token prefill of the 3B-shape model")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
+    ap.add_argument("--only-cpu", action="store_true",
+                    help="run only the CPU baseline (no GPU needed)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (the decode path is single-GPU; "
-              f"--gpus {args.gpus} is not supported)", file=sys.stderr)
+        print(f"bench.py measures one GPU only: every GPU box here has one GPU, so the "
+              f"decode path is built and measured single-GPU (--gpus {args.gpus} is not "
+              f"supported)", file=sys.stderr)
         sys.exit(2)
+
+    from taraference_amd import synth
+
+    if args.only_cpu:
+        print(json.dumps({"cpu_baseline": cpu_baseline(dict(synth.QWEN25_3B), args.cpu_budget)}),
+              flush=True)
+        return
 
     import torch
 
-    from taraference_amd import capi, synth
+    from taraference_amd import capi
 
     capi.load()
     if args.only_roofline:
@@ -348,7 +478,7 @@ def main():
         print(json.dumps(config4()), flush=True)
         return
     if args.q05:
-        print(json.dumps(q05_decode(args.warmup, max(2, args.steps))), flush=True)
+        print(json.dumps(q05_decode(CONTEXT, max(2, args.steps))), flush=True)
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
@@ -361,27 +491,33 @@ def main():
         return
     cfg = dict(synth.QWEN25_3B)
     steps = max(2, args.steps)
-    max_seq = args.warmup + steps + 8
+    warmup = max(0, args.warmup)
+    # the context, the warm-up steps and the timed steps (both from position
+    # CONTEXT) and the 512-token prefill leg all fit
+    max_seq = CONTEXT + max(steps, warmup) + 8
     m = build_model(cfg, 0x7A7A0003, max_seq)
     if args.path is not None:
         m.set_path(args.path)
     log("[bench] decode ...")
-    dt, toks, dt_ev = decode_throughput(m, cfg, args.warmup, steps, 3)
+    dt, toks, dt_ev = decode_throughput(m, cfg, CONTEXT, warmup, steps, 3)
     tok_s = steps / dt
-    log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    log(f"[bench] decode: {steps} tokens in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s "
+        f"(events {dt_ev * 1e3:.1f} ms)")
     wbytes = synth.weight_bytes(cfg)
     path = m.path()
-    pf = prefill_throughput(m, cfg, 512)
-    log(f"[bench] prefill: {pf}")
+    pf = None if args.only_decode else _leg("prefill", lambda: prefill_throughput(m, cfg, 512))
+    if pf is not None:
+        log(f"[bench] prefill: {pf}")
     m.close()
     del m
     torch.cuda.empty_cache()
 
     # the dominant kernel: one launch per decode step; algorithmic bytes per
     # launch = the weights once plus the K/V cache the attention reads (mean
-    # context of the timed steps); average launch duration = HIP events
-    # around the timed region on the launch stream / steps
-    ctx_mean = args.warmup + steps / 2.0
+    # context of the timed steps: positions CONTEXT .. CONTEXT+steps-1 attend
+    # over pos+1 rows); average launch duration = HIP events around the timed
+    # region on the launch stream / steps
+    ctx_mean = CONTEXT + (steps + 1) / 2.0
     kv_bytes = int(2 * cfg["n_layer"] * ctx_mean * cfg["n_kv"] * cfg["head_dim"] * 2)
     step_bytes = wbytes + kv_bytes
     us_step = dt_ev / steps * 1e6
@@ -391,44 +527,46 @@ def main():
             "traffic": DECODE_TRAFFIC if path == 4 else None,
             "kernel": DECODE_KERNEL if path == 4 else f"decode step, path {path} (several kernels)",
             "bytes_per_launch": step_bytes, "us_per_launch": round(us_step, 2)}
-    r = kernel_roofline(args.kernel_iters)
-    # average launch duration = event pair around a graph of back-to-back
-    # launches on the kernel's stream / launches
-    achieved = r["bytes"] / (r["b2b_us"] * 1e-6) / 1e9
-    roof_gemv = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                 "traffic": ROOFLINE_TRAFFIC,
-                 "kernel": ROOFLINE_KERNEL,
-                 "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
-                 "us_per_launch_single": round(r["per_us"], 3)}
-    table = {} if args.no_kernels else kernel_table(args.kernel_iters)
-    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
-
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(dt * 1e3 / steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_k/q6_k x q8 int8 dot, fp32 accumulate",
         "data": "synthetic (random-init Qwen2.5-3B-shape Q4_K_M weights, seeded)",
-        "config": {"workload": "config 3: Qwen2.5-3B-shape Q4_K_M greedy decode, batch 1",
-                   "context": args.warmup, "decode_tokens": steps,
+        "config": {"workload": "config 3: Qwen2.5-3B-shape Q4_K_M greedy decode, batch 1, "
+                               "512-token context",
+                   "context": CONTEXT, "decode_tokens": steps, "decode_path": path,
                    "weight_bytes_per_token": wbytes,
                    "effective_weight_GBs": round(wbytes * tok_s / 1e9, 1),
                    "parallelism": "single GPU"},
         "roofline": roof,
-        "roofline_q4k_gemv": roof_gemv,
-        "cpu_baseline": cpu,
-        "prefill": pf,
-        "kernels": table,
-        "greedy_tokens_head": [int(t) for t in toks[:8]],
     }
+    if not args.only_decode:
+        def gemv_roof():
+            r = kernel_roofline(args.kernel_iters)
+            # average launch duration = event pair around a graph of
+            # back-to-back launches on the kernel's stream / launches
+            achieved = r["bytes"] / (r["b2b_us"] * 1e-6) / 1e9
+            return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": ROOFLINE_TRAFFIC, "kernel": ROOFLINE_KERNEL,
+                    "bytes_per_launch": int(r["bytes"]), "us_per_launch": round(r["b2b_us"], 3),
+                    "us_per_launch_single": round(r["per_us"], 3)}
+
+        out["roofline_q4k_gemv"] = _leg("roofline_q4k_gemv", gemv_roof)
+        out["prefill"] = pf
+        out["kernels"] = {} if args.no_kernels else _leg("kernels",
+                                                         lambda: kernel_table(args.kernel_iters))
+    out["cpu_baseline"] = (None if args.no_cpu or args.only_decode
+                           else _leg("cpu_baseline", lambda: cpu_baseline(cfg, args.cpu_budget)))
+    out["greedy_tokens_head"] = [int(t) for t in toks[:8]]
     print(json.dumps(out), flush=True)
 
 

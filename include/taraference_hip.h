@@ -351,8 +351,11 @@ int tf_rope_neox(float *x, int n_heads, int head_dim, int pos,
  * f16(src[i]) with the reference's round-half-up conversion. */
 int tf_copy_kv_f16(const float *src, uint16_t *cache, int pos,
                    const int *pos_dev, int stride, tf_stream_t stream);
-/* kernels/ops.cu:573-599 argmax_f32: *out_idx = index of the largest x
- * (lowest index among exact ties). */
+/* kernels/ops.cu:573-599 argmax_f32 (one 256-thread block, layer.rs:2248-2255):
+ * *out_idx = the reference's winner.  NaN and values <= -1e30 never win
+ * (index 0 if nothing beats -1e30); among exact ties (-0 == +0) the index
+ * whose residue i mod 256, bit-reversed over 8 bits, is smallest wins, then
+ * the smallest i of that residue. */
 int tf_argmax(const float *x, int n, int *out_idx, tf_stream_t stream);
 
 /* ------------------------------------------------------ fused decode kernels */
@@ -424,7 +427,7 @@ int tf_gemv_q6k_head_argmax(const uint8_t *w, const float *x,
                             int n_rows, int n_cols, int col_bytes,
                             unsigned long long *amax_key, tf_stream_t stream);
 /* *out_idx = index of the largest key in amax_key[TF_ARGMAX_SLOTS] (largest
- * logit, lowest index among exact ties); every slot is reset to 0. */
+ * logit, ties and NaN as tf_argmax); every slot is reset to 0. */
 int tf_argmax_key_finalize(unsigned long long *amax_key, int *out_idx,
                            tf_stream_t stream);
 

@@ -387,3 +387,12 @@ def gemv_q6k_compact_q8_kway_mt(w, xq, xd, n_rows, n_cols, col_bytes, ways, nthr
     lib().or_gemv_q6k_compact_q8_kway_mt(_p(w), _p(xq), _p(xd), _p(out), n_rows, n_cols,
                                          col_bytes, ways, nthreads)
     return out
+
+
+def flash_partial_mt(q, k_cache, v_cache, n_head, n_kv, head_dim, pos0, n_split, scale,
+                     nthreads):
+    part = _f32(n_head * n_split * (2 + head_dim))
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_flash_partial_mt(_p(q), _p(k_cache), _p(v_cache), _p(part), n_head, n_kv,
+                              head_dim, pos0, n_split, C.c_float(scale), nthreads)
+    return part

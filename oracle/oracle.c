@@ -973,10 +973,23 @@ static float block_sum128(float *buf) {
     return buf[0];
 }
 
+static void flash_partial_heads(const float *q, const uint16_t *k_cache,
+                                const uint16_t *v_cache, float *partial, int n_head,
+                                int n_kv, int head_dim, int pos0, int n_split,
+                                float scale, int h0, int h1);
+
 void or_flash_partial(const float *q, const uint16_t *k_cache,
                       const uint16_t *v_cache, float *partial, int n_head,
                       int n_kv, int head_dim, int pos0, int n_split,
                       float scale) {
+    flash_partial_heads(q, k_cache, v_cache, partial, n_head, n_kv, head_dim, pos0,
+                        n_split, scale, 0, n_head);
+}
+
+static void flash_partial_heads(const float *q, const uint16_t *k_cache,
+                                const uint16_t *v_cache, float *partial, int n_head,
+                                int n_kv, int head_dim, int pos0, int n_split,
+                                float scale, int h0, int h1) {
     const int rep = n_head / n_kv;
     const int stride = n_kv * head_dim;
     const int seq_len = pos0 + 1;
@@ -984,7 +997,7 @@ void or_flash_partial(const float *q, const uint16_t *k_cache,
     float scores[OR_ATTN_TILE];
     float buf[OR_FLASH_THREADS];
     float *acc = malloc(sizeof(float) * head_dim);
-    for (int h = 0; h < n_head; h++) {
+    for (int h = h0; h < h1; h++) {
         const int kv_h = h / rep;
         const float *qh = q + (size_t)h * head_dim;
         for (int s = 0; s < n_split; s++) {
@@ -1150,22 +1163,43 @@ void or_f32_to_f16_array(const float *src, uint16_t *dst, int n) {
     for (int i = 0; i < n; i++) dst[i] = or_f32_to_f16_halfup(src[i]);
 }
 
+/* kernels/ops.cu:573-599 argmax_f32 as layer.rs:2248-2255 launches it: one
+ * block of 256 threads.  Thread t scans i = t, t+256, ... keeping the first
+ * strict maximum above -1e30 (index 0 if none); the slots then merge in the
+ * halving tree where slot t takes slot t+s only if strictly greater. */
 int or_argmax(const float *x, int n) {
-    int best = 0;
-    for (int i = 1; i < n; i++)
-        if (x[i] > x[best]) best = i;
-    return best;
+    enum { T = 256 };
+    float bv[T];
+    int bi[T];
+    for (int t = 0; t < T; t++) {
+        float best_v = -1e30f;
+        int best_i = 0;
+        for (int i = t; i < n; i += T) {
+            const float v = x[i];
+            if (v > best_v) { best_v = v; best_i = i; }
+        }
+        bv[t] = best_v;
+        bi[t] = best_i;
+    }
+    for (int s = T / 2; s > 0; s >>= 1)
+        for (int t = 0; t < s; t++)
+            if (bv[t + s] > bv[t]) { bv[t] = bv[t + s]; bi[t] = bi[t + s]; }
+    return bi[0];
 }
 
 /* ------------------------------------------------------ CPU baseline (MT) */
 
 typedef struct {
-    int kind; /* 0 q4k, 1 ffn, 2 q6 kway */
+    int kind; /* 0 q4k, 1 ffn, 2 q6 kway, 3 flash partial over heads */
     const uint8_t *w, *w2;
     const int8_t *xq;
     const float *xd;
     float *out;
     int n_rows, j0, j1, col_bytes, ways;
+    /* flash: q = (const float *)w, K/V = kc/vc, partial = out */
+    const uint16_t *kc, *vc;
+    int n_head, n_kv, head_dim, pos0, n_split;
+    float scale;
 } or_job;
 
 static void *or_worker(void *arg) {
@@ -1177,9 +1211,13 @@ static void *or_worker(void *arg) {
     } else if (jb->kind == 1) {
         ffn_cols(jb->w, jb->w2, jb->xq, jb->xd, jb->out, jb->n_rows, jb->j0, jb->j1,
                  jb->col_bytes, jb->ways);
-    } else {
+    } else if (jb->kind == 2) {
         q6_kway_cols(jb->w, jb->xq, jb->xd, jb->out, jb->n_rows, jb->j0, jb->j1,
                      jb->col_bytes, jb->ways, 0, NULL, 0, NULL);
+    } else {
+        flash_partial_heads((const float *)jb->w, jb->kc, jb->vc, jb->out, jb->n_head,
+                            jb->n_kv, jb->head_dim, jb->pos0, jb->n_split, jb->scale,
+                            jb->j0, jb->j1);
     }
     return NULL;
 }
@@ -1203,14 +1241,16 @@ static void or_run_mt(or_job proto, int n_cols, int nthreads) {
 void or_gemv_q4k_q8_mt(const uint8_t *w, const int8_t *xq, const float *xd,
                        float *out, int n_rows, int n_cols, int col_bytes,
                        int nthreads) {
-    or_job p = {0, w, NULL, xq, xd, out, n_rows, 0, 0, col_bytes, 1};
+    or_job p = {.kind = 0, .w = w, .xq = xq, .xd = xd, .out = out, .n_rows = n_rows,
+                .col_bytes = col_bytes, .ways = 1};
     or_run_mt(p, n_cols, nthreads);
 }
 
 void or_gemv_q4k_ffn_mt(const uint8_t *gate, const uint8_t *up,
                         const int8_t *xq, const float *xd, float *out,
                         int n_rows, int n_cols, int col_bytes, int nthreads) {
-    or_job p = {1, gate, up, xq, xd, out, n_rows, 0, 0, col_bytes, 1};
+    or_job p = {.kind = 1, .w = gate, .w2 = up, .xq = xq, .xd = xd, .out = out,
+                .n_rows = n_rows, .col_bytes = col_bytes, .ways = 1};
     or_run_mt(p, n_cols, nthreads);
 }
 
@@ -1218,6 +1258,18 @@ void or_gemv_q6k_compact_q8_kway_mt(const uint8_t *w, const int8_t *xq,
                                     const float *xd, float *out, int n_rows,
                                     int n_cols, int col_bytes, int ways,
                                     int nthreads) {
-    or_job p = {2, w, NULL, xq, xd, out, n_rows, 0, 0, col_bytes, ways};
+    or_job p = {.kind = 2, .w = w, .xq = xq, .xd = xd, .out = out, .n_rows = n_rows,
+                .col_bytes = col_bytes, .ways = ways};
     or_run_mt(p, n_cols, nthreads);
+}
+
+/* or_flash_partial with the query heads partitioned over threads. */
+void or_flash_partial_mt(const float *q, const uint16_t *k_cache,
+                         const uint16_t *v_cache, float *partial, int n_head,
+                         int n_kv, int head_dim, int pos0, int n_split,
+                         float scale, int nthreads) {
+    or_job p = {.kind = 3, .w = (const uint8_t *)q, .out = partial, .kc = k_cache,
+                .vc = v_cache, .n_head = n_head, .n_kv = n_kv, .head_dim = head_dim,
+                .pos0 = pos0, .n_split = n_split, .scale = scale};
+    or_run_mt(p, n_head, nthreads > n_head ? n_head : nthreads);
 }

@@ -208,6 +208,10 @@ void or_rope_neox(float *x, int n_heads, int head_dim, int pos, float theta);
 void or_f32_to_f16_array(const float *src, uint16_t *dst, int n);
 /* Largest value, lowest index among exact ties. */
 int or_argmax(const float *x, int n);
+void or_flash_partial_mt(const float *q, const uint16_t *k_cache,
+                         const uint16_t *v_cache, float *partial, int n_head,
+                         int n_kv, int head_dim, int pos0, int n_split,
+                         float scale, int nthreads);
 
 /* CPU baseline: or_gemv_q4k_q8 / or_gemv_q6k_compact_q8_kway with the
  * output columns partitioned over nthreads POSIX threads.           */

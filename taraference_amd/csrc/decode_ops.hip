@@ -8,6 +8,7 @@
 // (:471-504) and argmax_f32 (:573-599).
 #include <math.h>
 
+#include "argmax_key.hpp"
 #include "dequant.hpp"
 #include "tf_common.hpp"
 #include "tf_host.hpp"
@@ -158,44 +159,24 @@ __global__ __launch_bounds__(256) void tf_copy_kv_kernel(const float* __restrict
 
 // ------------------------------------------------------------ argmax
 
-// Index of the largest value; ties go to the lowest index.  The reference's
-// strided scan + tree (kernels/ops.cu:573-599) does not always pick the
-// lowest index among exact ties; that is the only difference.
+// argmax_f32 (kernels/ops.cu:573-599): the reference's winner, ties and
+// NaN included, through the 64-bit keys of argmax_key.hpp (every thread
+// max-merges the keys of a strided range, then the block merges).
 __global__ __launch_bounds__(1024) void tf_argmax_kernel(const float* __restrict__ x, int n,
                                                          int* __restrict__ out_idx) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
+    __shared__ unsigned long long part[16];
+    unsigned long long best = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
-        if (v > best) {
-            best = v;
-            idx = i;
-        }
+        const unsigned long long k = tf_argmax_key(x[i], i);
+        best = k > best ? k : best;
     }
-    for (int off = 1; off < 64; off <<= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
-    }
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = best;
-        bi[threadIdx.x >> 6] = idx;
-    }
+    best = tf_wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        float b = bv[0];
-        int k = bi[0];
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
-            if (bv[w] > b || (bv[w] == b && bi[w] < k)) {
-                b = bv[w];
-                k = bi[w];
-            }
-        out_idx[0] = k == 0x7fffffff ? 0 : k;
+        best = part[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = part[w] > best ? part[w] : best;
+        out_idx[0] = tf_argmax_key_index(best);
     }
 }
 

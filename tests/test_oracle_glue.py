@@ -159,10 +159,98 @@ def test_embed_row_matches_numpy_dequant(kind):
 
 # ------------------------------------------------------------------ argmax
 
-def test_argmax_lowest_index_on_ties():
+def _argmax_sim(x, threads=256):
+    """Brute-force simulation of argmax_f32 (kernels/ops.cu:573-599) as one
+    block of `threads` threads: each thread's strided strict-> scan from
+    -1e30, then the halving tree in which slot t takes slot t+s only when
+    strictly greater (Python floats; the comparisons are the same in fp32)."""
+    slots = []
+    for t in range(threads):
+        bv, bi = -1e30, 0
+        for i in range(t, len(x), threads):
+            v = float(x[i])
+            if v > bv:
+                bv, bi = v, i
+        slots.append((bv, bi))
+
+    n = threads
+    cur = list(slots)
+    s = n // 2
+    while s > 0:
+        nxt = list(cur)
+        for t in range(s):
+            if cur[t + s][0] > cur[t][0]:
+                nxt[t] = cur[t + s]
+        cur = nxt
+        s //= 2
+    return cur[0][1]
+
+
+def _argmax_rule(x):
+    """The closed-form winner: among finite-or-inf values above -1e30 with
+    the maximal value, the smallest 8-bit bit-reversed residue i mod 256,
+    then the smallest i; index 0 when no value beats -1e30."""
+    x = np.asarray(x, np.float32)
+    ok = np.where(x > np.float32(-1e30))[0]
+    if ok.size == 0:
+        return 0
+    m = x[ok].max()
+    cand = ok[x[ok] == m]
+    rev = [int(f"{int(i) & 255:08b}"[::-1], 2) for i in cand]
+    return int(min(zip(rev, cand.tolist()))[1])
+
+
+def test_argmax_reference_tie_rule_small():
+    # hand cases from the tree's tie order
+    for ties, want in (((1, 2), 2), ((10, 260), 260), ((64, 128), 128), ((0, 128), 0),
+                       ((3, 259), 3), ((5, 7), 5), ((255, 511), 255), ((6, 1), 6)):
+        x = np.zeros(600, np.float32) - 1
+        for i in ties:
+            x[i] = 7.0
+        assert _argmax_sim(x) == want, ties
+        assert oracle.argmax(x) == want, ties
+        assert _argmax_rule(x) == want, ties
+
+
+def test_argmax_reference_edges():
+    # nothing above -1e30 -> 0; NaN and -inf never win; -0 ties with +0
+    assert oracle.argmax(np.full(1000, -3e30, np.float32)) == 0
+    assert oracle.argmax(np.full(1000, -1e30, np.float32)) == 0
+    x = np.full(1000, np.nan, np.float32)
+    x[700] = -5.0
+    assert oracle.argmax(x) == 700
+    x = np.full(1000, -np.inf, np.float32)
+    assert oracle.argmax(x) == 0
+    x = np.full(300, -1.0, np.float32)
+    x[1], x[2] = np.float32(-0.0), np.float32(0.0)
+    assert oracle.argmax(x) == _argmax_sim(x) == 2
+    x[1], x[2] = np.float32(0.0), np.float32(-0.0)
+    assert oracle.argmax(x) == 2
+    x = np.full(10, -2.0, np.float32)
+    x[9] = np.inf
+    assert oracle.argmax(x) == 9
+    assert oracle.argmax(np.array([3.0], np.float32)) == 0
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_argmax_against_simulation(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 3000))
+    # few distinct values so ties across residues are common
+    x = rng.integers(-4, 4, n).astype(np.float32)
+    if seed % 2:
+        x[rng.integers(0, n, n // 7)] = np.nan
+    if seed == 5:
+        x[:] = -1e31
+        x[rng.integers(0, n, 3)] = -1e30
+    want = _argmax_sim(x)
+    assert oracle.argmax(x) == want
+    assert _argmax_rule(x) == want
+
+
+def test_argmax_vocab_random():
     rng = np.random.default_rng(4)
     x = rng.standard_normal(151936).astype(np.float32)
-    assert oracle.argmax(x) == int(np.argmax(x))
-    x[100] = x[90000] = np.float32(50.0)
-    assert oracle.argmax(x) == 100
-    assert oracle.argmax(np.full(1000, -3.0, np.float32)) == 0
+    assert oracle.argmax(x) == int(np.argmax(x))  # distinct values: the plain argmax
+    x[100] = x[90000] = np.float32(50.0)  # residues 100 (rev 38) and 144 (rev 9)
+    assert oracle.argmax(x) == 90000 == _argmax_rule(x)
