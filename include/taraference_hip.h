@@ -525,6 +525,21 @@ int tf_model_get_path(const tf_model *m);
 /* Device pointer of the last logits (n_vocab floats) and of the f16 K/V
  * cache of layer li. */
 const float *tf_model_logits(const tf_model *m);
+/* Inspection of the persistent step (path 4); no counterpart in the
+ * reference.  on != 0 before the first path-4 step makes the step keep one
+ * copy of every stage vector per layer instead of two alternating ones
+ * (hipErrorNotSupported once the step's buffers exist with the other
+ * setting).  tf_model_stage_vector then returns layer li's vector of `kind`
+ * after a step, as 64-bit words whose low half is the value bits and high
+ * half a tag: 0 = residual after the attention output projection (f32,
+ * n_embd words), 1 = residual after the FFN down projection (f32, n_embd),
+ * 2 = roped query (f32, n_head*head_dim), 4 = attention output and
+ * 5 = silu(gate)*up, both as Q8 in groups of 9 words per 32 values (8
+ * words of four int8 in value order, then the f32 scale).  NULL when not
+ * kept. */
+int tf_model_keep_stage_vectors(tf_model *m, int on);
+const unsigned long long *tf_model_stage_vector(const tf_model *m, int kind,
+                                                int li);
 uint16_t *tf_model_k_cache(const tf_model *m, int li);
 uint16_t *tf_model_v_cache(const tf_model *m, int li);
 

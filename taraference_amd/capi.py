@@ -127,7 +127,8 @@ def stream_ptr(stream=None) -> int | None:
 # Entry points bound elsewhere with their own argtypes (taraference_amd/model.py).
 BOUND_ELSEWHERE = {"tf_model_create", "tf_model_destroy", "tf_model_forward",
                    "tf_model_generate", "tf_model_set_path", "tf_model_get_path",
-                   "tf_model_logits", "tf_model_prefill",
+                   "tf_model_logits", "tf_model_prefill", "tf_model_keep_stage_vectors",
+                   "tf_model_stage_vector",
                    "tf_model_k_cache", "tf_model_v_cache", "tf_exported_symbol",
                    # taraference_amd/gguf.py
                    "tf_gguf_open", "tf_gguf_close", "tf_gguf_version", "tf_gguf_data_offset",

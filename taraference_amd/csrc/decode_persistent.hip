@@ -1704,10 +1704,11 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
 // launch was aborted.
 
 __device__ __forceinline__ unsigned long long* tf_p_vec(TfPA& a, int kind, int li) {
-    const int par = li & 1;
+    const int nbuf = a.nbuf;
+    const int par = nbuf == 2 ? (li & 1) : li;
     switch (kind) {
     case TF_PK_XA: return a.fx + (size_t)par * a.E;
-    case TF_PK_XB: return a.fx + (size_t)(2 + par) * a.E;
+    case TF_PK_XB: return a.fx + (size_t)(nbuf + par) * a.E;
     case TF_PK_Q: return a.fq + (size_t)par * a.H * a.HD;
     case TF_PK_KV: return a.fkv + (size_t)par * 2 * a.KV * a.HD;
     case TF_PK_O: return a.fo + (size_t)par * a.H * a.HD;

@@ -51,7 +51,11 @@ struct TfPArgs {
     // after down: parity 0, 1), fq [2][H * HD] roped query, fkv [2][KV][2][HD]
     // the new K and V rows (f16 bits), fo [2][H * HD] attention output,
     // fh [2][F] silu(gate) * up.
+    // nbuf = 2 double-buffers them by layer parity; nbuf = n_layer keeps
+    // one copy per layer (fx [2][n_layer][E]: after wo, then after down),
+    // so every layer's vectors can be read back after the step.
     unsigned long long *fx, *fq, *fkv, *fo, *fh;
+    int nbuf;
     float* logits;  // [n_vocab]
     // split-KV partials (m, l, O[HD]) as tagged words [KV][G][TF_P_MAX_SPLIT][2 + HD]
     unsigned long long* fpart;

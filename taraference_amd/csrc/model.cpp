@@ -119,6 +119,7 @@ struct tf_model {
     unsigned long long* p_part = nullptr;
     size_t p_part_words = 0;
     unsigned long long* p_flags = nullptr;  // the flagged stage vectors
+    bool p_keep = false;  // one copy of them per layer (tf_model_keep_stage_vectors)
     size_t p_flag_words = 0;
     // diagnostic stage timeline of the persistent step: when the environment
     // names a file in TF_P_TRACE, the last step of each run() is written there
@@ -438,9 +439,10 @@ struct tf_model {
                                  hipMemcpyHostToDevice), "copy layer table");
         d_bar = alloc<unsigned>(TF_BAR_WORDS);
         d_perr = alloc<int>(1);
-        p_flag_words = (size_t)4 * c.n_embd + 2 * (size_t)c.n_head * c.head_dim +
-                       4 * (size_t)c.n_kv * c.head_dim + 2 * (size_t)c.n_head * c.head_dim +
-                       2 * (size_t)c.n_ff;
+        const size_t nb = p_keep ? (size_t)c.n_layer : 2;
+        p_flag_words = nb * (2 * (size_t)c.n_embd + (size_t)c.n_head * c.head_dim +
+                             2 * (size_t)c.n_kv * c.head_dim + (size_t)c.n_head * c.head_dim +
+                             (size_t)c.n_ff);
         p_flags = alloc<unsigned long long>(p_flag_words);
         p_part_words = (size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim);
         p_part = alloc<unsigned long long>(p_part_words);
@@ -503,11 +505,13 @@ struct tf_model {
         a.head_cb = (int)output.compact_col_bytes;
         a.n_vocab = (int)output.n_cols;
         a.out_norm = output_norm;
+        const size_t nb = p_keep ? (size_t)c.n_layer : 2;
+        a.nbuf = (int)nb;
         a.fx = p_flags;
-        a.fq = a.fx + 4 * (size_t)c.n_embd;
-        a.fkv = a.fq + 2 * (size_t)c.n_head * c.head_dim;
-        a.fo = a.fkv + 4 * (size_t)c.n_kv * c.head_dim;
-        a.fh = a.fo + 2 * (size_t)c.n_head * c.head_dim;
+        a.fq = a.fx + 2 * nb * c.n_embd;
+        a.fkv = a.fq + nb * c.n_head * c.head_dim;
+        a.fo = a.fkv + 2 * nb * c.n_kv * c.head_dim;
+        a.fh = a.fo + nb * c.n_head * c.head_dim;
         a.logits = logits;
         a.fpart = p_part;
         a.amax = d_amax_key;
@@ -862,6 +866,27 @@ extern "C" int tf_model_set_path(tf_model* m, int path) {
         m->graph = nullptr;
     }
     return 0;
+}
+
+extern "C" int tf_model_keep_stage_vectors(tf_model* m, int on) {
+    if (!m) return (int)hipErrorInvalidValue;
+    if (m->d_players && m->p_keep != (on != 0)) return (int)hipErrorNotSupported;
+    if (on && m->cfg.n_layer < 2) return (int)hipErrorInvalidValue;
+    m->p_keep = on != 0;
+    return 0;
+}
+
+extern "C" const unsigned long long* tf_model_stage_vector(const tf_model* m, int kind, int li) {
+    if (!m || !m->p_keep || !m->d_players || li < 0 || li >= m->cfg.n_layer) return nullptr;
+    const TfPArgs& a = m->pargs;
+    switch (kind) {
+    case 0: return a.fx + (size_t)li * a.E;                 // residual after wo, f32
+    case 1: return a.fx + (size_t)(a.nbuf + li) * a.E;      // residual after down, f32
+    case 2: return a.fq + (size_t)li * a.H * a.HD;          // roped query, f32
+    case 4: return a.fo + (size_t)li * a.H * a.HD;          // attention output, Q8 groups
+    case 5: return a.fh + (size_t)li * a.F;                 // silu(gate)*up, Q8 groups
+    default: return nullptr;
+    }
 }
 
 extern "C" const float* tf_model_logits(const tf_model* m) { return m ? m->logits : nullptr; }

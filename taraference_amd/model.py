@@ -58,6 +58,10 @@ def _bind(lib):
     lib.tf_model_set_path.restype = C.c_int
     lib.tf_model_get_path.argtypes = [C.c_void_p]
     lib.tf_model_get_path.restype = C.c_int
+    lib.tf_model_keep_stage_vectors.argtypes = [C.c_void_p, C.c_int]
+    lib.tf_model_keep_stage_vectors.restype = C.c_int
+    lib.tf_model_stage_vector.argtypes = [C.c_void_p, C.c_int, C.c_int]
+    lib.tf_model_stage_vector.restype = C.c_void_p
     lib.tf_model_logits.argtypes = [C.c_void_p]
     lib.tf_model_logits.restype = C.c_void_p
     for n in ("tf_model_k_cache", "tf_model_v_cache"):
@@ -260,6 +264,39 @@ class DecodeModel:
         torch.cuda.synchronize()
         capi.memcpy_d2h(out, self.lib.tf_model_logits(self.h))
         return out
+
+    def keep_stage_vectors(self, on: bool = True) -> None:
+        """Make the persistent step (path 4) keep every layer's stage vectors
+        for stage_vector(); call before the first path-4 step."""
+        rc = self.lib.tf_model_keep_stage_vectors(self.h, int(on))
+        if rc != 0:
+            raise capi.HipError(f"tf_model_keep_stage_vectors returned {rc}")
+
+    STAGE_XA, STAGE_XB, STAGE_Q, STAGE_O, STAGE_H = 0, 1, 2, 4, 5
+
+    def stage_vector(self, kind: int, layer: int):
+        """Layer `layer`'s stage vector from the last persistent step: f32
+        values for STAGE_XA / STAGE_XB / STAGE_Q; (int8 q[n], f32 d[n/32])
+        for the Q8 vectors STAGE_O (attention output) and STAGE_H
+        (silu(gate)*up).  Also returns the tags (high word halves)."""
+        c = self.cfg
+        n = {0: c["n_embd"], 1: c["n_embd"], 2: c["n_head"] * c["head_dim"],
+             4: c["n_head"] * c["head_dim"], 5: c["n_ff"]}[kind]
+        words = n if kind in (0, 1, 2) else n // 32 * 9
+        p = self.lib.tf_model_stage_vector(self.h, kind, layer)
+        if not p:
+            raise capi.HipError("stage vectors are not kept (keep_stage_vectors before the step)")
+        w = np.empty(words, np.uint64)
+        torch.cuda.synchronize()
+        capi.memcpy_d2h(w, p)
+        lo = (w & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        tags = (w >> np.uint64(32)).astype(np.uint32)
+        if kind in (0, 1, 2):
+            return lo.view(np.float32), tags
+        g = lo.reshape(-1, 9)
+        q = np.ascontiguousarray(g[:, :8]).view(np.int8).reshape(-1)
+        d = np.ascontiguousarray(g[:, 8]).view(np.float32)
+        return (q, d), tags
 
     def kv_cache(self, layer: int, seq: int):
         """(K, V) f16 bits [seq, n_kv*head_dim] of one layer, copied to the host."""

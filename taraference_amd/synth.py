@@ -73,17 +73,47 @@ def q6k_blocks(rng: np.random.Generator, n: int) -> np.ndarray:
     return blk
 
 
-def q4k_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
-    """Q4_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*144."""
+def q4k_blocks_wc(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n well-conditioned Q4_K super-blocks: d ~ U[1e-4, 4e-4], sc ~ U{0..33},
+    m = round(1.875 sc), dmin = 4 d, so each 32-value sub-block's mean
+    d sc 7.5 - dmin m is about 0 and a weight's spread is about 0.02: a
+    2048-wide GEMV of an RMS-1 input gives outputs of RMS about 1."""
+    blk = np.empty((n, Q4K_BYTES), np.uint8)
+    d = rng.uniform(1e-4, 4e-4, n).astype(np.float16)
+    dmin = (d.astype(np.float32) * 4).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(n, 2)
+    sc = rng.integers(0, 34, (n, 8), dtype=np.uint8)
+    m = np.rint(sc * 1.875).astype(np.uint8)
+    blk[:, 4:16] = pack_q4k_scales(sc, m)
+    blk[:, 16:] = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+    return blk
+
+
+def q6k_blocks_wc(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n well-conditioned Q6_K super-blocks: scales ~ U[-8, 7], d ~ U[1e-4,
+    4e-4] (weights of spread about 0.02)."""
+    blk = np.empty((n, Q6K_BYTES), np.uint8)
+    blk[:, 0:192] = rng.integers(0, 256, (n, 192), dtype=np.uint8)
+    blk[:, 192:208] = rng.integers(-8, 8, (n, 16), dtype=np.int8).view(np.uint8)
+    d = rng.uniform(1e-4, 4e-4, n).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(n, 2)
+    return blk
+
+
+def q4k_matrix(rng, n_rows: int, n_cols: int, wc: bool = False) -> tuple[np.ndarray, int]:
+    """Q4_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*144
+    (wc: the well-conditioned distribution of q4k_blocks_wc)."""
     nb = (n_rows + 255) // 256
-    w = q4k_blocks(rng, n_cols * nb).reshape(n_cols, nb * Q4K_BYTES)
+    w = (q4k_blocks_wc if wc else q4k_blocks)(rng, n_cols * nb).reshape(n_cols, nb * Q4K_BYTES)
     return np.ascontiguousarray(w), nb * Q4K_BYTES
 
 
-def q6k_matrix(rng, n_rows: int, n_cols: int) -> tuple[np.ndarray, int]:
-    """Raw Q6_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*210."""
+def q6k_matrix(rng, n_rows: int, n_cols: int, wc: bool = False) -> tuple[np.ndarray, int]:
+    """Raw Q6_K matrix [n_cols, col_bytes]; col_bytes = ceil(n_rows/256)*210
+    (wc: the well-conditioned distribution of q6k_blocks_wc)."""
     nb = (n_rows + 255) // 256
-    w = q6k_blocks(rng, n_cols * nb).reshape(n_cols, nb * Q6K_BYTES)
+    w = (q6k_blocks_wc if wc else q6k_blocks)(rng, n_cols * nb).reshape(n_cols, nb * Q6K_BYTES)
     return np.ascontiguousarray(w), nb * Q6K_BYTES
 
 
@@ -161,33 +191,35 @@ def down_is_q6k(layer: int) -> bool:
     return layer % 2 == 1
 
 
-def qwen_layer(rng, cfg: dict, layer: int) -> dict:
+def qwen_layer(rng, cfg: dict, layer: int, wc: bool = False) -> dict:
     """Random-init weights of one dense Qwen2 layer in the Q4_K_M mix:
     Q4_K for q/k/o/gate/up, Q6_K for v, Q6_K or Q4_K for down; norms = 1,
-    q/k/v biases ~ N(0, 0.02)."""
+    q/k/v biases ~ N(0, 0.02).  wc: well-conditioned blocks (activations,
+    attention scores and logits of order 1, so the softmax is not one-hot)
+    instead of the benchmark's block distribution."""
     e, f = cfg["n_embd"], cfg["n_ff"]
     nq = cfg["n_head"] * cfg["head_dim"]
     nkv = cfg["n_kv"] * cfg["head_dim"]
     L = {}
     L["attn_norm"] = np.ones(e, np.float32)
     L["ffn_norm"] = np.ones(e, np.float32)
-    L["wq"] = q4k_matrix(rng, e, nq)
-    L["wk"] = q4k_matrix(rng, e, nkv)
-    L["wv"] = q6k_matrix(rng, e, nkv)
+    L["wq"] = q4k_matrix(rng, e, nq, wc)
+    L["wk"] = q4k_matrix(rng, e, nkv, wc)
+    L["wv"] = q6k_matrix(rng, e, nkv, wc)
     L["bq"] = (rng.standard_normal(nq) * 0.02).astype(np.float32)
     L["bk"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
     L["bv"] = (rng.standard_normal(nkv) * 0.02).astype(np.float32)
-    L["wo"] = q4k_matrix(rng, nq, e)
-    L["gate"] = q4k_matrix(rng, e, f)
-    L["up"] = q4k_matrix(rng, e, f)
-    L["down"] = q6k_matrix(rng, f, e) if down_is_q6k(layer) else q4k_matrix(rng, f, e)
+    L["wo"] = q4k_matrix(rng, nq, e, wc)
+    L["gate"] = q4k_matrix(rng, e, f, wc)
+    L["up"] = q4k_matrix(rng, e, f, wc)
+    L["down"] = q6k_matrix(rng, f, e, wc) if down_is_q6k(layer) else q4k_matrix(rng, f, e, wc)
     L["down_q6k"] = down_is_q6k(layer)
     return L
 
 
-def qwen_embedding(rng, cfg: dict):
+def qwen_embedding(rng, cfg: dict, wc: bool = False):
     """Tied token embedding / lm_head: Q6_K [n_vocab, n_embd]."""
-    return q6k_matrix(rng, cfg["n_embd"], cfg["n_vocab"])
+    return q6k_matrix(rng, cfg["n_embd"], cfg["n_vocab"], wc)
 
 
 def weight_bytes(cfg: dict) -> int:
