@@ -324,6 +324,18 @@ int tf_gemv_q4k_flash_out(const uint8_t *w, const float *partial, int n_head,
                           int head_dim, int n_split, float *out, int n_cols,
                           int col_bytes, int use_res, float *attn_out,
                           int8_t *attn_q8, float *attn_d8, tf_stream_t stream);
+/* No counterpart in the reference: tf_flash_decode for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split partials and merge
+ * counters live in a static device array of this library (one per GPU,
+ * held until the process ends): n_head * n_split * (2 + head_dim) <= 2^20
+ * floats and n_kv <= 256, else hipErrorInvalidValue.  Allocates nothing.
+ * Calls that overlap on one GPU share that array and race. */
+int tf_flash_decode_noalloc(const float *q, const uint16_t *k_cache,
+                            const uint16_t *v_cache, float *out, int8_t *q8,
+                            float *d8, int n_head, int n_kv, int head_dim,
+                            int pos0, const int *pos0_dev, int n_split,
+                            float scale, tf_stream_t stream);
 /* Partition count this library recommends for a context of max_seq tokens
  * (a multiple of 8; 8 for short contexts).  The reference fixes 8
  * (cuda/decode.rs:38-41); on MI355X long contexts need more partitions to

@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
     "tf_flash_decode_n_split": [_I, _I],
     "tf_gemv_q4k_flash_out": [_P, _P, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P],
     "tf_flash_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _F, _P],
+    "tf_flash_decode_noalloc": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _F, _P],
     "tf_gemv_q4k_f32": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P],
     "tf_gemv_q4k_ffn_norm": [_P, _P, _P, _P, _F, _P, _I, _I, _I, _P],
     "tf_fused_norm_qkv_rope_kv": [_P, _P, _F, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,

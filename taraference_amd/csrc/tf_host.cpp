@@ -119,6 +119,7 @@ static const char* const k_symbols[] = {
     "tf_norm_quant",
     "tf_flash_decode_reduce_q8",
     "tf_flash_decode",
+    "tf_flash_decode_noalloc",
     "tf_gemv_q4k_flash_out",
     "tf_gemv_q6k_q8_argmax",
     "tf_gemv_q4k_ffn_norm",
