@@ -299,14 +299,13 @@ int tf_flash_decode_reduce(const float *partial, float *out, int n_head,
                            int head_dim, int n_split, int n_q,
                            tf_stream_t stream);
 
-/* kernels/attn/flash.cu:16/:119 + :222 in one launch (layer.rs:2040-2121):
- * split-KV partials, then the log-sum-exp merge done by the last workgroup
- * of each kv head to finish; when q8/d8 are non-NULL the merged output is
- * also quantized to Q8 (quantize_q8 of the wo GEMV input, matmul.rs:191).
- * pos0_dev non-NULL reads the position from device memory (graph capture).
- * counters: n_kv unsigned ints, zero before the first call; every call
- * leaves them zero.  partial as for tf_flash_decode_partial.  For
- * n_split > 64 the merge runs as a second kernel. */
+/* kernels/attn/flash.cu:16/:119 + :222 as one call (layer.rs:2040-2121):
+ * split-KV partials, then the log-sum-exp merge (a second kernel); when
+ * q8/d8 are non-NULL the merged output is also quantized to Q8 (quantize_q8
+ * of the wo GEMV input, matmul.rs:191).  pos0_dev non-NULL reads the position
+ * from device memory (graph capture).  counters: n_kv unsigned ints, zero
+ * before the first call; every call leaves them zero.  partial as for
+ * tf_flash_decode_partial. */
 int tf_flash_decode(const float *q, const uint16_t *k_cache,
                     const uint16_t *v_cache, float *partial, unsigned *counters,
                     float *out, int8_t *q8, float *d8, int n_head, int n_kv,
