@@ -195,7 +195,8 @@ def copy_calibration(n_bytes=256 << 20, reps=3):
     return n_bytes
 
 
-def kernel_table(iters):
+def kernel_table(iters, only=None):
+    """Per-kernel GPU table; `only` keeps the rows whose name contains it."""
     from taraference_amd import benchkit as B
 
     rows = [
@@ -223,6 +224,8 @@ def kernel_table(iters):
         rows.append((f"cfg2_flash_L{L}_auto", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters)))
     out = {}
     for name, fn in rows:
+        if only and only not in name:
+            continue
         r = B.report(name, fn())
         out[name] = {"us": round(r["per_us"], 2), "us_b2b": round(r["b2b_us"], 2),
                      "MB": round(r["bytes"] / 1e6, 3), "GBs": round(r["gbs"], 1),
@@ -445,6 +448,8 @@ def main():
                          "path 0), 512-token context, 256 timed greedy tokens")
     ap.add_argument("--only-prefill", action="store_true",
                     help="only the runtime's 512-token prefill of the 3B-shape model")
+    ap.add_argument("--kernel-filter", default=None,
+                    help="with --only-kernels: rows whose name contains this text")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     ap.add_argument("--only-cpu", action="store_true",
@@ -482,7 +487,8 @@ def main():
         print(json.dumps(q05_decode(CONTEXT, max(2, args.steps))), flush=True)
         return
     if args.only_kernels:
-        print(json.dumps({"kernels": kernel_table(args.kernel_iters)}), flush=True)
+        print(json.dumps({"kernels": kernel_table(args.kernel_iters, args.kernel_filter)}),
+              flush=True)
         return
     if args.only_prefill:
         cfg = dict(synth.QWEN25_3B)
