@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "argmax_key.hpp"
+#include "lds_dma.hpp"
 #include "decode_persistent.hpp"
 #include "dequant.hpp"
 #include "q4k.hpp"
@@ -1301,21 +1302,247 @@ __device__ __forceinline__ unsigned long long* tf_p_part(TfPA& a, int kh, int g,
 }
 
 // Long contexts (one head group: all G <= 8 query heads of the kv head in
-// one workgroup, one wave per head) run the tile on the matrix cores, as
-// tf_flash_partial_mfma_kernel: S[16][64] = Q K^T by waves 0-3 (16 tokens
-// each; q split into three f16 parts after a power-of-two scale, K f16),
-// the softmax from DPP row reductions of the MFMA layout plus four per-wave
-// values through LDS, O[16][128] += P V by the eight waves (16 dims each;
-// p split into two f16 parts).  Every lane keeps (m, l) of heads
-// 4g .. 4g+3 (g = lane / 16).  After the tiles, O, m and l of head h go
-// through LDS to wave h, which then publishes them as the vector-ALU path
-// does.
-typedef _Float16 tf_p_h16x4 __attribute__((ext_vector_type(4)));
+// one workgroup) run the split as tf_flash_partial_dma_kernel does: each of
+// the 8 waves owns the 16-token tiles j = wave, wave + 8, ... of the split
+// and copies them HBM -> LDS itself (global_load_lds_dwordx4) into a private
+// two-slot ring, one tile computing while the next is in flight; the first
+// two tiles are issued before the q poll.  Per tile, on
+// v_mfma_f32_16x16x32_f16 with the query heads padded to 16 (lane l, n =
+// l % 16, g = l / 16): S^T[token][head] = K Q^T (q in two f16 parts after
+// a power-of-two scale, K f16), the online softmax of head n from a lane max
+// and two xor-shuffles, O^T[dim][head] += V^T P^T with p's hi and lo parts
+// in one k = 32 step.  The row `pos`, produced in this launch, is patched
+// into its LDS slot from the polled K/V row once the slot has landed.  The
+// eight waves' (m, l, O) are then combined through LDS and wave h takes
+// head h's values in the vector-ALU lane layout, so publication and the
+// split merge are unchanged.  LDS rows: a K row's 16-byte chunk c sits at
+// chunk c ^ (row % 16); V rows go in blocks of four with 32 bytes of
+// padding (both read patterns bank-conflict free).
+struct TfPDmaLayout {
+    static constexpr int VBLK = 1056;                  // 4 V rows + 32 bytes
+    static constexpr int SLOT = 4096 + 4 * VBLK;       // 16 K rows + 16 V rows
+    static constexpr int WAVE = 2 * SLOT;              // two-slot ring of a wave
+    static constexpr int Q = TF_P_WAVES * WAVE;        // q [G][HD] f32
+    static constexpr int BYTES = Q + 16 * TF_P_HD * 4;
+    static constexpr int CR = 2 + TF_P_HD + 2;         // combine row: m, l, pad, O
+    static constexpr int OL = 69632;                   // merged (O [8][HD], (m, l) [8])
+    static_assert(TF_P_WAVES * 16 * CR * 4 <= OL, "combine area");
+    static_assert(OL + (8 * TF_P_HD + 16) * 4 <= Q, "merged area");
+};
 typedef float tf_p_f32x4 __attribute__((ext_vector_type(4)));
-#define TF_P_SROW 68  // floats per weight row in LDS (64 tokens + 4)
 
-__device__ __forceinline__ tf_p_f32x4 tf_p_mfma16(tf_p_h16x4 a, tf_p_h16x4 b, tf_p_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+// 16-token tile j of the split -> slot b of this wave's ring: four copies of
+// 4 K rows, then four of 4 V rows; rows past the split repeat its last token
+// (their scores are masked).
+__device__ __forceinline__ void tf_p_attn_dma_tile(TfPL& L, const TfPAttnGeo& g, int stride,
+                                                   uint8_t* lds, int j, int b) {
+    const int lane = tf_p_tid() & 63, wave = tf_p_tid() >> 6;
+    const int n = lane & 15, r4 = lane >> 4;
+    const uint16_t* kb = L.k_cache + (size_t)g.kh * TF_P_HD;
+    const uint16_t* vb = L.v_cache + (size_t)g.kh * TF_P_HD;
+    const int t0 = g.t_begin + 16 * j;
+    const uint32_t base = tf_lds_off(lds) + wave * TfPDmaLayout::WAVE + b * TfPDmaLayout::SLOT;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * i + r4;
+        const int t = min(t0 + r, g.t_end - 1);
+        tf_lds_dma16(kb + (size_t)t * stride + 8 * (n ^ r), base + 1024 * i);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = min(t0 + 4 * i + r4, g.t_end - 1);
+        tf_lds_dma16(vb + (size_t)t * stride + 8 * n, base + 4096 + TfPDmaLayout::VBLK * i);
+    }
+}
+
+// The wave's first two tiles (before the q poll).
+__device__ __forceinline__ void tf_p_attn_dma_prime(TfPL& L, const TfPAttnGeo& g, int stride,
+                                                    uint8_t* lds) {
+    const int wave = tf_p_tid() >> 6;
+    const int n16 = (g.t_end - g.t_begin + 15) / 16;
+    if (wave < n16) tf_p_attn_dma_tile(L, g, stride, lds, wave, 0);
+    if (wave + TF_P_WAVES < n16) tf_p_attn_dma_tile(L, g, stride, lds, wave + TF_P_WAVES, 1);
+}
+
+// The split's tiles after the q poll; leaves head hd's (m, l) and O dims
+// 2 lane, 2 lane + 1 in m, l, o0, o1 of wave hd (valid).
+__device__ __forceinline__ void tf_p_attn_dma_run(TfPA& a, TfPL& L, const TfPAttnGeo& g,
+                                                  int pos, int stride, uint8_t* lds,
+                                                  const float* q_lds, bool valid, int hd,
+                                                  float& m_out, float& l_out, float& o0,
+                                                  float& o1) {
+    using DL = TfPDmaLayout;
+    constexpr int HD = TF_P_HD;
+    const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, gg = lane >> 4;
+    const int G = a.H / a.KV;
+    const int n16 = (g.t_end - g.t_begin + 15) / 16;
+    uint8_t* ring = lds + wave * DL::WAVE;
+
+    // q of head n, dims 32 gg + 8 jj .. +7 (the dim order of the K reads), in
+    // two f16 parts of q 2^-e: the largest |q| of the group lands in
+    // [2^14, 2^15), the residual of every element within 2^-25 of it
+    tf_h16x8 qa[4][2];
+    float sc;
+    {
+        float qv[4][8];
+        float qmax = 0.f;
+        const bool hv = n < G;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int h2 = 0; h2 < 2; h2++) {
+                float4 v = hv ? *reinterpret_cast<const float4*>(q_lds + n * HD + 32 * gg + 8 * jj + 4 * h2)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+                qv[jj][4 * h2 + 0] = v.x;
+                qv[jj][4 * h2 + 1] = v.y;
+                qv[jj][4 * h2 + 2] = v.z;
+                qv[jj][4 * h2 + 3] = v.w;
+                qmax = fmaxf(qmax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        qmax = tf_wave_max(qmax);
+        const int e = qmax > 0.f ? ilogbf(qmax) - 14 : 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = ldexpf(qv[jj][i], -e);
+                const _Float16 p0 = (_Float16)x;
+                qa[jj][0][i] = p0;
+                qa[jj][1][i] = (_Float16)(x - (float)p0);
+            }
+        sc = ldexpf(a.scale, e);
+    }
+    uint32_t koff[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) koff[jj] = n * 256 + 16 * ((4 * gg + jj) ^ n);
+    const uint32_t voff = 4096 + gg * DL::VBLK + 2 * n;
+
+    float m = TF_P_NEG_BIG, l = 0.f;  // head n: running max, this lane's share of the sum
+    tf_p_f32x4 o[8];                  // O^T of dims 16 db + 4 gg + r, head n
+#pragma unroll
+    for (int db = 0; db < 8; db++) o[db] = tf_p_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0, j = wave; j < n16; k++, j += TF_P_WAVES) {
+        if (j + TF_P_WAVES < n16)
+            asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // the next tile stays in flight
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint8_t* slot = ring + (k & 1) * DL::SLOT;
+        const int t0 = g.t_begin + 16 * j;
+        if (pos >= t0 && pos < t0 + 16) {  // wave-uniform: patch the row produced in this launch
+            const int rr = pos - t0;
+            if (lane < 16) {
+                *reinterpret_cast<tf_u32x4*>(slot + rr * 256 + 16 * (lane ^ rr)) =
+                    *reinterpret_cast<const tf_u32x4*>(tf_p_knew + 8 * lane);
+                *reinterpret_cast<tf_u32x4*>(slot + 4096 + (rr >> 2) * DL::VBLK + (rr & 3) * 256 +
+                                             16 * lane) =
+                    *reinterpret_cast<const tf_u32x4*>(tf_p_vnew + 8 * lane);
+            }
+        }
+        // ---- scores of tokens t0 + 4 gg + r, head n
+        float sv[4];
+        {
+            tf_h16x8 kf[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) kf[jj] = *reinterpret_cast<const tf_h16x8*>(slot + koff[jj]);
+            tf_p_f32x4 c0 = tf_p_f32x4{0.f, 0.f, 0.f, 0.f}, c1 = c0;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                c0 = tf_mfma_f16_k32(kf[jj], qa[jj][0], c0);
+                c1 = tf_mfma_f16_k32(kf[jj], qa[jj][1], c1);
+            }
+            const tf_p_f32x4 c = c0 + c1;
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv[r] = t0 + 4 * gg + r < g.t_end ? c[r] * sc : TF_P_NEG_BIG;
+        }
+        // ---- online softmax of head n
+        float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        const float m_new = fmaxf(m, tm);
+        const float alpha = __expf(m - m_new);
+        m = m_new;
+        tf_h16x8 pb;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = sv[r] > 0.5f * TF_P_NEG_BIG ? __expf(sv[r] - m_new) : 0.f;
+            ps += p;
+            const _Float16 h0 = (_Float16)p;
+            pb[r] = h0;
+            pb[4 + r] = (_Float16)(p - (float)h0);
+        }
+        l = l * alpha + ps;
+        // ---- O^T += V^T P^T (hi and lo parts of p in one k = 32 step)
+        {
+            _Float16 vv[8][4];
+            const uint8_t* vp = slot + voff;
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    vv[db][i] = *reinterpret_cast<const _Float16*>(vp + 256 * i + 32 * db);
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                tf_h16x8 va;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    va[i] = vv[db][i];
+                    va[4 + i] = vv[db][i];
+                }
+                o[db] = tf_mfma_f16_k32(va, pb, o[db] * alpha);
+            }
+        }
+        // the slot is consumed: refill it with tile j + 2 waves
+        if (j + 2 * TF_P_WAVES < n16) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            tf_p_attn_dma_tile(L, g, stride, lds, j + 2 * TF_P_WAVES, k & 1);
+        }
+    }
+
+    // ---- the eight waves' (m, l, O) through LDS, merged per head
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    __syncthreads();  // every wave is done with its ring
+    float* cmb = reinterpret_cast<float*>(lds);  // [waves][16 heads][CR]
+    float* row = cmb + (wave * 16 + n) * DL::CR;
+    if (gg == 0) {
+        row[0] = m;
+        row[1] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; db++)
+        *reinterpret_cast<tf_p_f32x4*>(row + 4 + 16 * db + 4 * gg) = o[db];
+    __syncthreads();
+    float* ol = reinterpret_cast<float*>(lds + DL::OL);  // O [8][HD], then (m, l) [8][2]
+    for (int i = tid; i < G * HD; i += TF_P_THREADS) {
+        const int h = i / HD, d = i % HD;
+        float mw[TF_P_WAVES], M = TF_P_NEG_BIG;
+#pragma unroll
+        for (int w = 0; w < TF_P_WAVES; w++) {
+            mw[w] = cmb[(w * 16 + h) * DL::CR];
+            M = fmaxf(M, mw[w]);
+        }
+        float O = 0.f, Ls = 0.f;
+#pragma unroll
+        for (int w = 0; w < TF_P_WAVES; w++) {
+            const float e = __expf(mw[w] - M);
+            O += e * cmb[(w * 16 + h) * DL::CR + 4 + d];
+            Ls += e * cmb[(w * 16 + h) * DL::CR + 1];
+        }
+        ol[h * HD + d] = O;
+        if (d == 0) {
+            ol[8 * HD + 2 * h] = M;
+            ol[8 * HD + 2 * h + 1] = Ls;
+        }
+    }
+    __syncthreads();
+    if (valid) {
+        m_out = ol[8 * HD + 2 * hd];
+        l_out = ol[8 * HD + 2 * hd + 1];
+        o0 = ol[hd * HD + 2 * lane];
+        o1 = ol[hd * HD + 2 * lane + 1];
+    }
 }
 
 template <bool MM>
@@ -1329,10 +1556,17 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     constexpr int HD = TF_P_HD;
     const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KV, stride = a.KV * HD;
+    // matrix-core tiles copied HBM -> LDS per wave, for a single head group
+    // with one wave per head (long contexts)
+    const bool mm = MM && g.n_hg == 1 && g.wph == 1;
     uint16_t* k_lds = reinterpret_cast<uint16_t*>(lds);
     uint16_t* v_lds = reinterpret_cast<uint16_t*>(lds + LA::K_BYTES);
-    float* q_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES);
+    float* q_lds = reinterpret_cast<float*>(mm ? lds + TfPDmaLayout::Q
+                                               : lds + LA::K_BYTES + LA::V_BYTES);
     float* p_lds = q_lds + 8 * HD;
+    // the first two tiles of this wave go out before the poll: the K/V
+    // stream overlaps the wait for q
+    if (mm) tf_p_attn_dma_prime(L, g, stride, lds);
     // q of the kv head's G query heads (words 0 .. G HD) and the new K/V row
     // (words G HD .. G HD + 2 HD): both vectors in one poll
     {
@@ -1350,47 +1584,6 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     }
     tf_p_stamp(a, sk, 1);
 
-    // matrix-core tiles for a single head group with one wave per head
-    const bool mm = MM && g.n_hg == 1 && g.wph == 1;
-    const int l16 = lane & 15, gq = lane >> 4;
-    float* mx_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES);
-    float* sm_lds = mx_lds + 64;  // [4 waves][16 heads] each, in the P area
-    float* pm_lds = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES +
-                                             LA::P_BYTES);  // weights [8][SROW], in the C area
-    tf_p_h16x4 qa[8][3];
-    float msc = 0.f, m4[4], l4[4];
-    tf_p_f32x4 om = tf_p_f32x4{0.f, 0.f, 0.f, 0.f}, oml = om;
-    if (mm) {
-        float qmax = 0.f;
-        const bool hv = l16 < G;
-#pragma unroll
-        for (int st = 0; st < 8; st++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                qmax = fmaxf(qmax, hv ? fabsf(q_lds[l16 * HD + 16 * st + 4 * gq + i]) : 0.f);
-        qmax = tf_wave_max(qmax);
-        const int e = qmax >= 16384.f ? ilogbf(qmax) - 13 : 0;
-#pragma unroll
-        for (int st = 0; st < 8; st++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float x = hv ? ldexpf(q_lds[l16 * HD + 16 * st + 4 * gq + i], -e) : 0.f;
-                const _Float16 p0 = (_Float16)x;
-                x -= (float)p0;
-                const _Float16 p1 = (_Float16)x;
-                x -= (float)p1;
-                qa[st][0][i] = p0;
-                qa[st][1][i] = p1;
-                qa[st][2][i] = (_Float16)x;
-            }
-        msc = ldexpf(a.scale, e);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            m4[r] = TF_P_NEG_BIG;
-            l4[r] = 0.f;
-        }
-    }
-
     // this wave: head hd (valid if hh < hpw and hd < G), token slice sl
     const int hh = wave / g.wph, sl = wave % g.wph;
     const int hd = g.hg * g.hpw + hh;
@@ -1402,7 +1595,8 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     const float scale = a.scale;
     float* cm = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES +
                                          LA::P_BYTES);  // [wave][2 + HD]
-    for (int it = 0; it < g.tpw; it++) {
+    if (mm) tf_p_attn_dma_run(a, L, g, pos, stride, lds, q_lds, valid, hd, m, l, o0, o1);
+    for (int it = 0; it < (mm ? 0 : g.tpw); it++) {
         const int t0 = g.t_begin + it * TF_P_TILE;
         __syncthreads();  // the previous tile is consumed
 #pragma unroll
@@ -1422,83 +1616,6 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         if (it + 1 < g.tpw) tf_p_attn_load(L, stride, g.kh, t0 + TF_P_TILE, g.t_end, pos, r);
         __syncthreads();
-        if (mm) {
-            const bool tv = t0 + 16 * wave + l16 < g.t_end;
-            float sv[4];
-            if (wave < 4) {
-                tf_p_f32x4 c0 = tf_p_f32x4{0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
-                const uint16_t* kp = k_lds + (16 * wave + l16) * TF_P_KROW + 4 * gq;
-                tf_p_h16x4 kf[8];
-#pragma unroll
-                for (int st = 0; st < 8; st++)
-                    kf[st] = *reinterpret_cast<const tf_p_h16x4*>(kp + 16 * st);
-#pragma unroll
-                for (int st = 0; st < 8; st++) {
-                    c0 = tf_p_mfma16(qa[st][0], kf[st], c0);
-                    c1 = tf_p_mfma16(qa[st][1], kf[st], c1);
-                    c2 = tf_p_mfma16(qa[st][2], kf[st], c2);
-                }
-                const tf_p_f32x4 c = c0 + (c1 + c2);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    sv[r] = tv ? c[r] * msc : TF_P_NEG_BIG;
-                    const float wm = tf_row16_max(sv[r]);  // one head's 16 tokens
-                    if (l16 == 0) mx_lds[wave * 16 + 4 * gq + r] = wm;
-                }
-            }
-            __syncthreads();
-            float alpha[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int h = 4 * gq + r;
-                const float tm = fmaxf(fmaxf(mx_lds[h], mx_lds[16 + h]),
-                                       fmaxf(mx_lds[32 + h], mx_lds[48 + h]));
-                const float m_new = fmaxf(m4[r], tm);
-                alpha[r] = __expf(m4[r] - m_new);
-                if (wave < 4) {
-                    const float pr = tv ? __expf(sv[r] - m_new) : 0.f;
-                    if (h < 8) pm_lds[h * TF_P_SROW + 16 * wave + l16] = pr;
-                    const float ws = tf_row16_sum(pr);
-                    if (l16 == 0) sm_lds[wave * 16 + h] = ws;
-                }
-                m4[r] = m_new;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int h = 4 * gq + r;
-                l4[r] = l4[r] * alpha[r] +
-                        ((sm_lds[h] + sm_lds[16 + h]) + (sm_lds[32 + h] + sm_lds[48 + h]));
-                om[r] *= alpha[r];
-                oml[r] *= alpha[r];
-            }
-            // PV for dims 16 wave .. +15
-            float4 pf[4];
-            uint16_t vf[4][4];
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++) {
-                pf[ts] = l16 < G ? *reinterpret_cast<const float4*>(pm_lds + l16 * TF_P_SROW + 16 * ts + 4 * gq)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    vf[ts][i] = v_lds[(16 * ts + 4 * gq + i) * HD + 16 * wave + l16];
-            }
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++) {
-                const float pp[4] = {pf[ts].x, pf[ts].y, pf[ts].z, pf[ts].w};
-                tf_p_h16x4 ahi, alo, bv;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const _Float16 h0 = (_Float16)pp[i];
-                    ahi[i] = h0;
-                    alo[i] = (_Float16)(pp[i] - (float)h0);
-                    bv[i] = __builtin_bit_cast(_Float16, vf[ts][i]);
-                }
-                om = tf_p_mfma16(ahi, bv, om);
-                oml = tf_p_mfma16(alo, bv, oml);
-            }
-            continue;
-        }
         if (!valid || t0 >= g.t_end) continue;
         // ---- scores: lane (ti, ds) sums dims ds DS .. + DS of token sl T + ti
         // in four chains; the WPH dim slices are then added across lanes
@@ -1558,28 +1675,6 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
         o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
         o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
-    }
-    if (mm) {
-        __syncthreads();  // the last tile's K/V readers are done: reuse the K area
-        float* ol = reinterpret_cast<float*>(lds);  // [8 heads][HD], then (m, l) [8][2]
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int h = 4 * gq + r;
-            if (h < G) {
-                ol[h * HD + 16 * wave + l16] = om[r] + oml[r];
-                if (wave == 0 && l16 == 0) {
-                    ol[8 * HD + 2 * h] = m4[r];
-                    ol[8 * HD + 2 * h + 1] = l4[r];
-                }
-            }
-        }
-        __syncthreads();
-        if (valid) {  // wave hd: its head's (m, l, O) in the vector-ALU lane layout
-            m = ol[8 * HD + 2 * hd];
-            l = ol[8 * HD + 2 * hd + 1];
-            o0 = ol[hd * HD + 2 * lane];
-            o1 = ol[hd * HD + 2 * lane + 1];
-        }
     }
     // ---- the WPH slices of a head: log-sum-exp merge, in slice order, by slice 0
     if (g.wph > 1) {
@@ -1787,7 +1882,9 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     const TfPAttnGeo g = tf_p_attn_geo(a, pos);
     if (!g.active) return true;
     TfPAttnRegs ra;
-    tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
+    // (the matrix-core path copies its tiles HBM -> LDS after the barrier)
+    if (!(MM && g.n_hg == 1 && g.wph == 1))
+        tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
     __syncthreads();  // the previous stage's LDS readers are done
     const bool ok = tf_p_attn_run<MM>(
@@ -2058,7 +2155,7 @@ template <int SE, int IE, int SF, int IF, bool MM>
 int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid_out,
                   int* lds_out) {
     auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, MM>;
-    const int lds = tf_p_lds(a);
+    const int lds = MM && tf_p_lds(a) < TfPDmaLayout::BYTES ? TfPDmaLayout::BYTES : tf_p_lds(a);
     static int attr_done[64];
     int dev = 0;
     (void)hipGetDevice(&dev);

@@ -23,6 +23,7 @@
 
 #include <atomic>
 
+#include "lds_dma.hpp"
 #include "tf_common.hpp"
 #include "tf_host.hpp"
 
@@ -662,8 +663,6 @@ __global__ __launch_bounds__(256) void tf_flash_partial_mfma_kernel(
 #define TF_FD_LDS (TF_FD_Q + 16 * 128 * 4)
 #define TF_FD_CR 132                           // combine row: m, l, pad, O[128]
 
-typedef _Float16 tf_h16x8 __attribute__((ext_vector_type(8)));
-
 #ifdef TF_FLASH_STAMPS
 __device__ unsigned long long tf_fd_stamps[4096 * 8];
 extern "C" int tf_flash_debug_fd_stamps(unsigned long long* host) {
@@ -675,31 +674,6 @@ extern "C" int tf_flash_debug_fd_stamps(unsigned long long* host) {
     do {               \
     } while (0)
 #endif
-
-// One 1 KB HBM -> LDS copy: lane l moves the 16 bytes at src to
-// lds_off + 16 l.  The LDS base goes through M0, which the compiler also
-// uses: it is saved and restored around the copy.  lds_off is wave-uniform.
-__device__ __forceinline__ void tf_fd_dma(const void* src, uint32_t lds_off) {
-    const uint32_t la = __builtin_amdgcn_readfirstlane(lds_off);
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %2, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(la), "v"(src)
-        : "memory");
-}
-
-__device__ __forceinline__ uint32_t tf_fd_lds_off(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-__device__ __forceinline__ tf_f32x4m tf_mfma_h16k32(tf_h16x8 a, tf_h16x8 b, tf_f32x4m c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
 
 __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
@@ -731,31 +705,31 @@ __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
     // G repeat head G - 1 and are zeroed below)
     {
         const int h = min(2 * wave + (lane >> 5), G - 1);
-        tf_fd_dma(q + ((size_t)kv_h * G + h) * HD + 4 * (lane & 31),
-                  tf_fd_lds_off(q_lds) + wave * 1024);
+        tf_lds_dma16(q + ((size_t)kv_h * G + h) * HD + 4 * (lane & 31),
+                  tf_lds_off(q_lds) + wave * 1024);
     }
     // tile j -> slot b: four copies of 4 K rows (issue_k), four of 4 V rows
     // (issue_v); rows past the split repeat its last token (their scores
     // are masked)
     auto issue_k = [&](int j, int b) {
         const int t0 = t_begin + TF_FD_TILE * j;
-        const uint32_t base = tf_fd_lds_off(ring) + b * TF_FD_SLOT;
+        const uint32_t base = tf_lds_off(ring) + b * TF_FD_SLOT;
         const int r4 = lane >> 4;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = 4 * i + r4;
             const int t = min(t0 + r, t_end - 1);
-            tf_fd_dma(kbase + (size_t)t * stride + 8 * (n ^ r), base + 1024 * i);
+            tf_lds_dma16(kbase + (size_t)t * stride + 8 * (n ^ r), base + 1024 * i);
         }
     };
     auto issue_v = [&](int j, int b) {
         const int t0 = t_begin + TF_FD_TILE * j;
-        const uint32_t base = tf_fd_lds_off(ring) + b * TF_FD_SLOT;
+        const uint32_t base = tf_lds_off(ring) + b * TF_FD_SLOT;
         const int r4 = lane >> 4;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = min(t0 + 4 * i + r4, t_end - 1);
-            tf_fd_dma(vbase + (size_t)t * stride + 8 * n, base + 4096 + TF_FD_VBLK * i);
+            tf_lds_dma16(vbase + (size_t)t * stride + 8 * n, base + 4096 + TF_FD_VBLK * i);
         }
     };
     // step of this wave: tiles j (slot 0) and j + 8 (slot 1), 32 tokens
@@ -836,8 +810,8 @@ __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
         tf_f32x4m c0 = tf_f32x4m{0.f, 0.f, 0.f, 0.f}, c1 = c0;
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
-            c0 = tf_mfma_h16k32(kf[jj], qa[jj][0], c0);
-            c1 = tf_mfma_h16k32(kf[jj], qa[jj][1], c1);
+            c0 = tf_mfma_f16_k32(kf[jj], qa[jj][0], c0);
+            c1 = tf_mfma_f16_k32(kf[jj], qa[jj][1], c1);
         }
         const tf_f32x4m c = c0 + c1;
 #pragma unroll
@@ -860,7 +834,7 @@ __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
                 va[i] = vv[db][i];
                 va[4 + i] = vv[db][i];
             }
-            o[db] = tf_mfma_h16k32(va, pb, o[db]);
+            o[db] = tf_mfma_f16_k32(va, pb, o[db]);
         }
     };
 
