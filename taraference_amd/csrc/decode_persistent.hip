@@ -1545,6 +1545,86 @@ __device__ __forceinline__ void tf_p_attn_dma_run(TfPA& a, TfPL& L, const TfPAtt
     }
 }
 
+// Split merge of the matrix-core path: workgroup ws merges the heads
+// h = ws, ws + n_ws, ... < G with all eight waves (attn/flash.cu:222-255).
+// Wave w polls the O words of splits w, w + 8, ... (lane = dims 2 lane,
+// 2 lane + 1) together with every split's (m, l) (lane s holds split s), so
+// a head's merge is one poll round for up to 64 splits instead of one per
+// 16 splits; M = max_s m_s, w_s = e^(m_s - M), L = sum_s w_s l_s; each wave
+// sums w_s O_s over its splits in split order, and the eight wave sums are
+// added in wave order through LDS.
+__device__ __forceinline__ bool tf_p_attn_merge_wg(TfPA& a, const TfPAttnGeo& g,
+                                                   unsigned long long* fo, unsigned to,
+                                                   unsigned tp) {
+    constexpr int HD = TF_P_HD;
+    constexpr size_t PS = 2 + HD;
+    constexpr int KM = TF_P_MAX_SPLIT / TF_P_WAVES;  // splits per wave at most
+    const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
+    const int G = a.H / a.KV;
+    float* red = reinterpret_cast<float*>(tf_p_lds);  // [waves][HD]
+    for (int h = g.ws; h < G; h += g.n_ws) {  // workgroup-uniform
+        const unsigned long long* pbase = tf_p_part(a, g.kh, h, 0);
+        const int sl = lane < g.n_ws ? lane : 0;
+        unsigned long long wm, wl, w0[KM], w1[KM];
+        auto load = [&]() {
+            wm = tf_ldc64(pbase + sl * PS);
+            wl = tf_ldc64(pbase + sl * PS + 1);
+#pragma unroll
+            for (int k = 0; k < KM; k++) {
+                const int s = wave + TF_P_WAVES * k;
+                const int sp = s < g.n_ws ? s : 0;
+                w0[k] = tf_ldc64(pbase + sp * PS + 2 + 2 * lane);
+                w1[k] = tf_ldc64(pbase + sp * PS + 3 + 2 * lane);
+            }
+        };
+        load();
+        for (int spins = 0;;) {
+            bool miss = lane < g.n_ws && ((unsigned)(wm >> 32) != tp || (unsigned)(wl >> 32) != tp);
+#pragma unroll
+            for (int k = 0; k < KM; k++)
+                miss |= wave + TF_P_WAVES * k < g.n_ws &&
+                        ((unsigned)(w0[k] >> 32) != tp || (unsigned)(w1[k] >> 32) != tp);
+            if (!__builtin_amdgcn_ballot_w64(miss)) break;
+            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
+                tf_p_abort(a);
+                return true;  // the launch is aborted; outputs are not used
+            }
+            __builtin_amdgcn_s_sleep(2);
+            load();
+        }
+        const float ms = lane < g.n_ws ? __uint_as_float((unsigned)wm) : TF_P_NEG_BIG;
+        const float Mx = tf_wave_max(ms);
+        const float ws_ = lane < g.n_ws ? __expf(ms - Mx) : 0.f;
+        const float Lt = tf_group_sum<64>(ws_ * __uint_as_float((unsigned)wl));
+        float A0 = 0.f, A1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < KM; k++) {
+            const int s = wave + TF_P_WAVES * k;
+            if (s < g.n_ws) {  // wave-uniform
+                const float w = tf_readlane(ws_, s);
+                A0 = fmaf(w, __uint_as_float((unsigned)w0[k]), A0);
+                A1 = fmaf(w, __uint_as_float((unsigned)w1[k]), A1);
+            }
+        }
+        red[wave * HD + 2 * lane] = A0;
+        red[wave * HD + 2 * lane + 1] = A1;
+        __syncthreads();
+        if (wave == 0) {
+            float B0 = 0.f, B1 = 0.f;
+#pragma unroll
+            for (int w = 0; w < TF_P_WAVES; w++) {
+                B0 += red[w * HD + 2 * lane];
+                B1 += red[w * HD + 2 * lane + 1];
+            }
+            const float den = fmaxf(Lt, 1e-20f);
+            const int og = ((g.kh * G + h) * HD + 2 * lane) / 32;
+            tf_p_put_pair16(fo, og, lane & 15, B0 / den, B1 / den, to);
+        }
+        __syncthreads();  // red is reused by the next head
+    }
+    return true;
+}
+
 template <bool MM>
 __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo& g, int pos,
                                               TfPAttnRegs& r, uint8_t* lds,
@@ -1726,6 +1806,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         tf_p_putf(pp + 2 + 2 * lane, o0, tp);
         tf_p_putf(pp + 3 + 2 * lane, o1, tp);
     }
+    if (mm) return tf_p_attn_merge_wg(a, g, fo, to, tp);
     if (!own || hd % g.n_ws != g.ws) return true;
     // lane s holds split s's (m, l); lane = dims 2 lane, 2 lane + 1 for O.
     // M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O = sum_s w_s O_s
