@@ -37,84 +37,11 @@ struct TfFlashLds {
     static constexpr int PER_THREAD = CHUNKS / 256;
 };
 
-// Log-sum-exp merge of the n_split partitions of heads h0 .. h0+G-1 by one
-// 256-thread workgroup (flash.cu:222-255), optionally quantizing the merged
-// output to Q8 (32-value groups).  Wave w takes heads w, w+4, ...: lane =
-// partition for the weights e^(m_s - M) (kept in LDS) and the normalizer
-// L = sum_s e^(m_s - M) l_s.  Then every thread owns (head, dim) outputs.
-// Needs n_split <= 64 and G * n_split + G floats of LDS scratch.
-template <int OUT>  // outputs per thread: OUT * 256 >= G * hd
-__device__ __forceinline__ void tf_flash_merge_group(const float* partial, float* out,
-                                                     int8_t* q8, float* d8, int h0, int G,
-                                                     int hd, int n_split, float* scratch) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int po = 2 + hd;
-    float* wts = scratch;
-    float* Ls = scratch + G * n_split;
-    for (int g = wave; g < G; g += 4) {
-        const float* ph = partial + (size_t)(h0 + g) * n_split * po;
-        const bool live = lane < n_split;
-        const float m = live ? ph[(size_t)lane * po] : TF_NEG_BIG;
-        const float lv = live ? ph[(size_t)lane * po + 1] : 0.f;
-        float M = m;
-        M = tf_wave_max(M);
-        const float a = live ? __expf(m - M) : 0.f;
-        const float Lsum = tf_group_sum<64>(a * lv);
-        if (live) wts[g * n_split + lane] = a;
-        if (lane == 0) Ls[g] = Lsum;
-    }
-    __syncthreads();
-    // Output idx = tid + 256k (k < OUT) is (head idx / hd, dim idx % hd);
-    // G * hd is a multiple of 64, so each wave's outputs are all live or all
-    // dead.  All partial loads of a split are issued together.
-    float acc[OUT];
-#pragma unroll
-    for (int k = 0; k < OUT; k++) acc[k] = 0.f;
-    for (int s0 = 0; s0 < n_split; s0 += 8) {
-        float v[8][OUT];
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-#pragma unroll
-            for (int k = 0; k < OUT; k++) {
-                const int idx = tid + 256 * k;
-                const int g = idx / hd, d = idx - g * hd;
-                v[u][k] = (s0 + u < n_split && idx < G * hd)
-                              ? partial[((size_t)(h0 + g) * n_split + s0 + u) * po + 2 + d]
-                              : 0.f;
-            }
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-#pragma unroll
-            for (int k = 0; k < OUT; k++) {
-                const int idx = tid + 256 * k;
-                if (s0 + u < n_split && idx < G * hd)
-                    acc[k] += wts[(idx / hd) * n_split + s0 + u] * v[u][k];
-            }
-    }
-#pragma unroll
-    for (int k = 0; k < OUT; k++) {
-        const int idx = tid + 256 * k;
-        if (idx >= G * hd) break;  // wave-uniform
-        const int g = idx / hd, d = idx - g * hd;
-        const float v = acc[k] / fmaxf(Ls[g], 1e-20f);
-        const size_t i = (size_t)(h0 + g) * hd + d;
-        out[i] = v;
-        if (q8) {
-            const float amax = tf_group32_max(fabsf(v));
-            const float dq = amax * (1.0f / 127.0f);
-            q8[i] = (int8_t)tf_q8_value(v, amax, dq);
-            if ((d & 31) == 0) d8[i >> 5] = dq;
-        }
-    }
-}
-
 template <int HD, int HPW>
 __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, float* __restrict__ partial, int n_head, int n_kv,
-    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale,
-    unsigned* __restrict__ counters, float* __restrict__ out, int8_t* __restrict__ q8,
-    float* __restrict__ d8) {
+    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale) {
     using L = TfFlashLds<HD>;
     constexpr int GMAX = 4 * HPW;
     constexpr int DPL = HD / 64;
@@ -291,25 +218,6 @@ __global__ __launch_bounds__(256) void tf_flash_partial_kernel(
             for (int i = 0; i < DPL; i++) base[2 + lane * DPL + i] = o[hh][i];
         }
     }
-    if (counters == nullptr) return;
-    // Fused merge: the last workgroup of this kv head to finish merges the
-    // n_split partials of its G heads.  Each wave releases its partial
-    // writes at device scope; one ticket per workgroup; the last holder
-    // acquires everyone else's writes, merges and re-arms the counter.
-    __shared__ int s_last;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(counters + kv_h, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)(n_split - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    tf_flash_merge_group<(GMAX * HD + 255) / 256>(partial, out, q8, d8, kv_h * G, G, HD, n_split,
-                                                  reinterpret_cast<float*>(lds_raw));
-    if (tid == 0) counters[kv_h] = 0u;
 }
 
 // ------------------------------------------------ matrix-core partial
@@ -367,9 +275,7 @@ __device__ __forceinline__ tf_f32x4m tf_mfma_h16(tf_h16x4 a, tf_h16x4 b, tf_f32x
 __global__ __launch_bounds__(256) void tf_flash_partial_mfma_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, float* __restrict__ partial, int n_head, int n_kv,
-    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale,
-    unsigned* __restrict__ counters, float* __restrict__ out, int8_t* __restrict__ q8,
-    float* __restrict__ d8) {
+    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale) {
     constexpr int HD = 128;
     constexpr int PER_THREAD = 64 * HD / 8 / 256;  // 16-byte chunks of a tile per thread
     extern __shared__ __align__(16) uint8_t lds_raw[];
@@ -600,22 +506,6 @@ __global__ __launch_bounds__(256) void tf_flash_partial_mfma_kernel(
                 partial[((size_t)(kv_h * G + h) * n_split + s) * po + 2 + 32 * wave + 16 * b + l16] =
                     o[b][r] + olo[b][r];
         }
-    if (counters == nullptr) return;
-    // fused merge, as the VALU kernel
-    __shared__ int s_last_m;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(counters + kv_h, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last_m = prev == (unsigned)(n_split - 1);
-    }
-    __syncthreads();
-    if (!s_last_m) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    tf_flash_merge_group<(16 * HD + 255) / 256>(partial, out, q8, d8, kv_h * G, G, HD, n_split,
-                                                reinterpret_cast<float*>(lds_raw));
-    if (tid == 0) counters[kv_h] = 0u;
 }
 
 // ------------------------------------------- matrix-core partial, DMA-fed
@@ -1081,11 +971,11 @@ static int tf_flash_lds_bytes(int hpw) {
 template <int HD>
 static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t* v,
                               float* partial, int n_head, int n_kv, int pos0,
-                              const int* pos0_dev, int n_split, float scale, unsigned* counters,
-                              float* out, int8_t* q8, float* d8, tf_stream_t stream) {
+                              const int* pos0_dev, int n_split, float scale,
+                              tf_stream_t stream) {
     const int G = n_head / n_kv;
     const dim3 grid(n_kv, n_split);
-    if (HD == 128 && G <= 16 && counters == nullptr && tf_flash_kernel_choice() == TF_FK_DMA) {
+    if (HD == 128 && G <= 16 && tf_flash_kernel_choice() == TF_FK_DMA) {
         const int rc = tf_flash_dma_prepare();
         if (rc) return rc;
         hipLaunchKernelGGL(tf_flash_partial_dma_kernel, grid, dim3(64 * TF_FD_WAVES), TF_FD_LDS,
@@ -1096,30 +986,28 @@ static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t*
     if (HD == 128 && G <= 16 && tf_flash_kernel_choice() != TF_FK_VALU) {
         hipLaunchKernelGGL(tf_flash_partial_mfma_kernel, grid, dim3(256), TF_FM_LDS,
                            tf_stream(stream), q, k, v, partial, n_head, n_kv, pos0, pos0_dev,
-                           n_split, scale, counters, out, q8, d8);
+                           n_split, scale);
         return TF_LAUNCH_RESULT();
     }
     if (G <= 4)
         hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 1>), grid, dim3(256),
                            tf_flash_lds_bytes<HD>(1), tf_stream(stream), q, k, v, partial, n_head,
-                           n_kv, pos0, pos0_dev, n_split, scale, counters, out, q8, d8);
+                           n_kv, pos0, pos0_dev, n_split, scale);
     else if (G <= 8)
         hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 2>), grid, dim3(256),
                            tf_flash_lds_bytes<HD>(2), tf_stream(stream), q, k, v, partial, n_head,
-                           n_kv, pos0, pos0_dev, n_split, scale, counters, out, q8, d8);
+                           n_kv, pos0, pos0_dev, n_split, scale);
     else
         hipLaunchKernelGGL((tf_flash_partial_kernel<HD, 4>), grid, dim3(256),
                            tf_flash_lds_bytes<HD>(4), tf_stream(stream), q, k, v, partial, n_head,
-                           n_kv, pos0, pos0_dev, n_split, scale, counters, out, q8, d8);
+                           n_kv, pos0, pos0_dev, n_split, scale);
     return TF_LAUNCH_RESULT();
 }
 
 static int tf_flash_partial_any(const float* q, const uint16_t* k, const uint16_t* v,
                                 float* partial, int n_head, int n_kv, int head_dim, int pos0,
                                 const int* pos0_dev, int n_q, int n_split, float scale,
-                                tf_stream_t stream, unsigned* counters = nullptr,
-                                float* out = nullptr, int8_t* q8 = nullptr,
-                                float* d8 = nullptr) {
+                                tf_stream_t stream) {
     TF_CHECK_ARG(q && k && v && partial && n_head > 0 && n_kv > 0 && n_head % n_kv == 0);
     TF_CHECK_ARG(n_head / n_kv <= 16 && n_q == 1 && n_split >= 1 && n_split <= 1024);
     TF_CHECK_ARG(pos0_dev || pos0 >= 0);
@@ -1127,13 +1015,13 @@ static int tf_flash_partial_any(const float* q, const uint16_t* k, const uint16_
     switch (head_dim) {
     case 64:
         return tf_flash_launch_hd<64>(q, k, v, partial, n_head, n_kv, pos0, pos0_dev, n_split,
-                                      scale, counters, out, q8, d8, stream);
+                                      scale, stream);
     case 128:
         return tf_flash_launch_hd<128>(q, k, v, partial, n_head, n_kv, pos0, pos0_dev, n_split,
-                                       scale, counters, out, q8, d8, stream);
+                                       scale, stream);
     case 256:
         return tf_flash_launch_hd<256>(q, k, v, partial, n_head, n_kv, pos0, pos0_dev, n_split,
-                                       scale, counters, out, q8, d8, stream);
+                                       scale, stream);
     default:
         return (int)hipErrorInvalidValue;
     }

@@ -79,13 +79,13 @@ def test_flash_prefix_of_longer_cache(gpu):
 
 @pytest.mark.parametrize("n_head,n_kv,hd,L,n_split", [
     (16, 2, 128, 1, 8), (16, 2, 128, 5, 8), (16, 2, 128, 777, 8), (16, 2, 128, 4096, 32),
-    (16, 2, 128, 5000, 64), (16, 2, 128, 32768, 256),      # 256: merge as a second kernel
+    (16, 2, 128, 5000, 64), (16, 2, 128, 32768, 256),
     (28, 4, 128, 3000, 16), (8, 8, 64, 100, 8), (32, 2, 128, 600, 8), (16, 4, 256, 700, 24)])
-def test_flash_decode_fused_merge(gpu, n_head, n_kv, hd, L, n_split):
-    """tf_flash_decode: partials + merge by the last workgroup of each kv head
-    (+ Q8 of the merged output).  Attention within 2e-3 of fp64 softmax
+def test_flash_decode_one_call(gpu, n_head, n_kv, hd, L, n_split):
+    """tf_flash_decode: split partials then the log-sum-exp merge (+ Q8 of
+    the merged output) in one call.  Attention within 2e-3 of fp64 softmax
     attention, the Q8 bit-exact against quantizing the f32 it wrote, and
-    the per-kv-head counters back at zero after each call (two calls in a
+    the per-kv-head counters still zero after each call (two calls in a
     row give the same result; the second reads the position from device
     memory)."""
     q, K, V = case(L, n_head, n_kv, hd, L + n_split)
