@@ -36,6 +36,7 @@
 // grid always drains.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "argmax_key.hpp"
@@ -2237,14 +2238,20 @@ int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid
                   int* lds_out) {
     auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, MM>;
     const int lds = MM && tf_p_lds(a) < TfPDmaLayout::BYTES ? TfPDmaLayout::BYTES : tf_p_lds(a);
-    static int attr_done[64];
+    // the dynamic LDS limit of this instantiation, raised per device to the
+    // largest size a model has needed so far
+    static std::mutex attr_mu;
+    static int attr_lds[64];
     int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (dev >= 0 && dev < 64 && !attr_done[dev]) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                lds) != hipSuccess)
-            return (int)hipErrorInvalidValue;
-        attr_done[dev] = 1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    {
+        std::lock_guard<std::mutex> lk(attr_mu);
+        if (attr_lds[dev] < lds) {
+            if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    lds) != hipSuccess)
+                return (int)hipErrorInvalidValue;
+            attr_lds[dev] = lds;
+        }
     }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, TF_P_THREADS,
