@@ -8,6 +8,7 @@ library is missing, loading raises.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load: shared HIP runtime)
@@ -86,12 +87,13 @@ class HipError(RuntimeError):
 _lib = None
 
 
-def load(path: Path | str = LIB_PATH) -> C.CDLL:
-    """Load the HIP library (raises if it has not been built)."""
+def load(path: Path | str | None = None) -> C.CDLL:
+    """Load the HIP library (raises if it has not been built).  TF_HIP_LIB
+    names another build of the same library (A/B measurements)."""
     global _lib
     if _lib is not None:
         return _lib
-    p = Path(path)
+    p = Path(path or os.environ.get("TF_HIP_LIB") or LIB_PATH)
     if not p.exists():
         raise FileNotFoundError(
             f"{p} is missing: build it with `python -m taraference_amd.build` "

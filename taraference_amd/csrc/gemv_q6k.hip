@@ -11,6 +11,7 @@
 // persistent, so the tall ffn_down and the wide lm_head use the same kernel.
 #include <type_traits>
 
+#include "lds_dma.hpp"
 #include "q6k.hpp"
 #include "tf_host.hpp"
 
@@ -57,6 +58,111 @@ __global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q6k_rows_kernel(
         }
         if constexpr (ITERS > 0) cur = nxt;
         j = jn;
+    }
+}
+
+// Wide Q6_K GEMV fed by HBM -> LDS copies (the lm_head: K = 2048, 151936
+// rows, 256 MB per launch).  Each of the 8 waves of a workgroup owns an
+// S-slot LDS ring and streams its tasks (R consecutive rows, one contiguous
+// run of R * NB * 212 bytes) into it with global_load_lds_dwordx4, S - 1
+// tasks in flight while one computes, so the wave's memory queue never waits
+// on its own arithmetic.  Lanes: 64 / R per row (row r = lane / (64 / R));
+// lane u of a row takes parts (sb, p) = (u / 4 + (16 / R) i, u % 4).  The
+// row's lanes are summed with one group reduction.  Same integer stage and
+// scaling as tf_q6k_part_dot.
+template <int NB, int R, int S>
+struct TfQ6Dma {
+    static constexpr int CHUNKS = R * NB * 212 / 16;  // 16-byte chunks per task
+    static constexpr int NI = (CHUNKS + 63) / 64;     // copy instructions per task
+    static constexpr int SLOT = NI * 1024;            // bytes per ring slot
+    static constexpr int LPR = 64 / R;                // lanes per row
+    static constexpr int UPL = NB * 4 / LPR;          // (super-block, part) units per lane
+    static_assert(R == 1 || R == 2 || R == 4, "rows per task");
+    static_assert(NB % 4 == 0 && UPL >= 1 && UPL * LPR == NB * 4, "lane map");
+    static constexpr int LDS = 8 * S * SLOT;          // the rings of the 8 waves
+};
+
+// Copies of task `task` into the slot at LDS byte slot_off: copy i of lane l
+// moves bytes [16 c, 16 c + 16) of the task's run, c = 64 i + l; chunks past
+// the run (or past the matrix) copy the run's first bytes into LDS bytes
+// nothing reads.
+template <int NB, int R, int S>
+__device__ __forceinline__ void tf_q6d_issue(const uint8_t* __restrict__ w, int n_cols,
+                                             int task, uint32_t slot_off, int lane) {
+    using D = TfQ6Dma<NB, R, S>;
+    const uint8_t* base = w + (size_t)task * (R * NB * 212);
+    const int left = (n_cols - task * R) * (NB * 212 / 16);  // chunks inside the matrix
+#pragma unroll
+    for (int i = 0; i < D::NI; i++) {
+        const int c = 64 * i + lane;
+        tf_lds_dma16(c < D::CHUNKS && c < left ? base + 16 * c : base, slot_off + 1024 * i);
+    }
+}
+
+template <int NB, int R, int S, int SK>
+__global__ __launch_bounds__(512) void tf_q6k_dma_rows_kernel(
+    const uint8_t* __restrict__ w, TfActSrc src, float* __restrict__ out, int n_cols,
+    int col_bytes) {
+    using D = TfQ6Dma<NB, R, S>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int act = (tf_act_lds_bytes(NB, false) + 15) & ~15;
+    uint8_t* ring = lds + act + wave * S * D::SLOT;
+    const uint32_t ring_off = tf_lds_off(ring);
+    const int n_tasks = (n_cols + R - 1) / R;
+    const int G = gridDim.x * 8;
+    const int g = wave * gridDim.x + blockIdx.x;  // this wave's first task
+    // the first S - 1 tasks in flight (wave 0 stages the activation first: its
+    // staging loads would otherwise wait behind its copies)
+    if (wave != 0) {
+#pragma unroll
+        for (int q = 0; q < S - 1; q++)
+            if (g + q * G < n_tasks)
+                tf_q6d_issue<NB, R, S>(w, n_cols, g + q * G, ring_off + q * D::SLOT, lane);
+    }
+    tf_stage_act<false, SK>(src, NB, lds);
+    if (wave == 0) {
+#pragma unroll
+        for (int q = 0; q < S - 1; q++)
+            if (g + q * G < n_tasks)
+                tf_q6d_issue<NB, R, S>(w, n_cols, g + q * G, ring_off + q * D::SLOT, lane);
+    }
+    const TfAct x = tf_act_view(lds, NB);
+    const int r = lane / D::LPR, u = lane % D::LPR, p = u & 3, n = p >> 1, h = p & 1;
+    int k = 0;
+    for (int task = g; task < n_tasks; task += G) {
+        // refill: task + (S - 1) G goes to the slot freed by the previous task
+        if (task + (S - 1) * G < n_tasks)
+            tf_q6d_issue<NB, R, S>(w, n_cols, task + (S - 1) * G,
+                                   ring_off + (k == 0 ? S - 1 : k - 1) * D::SLOT, lane);
+        // this task's copies have landed: at most the S - 1 later tasks' are pending
+        if (task + (S - 1) * G < n_tasks)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 1) * D::NI) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint8_t* rowp = ring + k * D::SLOT + r * (NB * 212);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < D::UPL; i++) {
+            const int sb = (u >> 2) + (D::LPR / 4) * i;
+            // a block is 4-byte aligned in LDS (212 = 4 * 53)
+            const uint32_t* blk = reinterpret_cast<const uint32_t*>(rowp + sb * 212);
+            TfQ6kPart q;
+            const uint32_t* pa = blk + 16 * n + 4 * h;
+            const uint32_t* ph = blk + 32 + 8 * n + 4 * h;
+            q.a = tf_u32x4{pa[0], pa[1], pa[2], pa[3]};
+            q.b = tf_u32x4{pa[8], pa[9], pa[10], pa[11]};
+            q.hq = tf_u32x4{ph[0], ph[1], ph[2], ph[3]};
+            q.sc = tf_u32x2{blk[48 + 2 * n], blk[49 + 2 * n]};
+            q.d = blk[52];
+            acc += tf_q6k_part_dot(q, p, sb, x);
+        }
+        acc = tf_group_sum<D::LPR>(acc);
+        const int j = task * R + r;
+        if (u == 0 && j < n_cols) out[j] = acc;
+        // the slot's reads are done before the next iteration refills it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        k = k + 1 == S ? 0 : k + 1;
     }
 }
 
@@ -232,6 +338,17 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212;
 }
 
+// The LDS-fed kernel serves wide matrices with K = 1024 or 2048 and a plain
+// output (TF_Q6K_DMA=0 turns it off for comparisons).
+static bool tf_q6k_dma_ok(int nb, int n_cols, int col_bytes, int use_bias, int use_res) {
+    static const bool on = [] {
+        const char* e = getenv("TF_Q6K_DMA");
+        return !(e && e[0] == '0');
+    }();
+    return on && (nb == 8 || nb == 4) && col_bytes == nb * 212 && n_cols >= 65536 && !use_bias &&
+           use_res == 0;
+}
+
 static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_rows,
                        int n_cols, int col_bytes, int use_bias, const float* bias, int use_res,
                        const float* residual, tf_stream_t stream) {
@@ -243,6 +360,24 @@ static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_
     TF_CHECK_ARG(src.kind == TF_SRC_Q8 ? (src.xq && src.xd) : (src.x != nullptr));
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
+    if (tf_q6k_dma_ok(nb, n_cols, col_bytes, use_bias, use_res)) {
+        auto go = [&](auto nbc, auto rc_, auto sc_) {
+            constexpr int NB = decltype(nbc)::value, R = decltype(rc_)::value,
+                          S = decltype(sc_)::value;
+            auto fn = tf_sk_pick(src.kind, tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_Q8>,
+                                 tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_F32>,
+                                 tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_NORM>);
+            const int bytes = ((tf_act_lds_bytes(NB, false) + 15) & ~15) + TfQ6Dma<NB, R, S>::LDS;
+            if (tf_set_lds_limit((const void*)fn, bytes) != 0) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL(fn, dim3(tf_device_cus()), dim3(512), bytes, tf_stream(stream), w,
+                               src, out, n_cols, col_bytes);
+            return (int)TF_LAUNCH_RESULT();
+        };
+        // four rows per task, two ring slots per wave (measured on the 3B
+        // lm_head against 2 rows x 3 or 4 slots and register-staged copies)
+        if (nb == 4) return go(tf_ic6<4>{}, tf_ic6<4>{}, tf_ic6<2>{});
+        return go(tf_ic6<8>{}, tf_ic6<4>{}, tf_ic6<2>{});
+    }
     tf_q6k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         auto fn = tf_sk_pick(src.kind, tf_q6k_rows_kernel<SPR, IT, TF_SRC_Q8>,

@@ -178,3 +178,18 @@ extern "C" const char* tf_exported_symbol(int i) {
     if (i < 0 || i >= tf_exported_symbol_count()) return nullptr;
     return k_symbols[i];
 }
+
+int tf_set_lds_limit(const void* kernel, int bytes) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, int> done[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    int& have = done[dev][kernel];
+    if (have >= bytes) return 0;
+    const hipError_t rc =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (rc != hipSuccess) return (int)rc;
+    have = bytes;
+    return 0;
+}

@@ -14,3 +14,7 @@ int tf_device_cus();
 // CU while large ones get one CU-wide workgroup.
 int tf_block_threads(int max_threads, long long tasks);
 int tf_persistent_blocks(const void* kernel, int threads, int lds_bytes, int tasks);
+
+// Raises a kernel's dynamic LDS limit on the current device to at least
+// `bytes` (once per kernel, device and size; thread-safe).  0 or a HIP error.
+int tf_set_lds_limit(const void* kernel, int bytes);
