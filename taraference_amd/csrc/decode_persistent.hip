@@ -1016,7 +1016,7 @@ struct TfPGuMap {
 
 // LDS gather of h: the outputs of the workgroup's half-groups, then (one more
 // half-group) the second half of a split group.
-__shared__ float tf_p_hbuf[6 * 16];
+__shared__ __align__(16) float tf_p_hbuf[6 * 16];
 
 // Half-groups [s, e) of this workgroup.
 struct TfPGuSpan {
@@ -1052,6 +1052,22 @@ __device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int n_out, int j0
         tf_q4k_row_load_u<SPR, IT>(L.gate + (size_t)j * L.cb_gu, nb, ln.sir, ln.t, r.a);
         tf_q4k_row_load_u<SPR, IT>(L.up + (size_t)j * L.cb_gu, nb, ln.sir, ln.t, r.b);
     }
+}
+
+// Publishes the Q8 of one 32-value group held as two values per lane of a
+// 16-lane row (tf_q8_pair layout, the quantization of tf_quantize_q8) in the
+// tf_p_put_oct word layout: group G_ at words 9 G_ ... ; m = lane & 15.
+__device__ __forceinline__ void tf_p_put_pair16_if(unsigned long long* dst, int G_, int m,
+                                                   float v0, float v1, unsigned tag, bool put) {
+    const TfQ8Pair r = tf_q8_pair<false>(v0, v1);
+    const uint32_t h16 = (uint32_t)(r.q0 & 0xff) | ((uint32_t)(r.q1 & 0xff) << 8);
+    const uint32_t other = (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)h16);  // lane m ^ 1
+    if (put && (m & 1) == 0) tf_p_put(dst + 9 * G_ + (m >> 1), h16 | (other << 16), tag);
+    if (put && m == 0) tf_p_put(dst + 9 * G_ + 8, __float_as_uint(r.d), tag);
+}
+__device__ __forceinline__ void tf_p_put_pair16(unsigned long long* dst, int G_, int m, float v0,
+                                                float v1, unsigned tag) {
+    tf_p_put_pair16_if(dst, G_, m, v0, v1, tag, true);
 }
 
 // Publishes the Q8 of one 32-value group held as 8 values per lane of a
@@ -1135,17 +1151,18 @@ __device__ __forceinline__ void tf_p_gu_exchange(TfPA& a, const TfPGuSpan& sp,
     if (lane < 16) tf_p_hbuf[16 * (sp.e - sp.s) + lane] = __uint_as_float((unsigned)w);
 }
 
+// A workgroup holds at most two such groups (HMAX <= 5 half-groups, the
+// first of them possibly the second half of a group): 16-lane row k of the
+// wave takes group g0 + k, two values per lane (tf_q8_pair: the same Q8 as
+// tf_quantize_q8), so the quantization is a few dozen instructions.
 __device__ __forceinline__ void tf_p_gu_quantize(const TfPGuSpan& sp, unsigned long long* fh,
                                                  unsigned tag) {
     const int lane = tf_p_tid() & 63;
     const int g0 = (sp.s + 1) >> 1, ng = ((sp.e + 1) >> 1) - g0;
-    const int k = lane >> 2, j = lane & 3;  // quad k: group g0 + k, values 8 j .. 8 j + 7
-    const int o = k < ng ? 16 * (2 * (g0 + k) - sp.s) + 8 * j : 0;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = tf_p_hbuf[o + i];
-    const TfQ8Oct q = tf_q8_oct<false>(v);
-    if (k < ng) tf_p_put_oct(fh, g0 + k, j, q, tag);
+    const int k = lane >> 4, m = lane & 15;  // row k: group g0 + k, values 2 m, 2 m + 1
+    const int o = k < ng ? 16 * (2 * (g0 + k) - sp.s) + 2 * m : 0;
+    const float2 v = *reinterpret_cast<const float2*>(tf_p_hbuf + o);
+    tf_p_put_pair16_if(fh, g0 + k, m, v.x, v.y, tag, k < ng);
 }
 
 // Polls a Q8 vector published as 9-word groups (tf_p_put_oct layout) into the
@@ -1283,18 +1300,6 @@ __device__ __forceinline__ void tf_p_attn_load(TfPL& L, int stride, int kh, int 
 
 // Static LDS for the new K/V row of this workgroup's kv head (f16 bits).
 __shared__ __align__(16) uint16_t tf_p_knew[TF_P_HD], tf_p_vnew[TF_P_HD];
-
-// Publishes the Q8 of one 32-value group held as two values per lane of a
-// 16-lane row (tf_q8_pair layout, the quantization of tf_quantize_q8) in the
-// tf_p_put_oct word layout: group G_ at words 9 G_ ... ; m = lane & 15.
-__device__ __forceinline__ void tf_p_put_pair16(unsigned long long* dst, int G_, int m, float v0,
-                                                float v1, unsigned tag) {
-    const TfQ8Pair r = tf_q8_pair<false>(v0, v1);
-    const uint32_t h16 = (uint32_t)(r.q0 & 0xff) | ((uint32_t)(r.q1 & 0xff) << 8);
-    const uint32_t other = (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)h16);  // lane m ^ 1
-    if ((m & 1) == 0) tf_p_put(dst + 9 * G_ + (m >> 1), h16 | (other << 16), tag);
-    if (m == 0) tf_p_put(dst + 9 * G_ + 8, __float_as_uint(r.d), tag);
-}
 
 // Partial of (kv head kh, head g, split s): 2 + HD tagged words.
 __device__ __forceinline__ unsigned long long* tf_p_part(TfPA& a, int kh, int g, int s) {
