@@ -87,42 +87,6 @@ __device__ __forceinline__ void tf_q4k_idots(const TfQ4kPart& p, const int8_t* q
     tf_q4k_idots_r(p, qv[0], qv[1], qv[2], qv[3], dlo, dhi);
 }
 
-// A lane's activation operands for one super-block (the 64 Q8 bytes of
-// groups 2t, 2t + 1, their d8 and d8 * sum), read once from the LDS image
-// and reused for every row the lane takes.
-struct TfQ4kXFrag {
-    tf_u32x4 u0, u1, w0, w1;
-    float2 d8, ds;
-};
-
-__device__ __forceinline__ TfQ4kXFrag tf_q4k_xfrag(const TfAct& x, int sb, int t) {
-    TfQ4kXFrag f;
-    const tf_u32x4* qv = reinterpret_cast<const tf_u32x4*>(x.q8 + tf_q8_pad(sb * 256 + 64 * t));
-    f.u0 = qv[0];
-    f.u1 = qv[1];
-    f.w0 = qv[2];
-    f.w1 = qv[3];
-    const int g = sb * 8 + 2 * t;
-    f.d8 = *reinterpret_cast<const float2*>(x.d8 + g);
-    f.ds = *reinterpret_cast<const float2*>(x.ds + g);
-    return f;
-}
-
-// tf_q4k_part_dot with the activation operands in registers (same
-// arithmetic, same order).
-__device__ __forceinline__ float tf_q4k_part_dot_x(const TfQ4kPart& p, int t,
-                                                   const TfQ4kXFrag& f) {
-    int dlo, dhi;
-    tf_q4k_idots_r(p, f.u0, f.u1, f.w0, f.w1, dlo, dhi);
-    int sc0, sc1, m0, m1;
-    tf_q4k_scales(p.h, t, sc0, sc1, m0, m1);
-    const float d = tf_h2f(p.h.x);
-    const float dmin = tf_h2f(p.h.x >> 16);
-    const float scale_term = f.d8.x * (float)(dlo * sc0) + f.d8.y * (float)(dhi * sc1);
-    const float min_term = (float)m0 * f.ds.x + (float)m1 * f.ds.y;
-    return d * scale_term - dmin * min_term;
-}
-
 // fp32 contribution of this lane's two sub-blocks of super-block sb.
 __device__ __forceinline__ float tf_q4k_part_dot(const TfQ4kPart& p, int t, int sb,
                                                  const TfQ8Lds& x) {
