@@ -65,9 +65,9 @@ def test_invalid_args_rejected(capi):
     assert lib.tf_flash_decode_reduce(16, 16, 16, 128, 0, 1, None) == INVALID
     assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 96, None) == INVALID   # n % 128
     assert lib.tf_norm_quant(16, 16, 1e-6, 16, 16, 16, 8320, None) == INVALID  # n > 8192
-    # prefill GEMMs: a width that is not whole super-blocks (n_rows % 256)
-    assert lib.tf_gemm_q4k_f32(16, 16, 16, 512 + 4, 16, 2 * 144, 1, None) == INVALID
-    assert lib.tf_gemm_q6k_f32(16, 16, 16, 512 + 4, 16, 2 * 210, 1, None) == INVALID
+    # prefill GEMMs: K not a multiple of 4, or a column shorter than its blocks
+    assert lib.tf_gemm_q4k_f32(16, 16, 16, 512 + 2, 16, 2 * 144, 1, None) == INVALID
+    assert lib.tf_gemm_q6k_f32(16, 16, 16, 512, 16, 2 * 210 - 2, 1, None) == INVALID
     assert lib.tf_version() >= 100
 
 
