@@ -1961,13 +1961,67 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     return true;
 }
 
+// L2 warm-up of the layer's gate/up weights by the workgroups without
+// attention work.  Workgroup b runs on XCD b % 8 (the dispatcher deals the
+// persistent grid round-robin over the XCDs), and the 32 workgroups of an XCD
+// share its 4 MB L2.  During the attention stage HBM is nearly idle, so the
+// XCD's non-attention workgroups copy the gate and up row runs of every
+// workgroup of their XCD (about 3.2 MB per XCD at the 3B shape) HBM -> LDS,
+// into a scratch KB per wave that nothing reads: the lines stay in the L2,
+// and the gate/up stage's weight loads, and the drain of its prefetch ahead of
+// the x' poll, then run from L2.  The copies start TF_P_WARM_DELAY x 10 ns
+// after the stage starts, once the attention workgroups' q poll is done (its
+// round trip slows under the extra traffic), and each wave keeps at most
+// 2 TF_P_WARM copies in flight.  Only when the XCD's share fits the L2 with
+// room to spare (gate + up at most 28 MB).  Their own wo poll, about 5 us
+// later, finds the copies drained.
+#ifndef TF_P_WARM
+#define TF_P_WARM 4
+#endif
+#ifndef TF_P_WARM_DELAY
+#define TF_P_WARM_DELAY 150
+#endif
+#define TF_P_WARM_LDS 49152  // scratch: above every activation image and the attention tiles
+
+__device__ __forceinline__ void tf_p_gu_warm(TfPA& a, TfPL& L, int n_active) {
+    const size_t cb = L.cb_gu;
+    if (2 * (size_t)a.F * cb > ((size_t)28 << 20)) return;
+    const int G = gridDim.x, b = blockIdx.x, x = b & 7;
+    const int per = (G - x + 7) / 8;                            // workgroups on XCD x
+    const int att = n_active > x ? (n_active - x + 7) / 8 : 0;  // of them with attention
+    const int idx = (b - x) / 8 - att, nidle = per - att;
+    if (idx < 0 || nidle <= 0) return;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < TF_P_WARM_DELAY) __builtin_amdgcn_s_sleep(8);
+    const int lane = tf_p_tid() & 63, wave = tf_p_tid() >> 6;
+    const uint32_t dump = tf_lds_off(tf_p_lds + TF_P_WARM_LDS + 1024 * wave);
+    const int nh = a.F / 16;
+    const size_t end = (size_t)a.F * cb - 16;
+    int issued = 0;
+    for (int jj = idx; jj < per; jj += nidle) {
+        // the gate/up span of workgroup x + 8 jj (tf_p_gu_span)
+        const int bb = x + 8 * jj;
+        const int s0 = (int)((long long)nh * bb / G), e0 = (int)((long long)nh * (bb + 1) / G);
+        const size_t pieces = ((size_t)16 * (e0 - s0) * cb + 1023) / 1024;
+        for (size_t pc = wave; pc < 2 * pieces; pc += TF_P_WAVES) {
+            const int m = pc >= pieces ? 1 : 0;
+            const size_t off = (size_t)16 * s0 * cb + (pc - m * pieces) * 1024 + 16 * lane;
+            tf_lds_dma16((m ? L.up : L.gate) + (off < end ? off : end), dump);
+            if ((++issued & 3) == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(TF_P_WARM) : "memory");
+        }
+    }
+}
+
 template <bool MM>
 __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
     const TfPAttnGeo g = tf_p_attn_geo(a, pos);
-    if (!g.active) return true;
+    if (!g.active) {
+        if constexpr (!MM) tf_p_gu_warm(a, L, a.KV * g.n_hg * g.n_ws);
+        return true;
+    }
     TfPAttnRegs ra;
     // (the matrix-core path copies its tiles HBM -> LDS after the barrier)
     if (!(MM && g.n_hg == 1 && g.wph == 1))
@@ -2230,7 +2284,9 @@ int tf_p_lds(const TfPArgs& a) {
     const int f = tf_act_lds_bytes(nbF, true);
     if (f > b) b = f;
     const int at = TfPAttnLayout::BYTES;
-    return at > b ? at : b;
+    b = at > b ? at : b;
+    // the warm-up's scratch (tf_p_gu_warm)
+    return TF_P_WARM_LDS + TF_P_WAVES * 1024 > b ? TF_P_WARM_LDS + TF_P_WAVES * 1024 : b;
 }
 
 struct TfPLaunch {
