@@ -338,8 +338,8 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212;
 }
 
-// The LDS-fed kernel serves wide matrices with K = 1024 or 2048 and a plain
-// output (TF_Q6K_DMA=0 turns it off for comparisons).
+// The LDS-fed kernel serves wide matrices with K = 1024 or 2048, a Q8
+// activation and a plain output (TF_Q6K_DMA=0 turns it off for comparisons).
 static bool tf_q6k_dma_ok(int nb, int n_cols, int col_bytes, int use_bias, int use_res) {
     static const bool on = [] {
         const char* e = getenv("TF_Q6K_DMA");
@@ -360,13 +360,11 @@ static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_
     TF_CHECK_ARG(src.kind == TF_SRC_Q8 ? (src.xq && src.xd) : (src.x != nullptr));
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
-    if (tf_q6k_dma_ok(nb, n_cols, col_bytes, use_bias, use_res)) {
+    if (src.kind == TF_SRC_Q8 && tf_q6k_dma_ok(nb, n_cols, col_bytes, use_bias, use_res)) {
         auto go = [&](auto nbc, auto rc_, auto sc_) {
             constexpr int NB = decltype(nbc)::value, R = decltype(rc_)::value,
                           S = decltype(sc_)::value;
-            auto fn = tf_sk_pick(src.kind, tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_Q8>,
-                                 tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_F32>,
-                                 tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_NORM>);
+            auto fn = tf_q6k_dma_rows_kernel<NB, R, S, TF_SRC_Q8>;
             const int bytes = ((tf_act_lds_bytes(NB, false) + 15) & ~15) + TfQ6Dma<NB, R, S>::LDS;
             if (tf_set_lds_limit((const void*)fn, bytes) != 0) return (int)hipErrorInvalidValue;
             hipLaunchKernelGGL(fn, dim3(tf_device_cus()), dim3(512), bytes, tf_stream(stream), w,

@@ -191,6 +191,9 @@ def test_q6k_block_dots_exact(gpu, n_rows, n_cols):
     (11008, 2048, "tf_gemv_q6k_down_splitk", 2, False),   # config 1b
     (18944, 512, "tf_gemv_q6k_down_splitk", 2, True),
     (2048, 151936, "tf_gemv_q6k_compact_q8", 0, False),   # Qwen2.5-3B lm_head
+    # the LDS-fed wide kernel: K = 2048 with a ragged last four-row task, K = 1024
+    (2048, 65539, "tf_gemv_q6k_compact_q8", 0, False),
+    (1024, 70001, "tf_gemv_q6k_compact_q8", 0, False),
     (3584, 300, "tf_gemv_q6k_compact_q8", 1, True),
     (256, 9, "tf_gemv_q6k_compact_q8", 0, False),
 ])
