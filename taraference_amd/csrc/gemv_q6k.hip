@@ -338,15 +338,16 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
     return w && ((uintptr_t)w & 3) == 0 && (col_bytes & 3) == 0 && col_bytes >= nb * 212;
 }
 
-// The LDS-fed kernel serves wide matrices with K = 1024 or 2048, a Q8
-// activation and a plain output (TF_Q6K_DMA=0 turns it off for comparisons).
-static bool tf_q6k_dma_ok(int nb, int n_cols, int col_bytes, int use_bias, int use_res) {
+// The LDS-fed kernel serves wide matrices with K = 1024 or 2048, 16-byte
+// aligned rows of exactly nb compact blocks, a Q8 activation and a plain output (TF_Q6K_DMA=0 turns it off for comparisons).
+static bool tf_q6k_dma_ok(const uint8_t* w, int nb, int n_cols, int col_bytes, int use_bias,
+                          int use_res) {
     static const bool on = [] {
         const char* e = getenv("TF_Q6K_DMA");
         return !(e && e[0] == '0');
     }();
-    return on && (nb == 8 || nb == 4) && col_bytes == nb * 212 && n_cols >= 65536 && !use_bias &&
-           use_res == 0;
+    return on && (nb == 8 || nb == 4) && col_bytes == nb * 212 && ((uintptr_t)w & 15) == 0 &&
+           n_cols >= 65536 && !use_bias && use_res == 0;
 }
 
 static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_rows,
@@ -360,7 +361,7 @@ static int tf_q6k_rows(const uint8_t* w, const TfActSrc& src, float* out, int n_
     TF_CHECK_ARG(src.kind == TF_SRC_Q8 ? (src.xq && src.xd) : (src.x != nullptr));
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
-    if (src.kind == TF_SRC_Q8 && tf_q6k_dma_ok(nb, n_cols, col_bytes, use_bias, use_res)) {
+    if (src.kind == TF_SRC_Q8 && tf_q6k_dma_ok(w, nb, n_cols, col_bytes, use_bias, use_res)) {
         auto go = [&](auto nbc, auto rc_, auto sc_) {
             constexpr int NB = decltype(nbc)::value, R = decltype(rc_)::value,
                           S = decltype(sc_)::value;
