@@ -138,6 +138,10 @@ struct tf_model {
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    // kGraphSteps consecutive steps in one graph (fewer graph launches per token)
+    static constexpr int kGraphSteps = 8;
+    hipGraph_t graph_n = nullptr;
+    hipGraphExec_t graph_exec_n = nullptr;
     hipStream_t capture_stream = nullptr;
 
     template <class T>
@@ -148,8 +152,7 @@ struct tf_model {
     }
 
     ~tf_model() {
-        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
-        if (graph) (void)hipGraphDestroy(graph);
+        drop_graph();
         if (capture_stream) (void)hipStreamDestroy(capture_stream);
         for (void* p : allocs) (void)hipFree(p);
     }
@@ -554,25 +557,33 @@ struct tf_model {
     void drop_graph() {
         if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
         if (graph) (void)hipGraphDestroy(graph);
+        if (graph_exec_n) (void)hipGraphExecDestroy(graph_exec_n);
+        if (graph_n) (void)hipGraphDestroy(graph_n);
         graph_exec = nullptr;
         graph = nullptr;
+        graph_exec_n = nullptr;
+        graph_n = nullptr;
     }
 
-    void capture() {
-        if (graph_exec) return;
+    // A graph of `steps` consecutive decode steps (the state advances on the
+    // device, so replaying it runs that many tokens).
+    void capture_steps(int steps, hipGraph_t& g_out, hipGraphExec_t& e_out) {
+        if (e_out) return;
         if (!capture_stream) tf::check((int)hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking), "stream");
         tf::check((int)hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal), "capture");
         try {
-            run_step(capture_stream, 0, 0, true);
+            for (int i = 0; i < steps; i++) run_step(capture_stream, 0, 0, true);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(capture_stream, &g);
             if (g) (void)hipGraphDestroy(g);
             throw;
         }
-        tf::check((int)hipStreamEndCapture(capture_stream, &graph), "end capture");
-        tf::check((int)hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "instantiate");
+        tf::check((int)hipStreamEndCapture(capture_stream, &g_out), "end capture");
+        tf::check((int)hipGraphInstantiate(&e_out, g_out, nullptr, nullptr, 0), "instantiate");
     }
+
+    void capture() { capture_steps(1, graph, graph_exec); }
 
     // Runs n_forced + max(n_gen, 1) - 1 steps from position pos0 with
     // device-resident state; tokens[i] = argmax of step n_forced - 1 + i.
@@ -601,10 +612,19 @@ struct tf_model {
                 drop_graph();
             }
         }
-        if (use_graph) capture();
-        for (int i = 0; i < total; i++) {
-            if (use_graph) tf::check((int)hipGraphLaunch(graph_exec, s), "graph launch");
-            else run_step(s, 0, 0, true);
+        if (use_graph) {
+            capture();
+            if (total >= kGraphSteps) capture_steps(kGraphSteps, graph_n, graph_exec_n);
+        }
+        for (int i = 0; i < total;) {
+            if (use_graph && total - i >= kGraphSteps) {
+                tf::check((int)hipGraphLaunch(graph_exec_n, s), "graph launch");
+                i += kGraphSteps;
+            } else {
+                if (use_graph) tf::check((int)hipGraphLaunch(graph_exec, s), "graph launch");
+                else run_step(s, 0, 0, true);
+                i++;
+            }
         }
         if (n_gen > 0 && tokens)
             tf::check((int)hipMemcpyAsync(tokens, d_log + n_forced - 1, sizeof(int) * n_gen,
@@ -860,10 +880,7 @@ extern "C" int tf_model_set_path(tf_model* m, int path) {
     if (path >= 1 && !m->kquant_ok()) return (int)hipErrorNotSupported;
     if (m->path != path) {
         m->path = path;
-        if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
-        if (m->graph) (void)hipGraphDestroy(m->graph);
-        m->graph_exec = nullptr;
-        m->graph = nullptr;
+        m->drop_graph();
     }
     return 0;
 }
