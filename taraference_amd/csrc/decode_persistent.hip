@@ -683,6 +683,7 @@ template <int SPR, int IT>
 struct TfPQkvRegs {
     TfQ4kRow<IT> a, b;
     TfQ6kPart v[IT];
+    float b0, b1;  // the biases of the task's rows (loaded with the weights)
 };
 
 struct TfPQkvGeo {
@@ -719,6 +720,8 @@ __device__ __forceinline__ void tf_p_qkv_load(TfPA& a, TfPL& L, int task,
             const uint8_t* col = row < g.n_q ? L.wq + (size_t)row * L.cb_qk
                                              : L.wk + (size_t)(row - g.n_q) * L.cb_qk;
             tf_q4k_row_load<SPR, IT>(col, valid, 0, nb, ln.sir, ln.t, r.a);
+            const float* bias = row < g.n_q ? L.bq : L.bk;
+            if (bias) r.b0 = tf_gld(bias + (row < g.n_q ? row : row - g.n_q));
         } else {
             const int r0 = (task / half) * hd + task % half, r1 = r0 + half;
             const bool is_q = r0 < g.n_q;
@@ -728,11 +731,17 @@ __device__ __forceinline__ void tf_p_qkv_load(TfPA& a, TfPL& L, int task,
                                      r.a);
             tf_q4k_row_load<SPR, IT>(base + (size_t)(r1 - off) * L.cb_qk, true, 0, nb, ln.sir, ln.t,
                                      r.b);
+            const float* bias = is_q ? L.bq : L.bk;
+            if (bias) {
+                r.b0 = tf_gld(bias + (r0 - off));
+                r.b1 = tf_gld(bias + (r1 - off));
+            }
         }
     } else {
         const int j = (task - g.pair_tasks) * UNITS + ln.unit;
         const bool valid = j < g.n_v;
         const uint8_t* col = L.wv + (size_t)(valid ? j : 0) * L.cb_v;
+        if (L.bv) r.b0 = tf_gld(L.bv + (valid ? j : 0));
         if (L.v_q6k) {
 #pragma unroll
             for (int i = 0; i < IT; i++) {
@@ -767,7 +776,7 @@ __device__ __forceinline__ void tf_p_qkv_task(TfPA& a, TfPL& L, int task, int po
             float acc = tf_q4k_row_partial<SPR, IT>(r.a, valid, 0, nb, ln.sir, ln.t, x);
             acc = tf_group_sum<4 * SPR>(acc);
             const float* bias = is_q ? L.bq : L.bk;
-            if (valid && bias) acc += tf_gld(bias + (is_q ? row : row - g.n_q));
+            if (valid && bias) acc += r.b0;
             const float other = __shfl(acc, ln.lane ^ (4 * SPR), 64);
             const float x0 = member == 0 ? acc : other;
             const float x1 = member == 0 ? other : acc;
@@ -792,8 +801,8 @@ __device__ __forceinline__ void tf_p_qkv_task(TfPA& a, TfPL& L, int task, int po
             float x1 = tf_group_sum<64>(tf_q4k_row_partial<SPR, IT>(r.b, true, 0, nb, ln.sir, ln.t, x));
             const float* bias = is_q ? L.bq : L.bk;
             if (bias) {
-                x0 += tf_gld(bias + (r0 - off));
-                x1 += tf_gld(bias + (r1 - off));
+                x0 += r.b0;
+                x1 += r.b1;
             }
             float y0, y1;
             tf_p_rope(x0, x1, i, y0, y1);
@@ -825,7 +834,7 @@ __device__ __forceinline__ void tf_p_qkv_task(TfPA& a, TfPL& L, int task, int po
             acc = tf_group_sum<4 * SPR>(tf_q4k_row_partial<SPR, IT>(r.a, valid, 0, nb, ln.sir, ln.t, x));
         }
         if (valid && lead) {
-            if (L.bv) acc += tf_gld(L.bv + j);
+            if (L.bv) acc += r.b0;
             const uint16_t hv = tf_f2h_halfup(acc);
             *(TF_GAS uint16_t*)(L.v_cache + (size_t)pos * stride + j) = hv;
             tf_p_put(fkv + tf_p_kv_k(j, hd) + hd, hv, tkv);
@@ -930,6 +939,7 @@ __device__ __forceinline__ void tf_p_rows_prefetch(const uint8_t* w, int cb, int
 template <int SPR, int IT, bool Q6, int D, int EPI, class Res>
 __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, int n_rows,
                                               const TfAct& x, TfPRow<IT, Q6> (&r)[D], Res res,
+                                              float res_first,
                                               unsigned long long* fout, unsigned tag,
                                               float* out, unsigned long long* amax) {
     constexpr int UNITS = 16 / SPR;
@@ -952,7 +962,7 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
             acc = tf_group_sum<4 * SPR>(acc);
             if (valid && lead) {
                 if constexpr (EPI == 0) {
-                    tf_p_putf(fout + j, acc + res(j), tag);
+                    tf_p_putf(fout + j, acc + (task == wid ? res_first : res(j)), tag);
                 } else {
                     *(TF_GAS float*)(out + j) = acc;
                     const unsigned long long k = tf_argmax_key(acc, j);
@@ -1919,8 +1929,13 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     const int cwid = (wave - 1) * (int)gridDim.x + (int)blockIdx.x, ncw = gridDim.x * TF_P_CW;
     float nw[NS][4];
     tf_p_norm_wload4<NS>(L.attn_norm, a.E, nw);
-    TfPQkvRegs<SPR, IT> rq;
-    if (wave != 0) tf_p_qkv_load<SPR, IT>(a, L, cwid, rq);
+    // the first two tasks of the wave are loaded before the poll (a wave has
+    // two when the rows outnumber the compute waves, e.g. the 7B widths)
+    TfPQkvRegs<SPR, IT> rq0, rq1;
+    if (wave != 0) {
+        tf_p_qkv_load<SPR, IT>(a, L, cwid, rq0);
+        tf_p_qkv_load<SPR, IT>(a, L, cwid + ncw, rq1);
+    }
     float* raw = tf_p_raw(lds, nbE);
     tf_p_stamp(a, 5 * li, 0);
     __syncthreads();  // the previous stage's LDS readers are done
@@ -1953,9 +1968,12 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     unsigned long long* fq = tf_p_vec(a, TF_PK_Q, li);
     unsigned long long* fkv = tf_p_vec(a, TF_PK_KV, li);
     const unsigned tq = tf_p_tag(tb, li, TF_PK_Q), tkv = tf_p_tag(tb, li, TF_PK_KV);
-    for (int task = cwid; task < g.n_tasks; task += ncw) {
-        if (task != cwid) tf_p_qkv_load<SPR, IT>(a, L, task, rq);
-        tf_p_qkv_task<SPR, IT>(a, L, task, pos, xE, rq, fq, fkv, tq, tkv);
+    if (cwid < g.n_tasks) tf_p_qkv_task<SPR, IT>(a, L, cwid, pos, xE, rq0, fq, fkv, tq, tkv);
+    if (cwid + ncw < g.n_tasks)
+        tf_p_qkv_task<SPR, IT>(a, L, cwid + ncw, pos, xE, rq1, fq, fkv, tq, tkv);
+    for (int task = cwid + 2 * ncw; task < g.n_tasks; task += ncw) {
+        tf_p_qkv_load<SPR, IT>(a, L, task, rq0);
+        tf_p_qkv_task<SPR, IT>(a, L, task, pos, xE, rq0, fq, fkv, tq, tkv);
     }
     tf_p_stamp(a, 5 * li, 3, 64);
     return true;
@@ -2057,6 +2075,9 @@ __device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int
     const TfAct xE = tf_act_view(lds, nbE);
     TfPRow<IT, false> ro[1];
     tf_p_rows_prefetch<SPR, IT, false, 1>(L.wo, L.cb_o, nbE, a.E, ro);
+    // the residual of the wave's first row (polled by the QKV stage already)
+    const int j0 = tf_p_wid() * (16 / SPR) + tf_p_lane<SPR>().unit;
+    const float res0 = j0 < a.E ? tf_p_res_in(a, li, tb, token, j0) : 0.f;
     tf_p_stamp(a, 5 * li + 2, 0);
     __syncthreads();  // the previous stage's LDS readers are done
     if (!tf_p_poll_q8img<(9 * 4096 / 32 + TF_P_THREADS - 1) / TF_P_THREADS>(
@@ -2066,7 +2087,7 @@ __device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int
     tf_p_stamp(a, 5 * li + 2, 2);
     tf_p_rows_run<SPR, IT, false, 1, 0>(
         L.wo, L.cb_o, nbE, a.E, xE, ro, [&](int j) { return tf_p_res_in(a, li, tb, token, j); },
-        tf_p_vec(a, TF_PK_XA, li), tf_p_tag(tb, li, TF_PK_XA), nullptr, nullptr);
+        res0, tf_p_vec(a, TF_PK_XA, li), tf_p_tag(tb, li, TF_PK_XA), nullptr, nullptr);
     tf_p_stamp(a, 5 * li + 2, 3);
     return true;
 }
@@ -2132,6 +2153,10 @@ __device__ __forceinline__ bool tf_p_down_body(TfPA& a, TfPL& L, int li, unsigne
     const TfAct xF = tf_act_view(lds, nbF);
     TfPRow<IT, Q6> rd[1];
     tf_p_rows_prefetch<SPR, IT, Q6, 1>(L.down, L.cb_down, nbF, a.E, rd);
+    // the residual of the wave's first row (polled by the gate/up stage already)
+    const unsigned long long* xm = tf_p_vec(a, TF_PK_XA, li);
+    const int j0 = tf_p_wid() * (16 / SPR) + tf_p_lane<SPR>().unit;
+    const float res0 = __uint_as_float((unsigned)tf_ldc64(xm + (j0 < a.E ? j0 : 0)));
     tf_p_stamp(a, 5 * li + 4, 0);
     __syncthreads();  // the previous stage's LDS readers are done
     // Q8 h: 9 words per 32 values, one pass (up to 19456 values: nbF <= 76)
@@ -2140,10 +2165,9 @@ __device__ __forceinline__ bool tf_p_down_body(TfPA& a, TfPL& L, int li, unsigne
         return false;
     tf_p_stamp(a, 5 * li + 4, 1);
     tf_p_stamp(a, 5 * li + 4, 2);  // (no staging: h arrives in Q8)
-    const unsigned long long* xm = tf_p_vec(a, TF_PK_XA, li);
     tf_p_rows_run<SPR, IT, Q6, 1, 0>(
         L.down, L.cb_down, nbF, a.E, xF, rd,
-        [&](int j) { return __uint_as_float((unsigned)tf_ldc64(xm + j)); },
+        [&](int j) { return __uint_as_float((unsigned)tf_ldc64(xm + j)); }, res0,
         tf_p_vec(a, TF_PK_XB, li), tf_p_tag(tb, li, TF_PK_XB), nullptr, nullptr);
     tf_p_stamp(a, 5 * li + 4, 3);
     return true;
