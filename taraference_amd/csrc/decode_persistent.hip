@@ -1380,6 +1380,49 @@ __device__ __forceinline__ void tf_p_attn_dma_prime(TfPL& L, const TfPAttnGeo& g
     if (wave + TF_P_WAVES < n16) tf_p_attn_dma_tile(L, g, stride, lds, wave + TF_P_WAVES, 1);
 }
 
+// Short splits (one 64-token tile, four waves per head: wph = 4, wave w
+// scoring the 16 tokens of slice w % 4): waves 0-3 copy slice w HBM -> LDS
+// into slot w (the layout of tf_p_attn_dma_tile) before the stage's barrier,
+// above the QKV stage's activation image, and the q poll's closing barrier
+// publishes the slots; the tile then needs neither register staging nor
+// barriers of its own.  Offsets relative to tf_p_dt_base.
+struct TfPDtLayout {
+    static constexpr int SLOT = TfPDmaLayout::SLOT;
+    static constexpr int Q = 4 * SLOT;                    // q [8][HD] f32
+    static constexpr int P = Q + 8 * TF_P_HD * 4;         // p [8][TILE]
+    static constexpr int C = P + 8 * TF_P_TILE * 4;       // slice combine
+    static constexpr int BYTES = C + TF_P_WAVES * (2 + TF_P_HD) * 4;
+};
+__host__ __device__ __forceinline__ int tf_p_dt_base(int E) {
+    return (tf_act_lds_bytes(E / 256, true) + 4 * E + 1023) & ~1023;
+}
+__device__ __forceinline__ bool tf_p_attn_dt(const TfPAttnGeo& g) {
+    return g.tpw == 1 && g.wph == 4;
+}
+// Slice rows past the split load its last row, and the row `pos` (produced
+// in this launch) is read from the polled K/V row instead of its slot.
+__device__ __forceinline__ void tf_p_attn_dt_issue(TfPL& L, const TfPAttnGeo& g, int stride,
+                                                   uint8_t* lds) {
+    const int lane = tf_p_tid() & 63, wave = tf_p_tid() >> 6;
+    const int n = lane & 15, r4 = lane >> 4;
+    const uint16_t* kb = L.k_cache + (size_t)g.kh * TF_P_HD;
+    const uint16_t* vb = L.v_cache + (size_t)g.kh * TF_P_HD;
+    if (wave >= 4) return;
+    const int t0 = g.t_begin + 16 * wave;
+    const uint32_t base = tf_lds_off(lds) + wave * TfPDtLayout::SLOT;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * i + r4;
+        const int t = min(t0 + r, g.t_end - 1);
+        tf_lds_dma16(kb + (size_t)t * stride + 8 * (n ^ r), base + 1024 * i);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = min(t0 + 4 * i + r4, g.t_end - 1);
+        tf_lds_dma16(vb + (size_t)t * stride + 8 * n, base + 4096 + TfPDmaLayout::VBLK * i);
+    }
+}
+
 // The split's tiles after the q poll; leaves head hd's (m, l) and O dims
 // 2 lane, 2 lane + 1 in m, l, o0, o1 of wave hd (valid).
 __device__ __forceinline__ void tf_p_attn_dma_run(TfPA& a, TfPL& L, const TfPAttnGeo& g,
@@ -1655,10 +1698,13 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     // matrix-core tiles copied HBM -> LDS per wave, for a single head group
     // with one wave per head (long contexts)
     const bool mm = MM && g.n_hg == 1 && g.wph == 1;
+    const bool dt = !mm && tf_p_attn_dt(g);
     uint16_t* k_lds = reinterpret_cast<uint16_t*>(lds);
     uint16_t* v_lds = reinterpret_cast<uint16_t*>(lds + LA::K_BYTES);
-    float* q_lds = reinterpret_cast<float*>(mm ? lds + TfPDmaLayout::Q
-                                               : lds + LA::K_BYTES + LA::V_BYTES);
+    uint8_t* dtl = lds + tf_p_dt_base(a.E);  // the short-split area
+    float* q_lds = reinterpret_cast<float*>(mm   ? lds + TfPDmaLayout::Q
+                                            : dt ? dtl + TfPDtLayout::Q
+                                                 : lds + LA::K_BYTES + LA::V_BYTES);
     float* p_lds = q_lds + 8 * HD;
     // the first two tiles of this wave go out before the poll: the K/V
     // stream overlaps the wait for q
@@ -1689,10 +1735,74 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     const int ti = lane % T, ds = lane / T;      // score lane: token ti, dim slice ds
     float m = TF_P_NEG_BIG, l = 0.f, o0 = 0.f, o1 = 0.f;
     const float scale = a.scale;
-    float* cm = reinterpret_cast<float*>(lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES +
-                                         LA::P_BYTES);  // [wave][2 + HD]
+    float* cm = reinterpret_cast<float*>(
+        dt ? dtl + TfPDtLayout::C
+           : lds + LA::K_BYTES + LA::V_BYTES + LA::Q_BYTES + LA::P_BYTES);  // [wave][2 + HD]
     if (mm) tf_p_attn_dma_run(a, L, g, pos, stride, lds, q_lds, valid, hd, m, l, o0, o1);
-    for (int it = 0; it < (mm ? 0 : g.tpw); it++) {
+    if (dt && valid && g.t_begin < g.t_end) {
+        // the arithmetic of the tile loop below, operands from the wave's slot
+        const uint8_t* slot = dtl + sl * TfPDtLayout::SLOT;
+        const int t0 = g.t_begin, ts = t0 + 16 * sl, t = ts + ti;
+        const bool tv = t < g.t_end;
+        const float* qh = q_lds + hd * HD + 32 * ds;
+        float sa[4];
+#pragma unroll
+        for (int dd = 0; dd < 4; dd++) {
+            const tf_u32x4 kw =
+                t == pos ? *reinterpret_cast<const tf_u32x4*>(tf_p_knew + 32 * ds + 8 * dd)
+                         : *reinterpret_cast<const tf_u32x4*>(slot + 256 * ti +
+                                                              16 * ((4 * ds + dd) ^ ti));
+            const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * dd);
+            const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * dd + 4);
+            float acc = 0.f;
+            acc += qa.x * tf_h2f(kw.x);
+            acc += qa.y * tf_h2f(kw.x >> 16);
+            acc += qa.z * tf_h2f(kw.y);
+            acc += qa.w * tf_h2f(kw.y >> 16);
+            acc += qb.x * tf_h2f(kw.z);
+            acc += qb.y * tf_h2f(kw.z >> 16);
+            acc += qb.z * tf_h2f(kw.w);
+            acc += qb.w * tf_h2f(kw.w >> 16);
+            sa[dd] = acc;
+        }
+        float sd = (sa[0] + sa[1]) + (sa[2] + sa[3]);
+        sd += tf_swap16(sd);
+        sd += __shfl_xor(sd, 32, 64);
+        const float sv = tv ? sd * scale : TF_P_NEG_BIG;
+        const float m_new = fmaxf(m, tf_wave_max(sv));
+        const float alpha = __expf(m - m_new);
+        const float e = tv ? __expf(sv - m_new) : 0.f;
+        if (lane < 16) p_lds[wave * TF_P_TILE + ti] = e;
+        l = l * alpha + tf_group_sum<64>(lane < 16 ? e : 0.f);
+        m = m_new;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int tlen = max(0, min(16, g.t_end - ts));
+        const float* pw = p_lds + wave * TF_P_TILE;
+        const uint32_t vnew = reinterpret_cast<const uint32_t*>(tf_p_vnew)[lane];
+        float c0[4] = {0.f, 0.f, 0.f, 0.f}, c1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 16; tt += 4) {
+            if (tt < tlen) {  // wave-uniform
+                const float4 pv = *reinterpret_cast<const float4*>(pw + tt);
+                const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int tok = tt + u;  // rows past the split count as zeros
+                    uint32_t vv = *reinterpret_cast<const uint32_t*>(
+                        slot + 4096 + TfPDmaLayout::VBLK * (tok >> 2) + 256 * (tok & 3) + 4 * lane);
+                    vv = ts + tok == pos ? vnew : vv;
+                    vv = tok < tlen ? vv : 0u;
+                    c0[u] = fmaf(pp[u], tf_h2f(vv), c0[u]);
+                    c1[u] = fmaf(pp[u], tf_h2f(vv >> 16), c1[u]);
+                }
+            }
+        }
+        o0 = o0 * alpha + ((c0[0] + c0[1]) + (c0[2] + c0[3]));
+        o1 = o1 * alpha + ((c1[0] + c1[1]) + (c1[2] + c1[3]));
+    }
+    for (int it = 0; it < (mm || dt ? 0 : g.tpw); it++) {
         const int t0 = g.t_begin + it * TF_P_TILE;
         __syncthreads();  // the previous tile is consumed
 #pragma unroll
@@ -2042,7 +2152,9 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     }
     TfPAttnRegs ra;
     // (the matrix-core path copies its tiles HBM -> LDS after the barrier)
-    if (!(MM && g.n_hg == 1 && g.wph == 1))
+    if (tf_p_attn_dt(g))
+        tf_p_attn_dt_issue(L, g, a.KV * TF_P_HD, lds + tf_p_dt_base(a.E));
+    else if (!(MM && g.n_hg == 1 && g.wph == 1))
         tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
     __syncthreads();  // the previous stage's LDS readers are done
@@ -2307,7 +2419,8 @@ int tf_p_lds(const TfPArgs& a) {
     int b = tf_act_lds_bytes(nbE, true) + 4 * a.E;
     const int f = tf_act_lds_bytes(nbF, true);
     if (f > b) b = f;
-    const int at = TfPAttnLayout::BYTES;
+    const int dt = tf_p_dt_base(a.E) + TfPDtLayout::BYTES;
+    const int at = TfPAttnLayout::BYTES > dt ? TfPAttnLayout::BYTES : dt;
     b = at > b ? at : b;
     // the warm-up's scratch (tf_p_gu_warm)
     return TF_P_WARM_LDS + TF_P_WAVES * 1024 > b ? TF_P_WARM_LDS + TF_P_WAVES * 1024 : b;
