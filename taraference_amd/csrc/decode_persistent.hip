@@ -1003,8 +1003,13 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 // issue order, so a poll issued behind a weight prefetch would also wait for
 // all of that prefetch; with the roles split the input is staged as soon as
 // it arrives, and each compute wave then consumes its tasks one by one as
-// their weights land.
+// their weights land (QKV).
 #define TF_P_CW (TF_P_WAVES - 1)
+// Gate/up, whose compute is VALU-bound, is the exception: wave 0 polls and
+// quantizes and also computes a share of the tasks, so each SIMD carries two
+// waves' tasks (with seven compute waves one SIMD had one and the other three
+// two).  Wave 0's poll waits for its own prefetch, which the warm-up has
+// mostly brought into the L2.
 #ifndef TF_P_GU_D
 #define TF_P_GU_D 3
 #endif
@@ -1019,7 +1024,7 @@ struct TfPGuMap {
     static constexpr int JPW = SPR <= 8 ? 16 / SPR / 2 : 1;  // outputs per task
     static constexpr int HMAX = SPR <= 8 ? 3 : 5;            // half-groups per workgroup
     // tasks per compute wave, and register sets in flight
-    static constexpr int K = (16 * HMAX + TF_P_CW * JPW - 1) / (TF_P_CW * JPW);
+    static constexpr int K = (16 * HMAX + TF_P_WAVES * JPW - 1) / (TF_P_WAVES * JPW);
     static constexpr int D = SPR <= 8 ? TF_P_GU_D : 4;
     static_assert(JPW >= 1 && JPW <= 2, "gate/up lane map needs SPR >= 4");
 };
@@ -1039,10 +1044,10 @@ __device__ __forceinline__ TfPGuSpan tf_p_gu_span(TfPA& a) {
 }
 
 // Output (index into the workgroup's outputs, 16 s + o is the row) of task q
-// of compute wave cw, for this lane's unit.
+// of wave cw, for this lane's unit.
 template <int SPR>
 __device__ __forceinline__ int tf_p_gu_out(int cw, int q, int unit) {
-    const int u = cw + TF_P_CW * q;
+    const int u = cw + TF_P_WAVES * q;
     if constexpr (SPR <= 8) return u * TfPGuMap<SPR>::JPW + (unit >> 1);
     else return u;
 }
@@ -1053,7 +1058,7 @@ __device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int n_out, int j0
                                              TfPGuRegs<IT>& r) {
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    const int o = tf_p_gu_out<SPR>((tf_p_tid() >> 6) - 1, q, ln.unit);
+    const int o = tf_p_gu_out<SPR>(tf_p_tid() >> 6, q, ln.unit);
     const int j = j0 + (o < n_out ? o : 0);
     if constexpr (SPR <= 8) {
         const uint8_t* w = (ln.unit & 1) ? L.up : L.gate;
@@ -1095,7 +1100,7 @@ __device__ __forceinline__ void tf_p_put_oct(unsigned long long* dst, int g, int
     if (j == 0) tf_p_put(dst + 9 * g + 8, __float_as_uint(r.d), tag);
 }
 
-// Compute-wave part of gate/up: h = silu(gate) * up of this wave's outputs
+// Gate/up tasks of this wave: h = silu(gate) * up of the wave's outputs
 // into tf_p_hbuf (and, for the first half-group when it is the second half
 // of a group, into the exchange area).  r holds tasks 0 .. D - 1 on entry.
 template <int SPR, int IT>
@@ -1106,7 +1111,7 @@ __device__ __forceinline__ void tf_p_gu_compute(TfPA& a, TfPL& L, const TfAct& x
     using M = TfPGuMap<SPR>;
     const TfPLane ln = tf_p_lane<SPR>();
     const int nb = a.E / 256;
-    const int cw = (tf_p_tid() >> 6) - 1;
+    const int cw = tf_p_tid() >> 6;
     const int n_out = 16 * (sp.e - sp.s);
     const int j0 = 16 * sp.s < a.F ? 16 * sp.s : 0;
     const bool sends = (sp.s & 1) && n_out > 0;  // half-group s is a second half
@@ -2222,37 +2227,33 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     // the norm weights first: waiting for them does not wait for the weights
     float nw[NS][4];
     tf_p_norm_wload4<NS>(L.ffn_norm, a.E, nw);
+    const int n_out = 16 * (sp.e - sp.s);
+    const int j0 = 16 * sp.s < a.F ? 16 * sp.s : 0;
+    TfPGuRegs<IT> rg[M::D];
+#pragma unroll
+    for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
+    if (wave == 0) tf_p_stamp(a, 5 * li + 3, 0);
+    __syncthreads();  // the previous stage's LDS readers are done
     if (wave == 0) {
-        tf_p_stamp(a, 5 * li + 3, 0);
-        __syncthreads();  // the previous stage's LDS readers are done
         // E <= 256 SPR: 4 SPR words per lane, in passes of up to 32
         constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
         const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
                                                tf_p_tag(tb, li, TF_PK_XA), a.eps);
         if (tf_p_tid() == 0) tf_p_rms = sc;
         tf_p_stamp(a, 5 * li + 3, 1);
-        __syncthreads();  // raw row and scale in LDS
-        if (tf_p_flag) return false;
-        tf_p_stage8b<false, true, NS>(lds, nbE, raw, sc, nw);
-        tf_p_stamp(a, 5 * li + 3, 2);
-        tf_p_gu_exchange(a, sp, fx, tag_x);
-        __syncthreads();  // h of every compute wave in LDS
-        if (tf_p_flag) return false;
+    }
+    __syncthreads();  // raw row and scale in LDS
+    if (tf_p_flag) return false;
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
+    if (wave == 0) tf_p_stamp(a, 5 * li + 3, 2);
+    tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
+    // wave 0 takes the second half of a group whose first half ends the span
+    if (wave == 0) tf_p_gu_exchange(a, sp, fx, tag_x);
+    __syncthreads();  // h of every wave in LDS
+    if (tf_p_flag) return false;
+    if (wave == 0) {
         tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H));
         tf_p_stamp(a, 5 * li + 3, 3);
-    } else {
-        const int n_out = 16 * (sp.e - sp.s);
-        const int j0 = 16 * sp.s < a.F ? 16 * sp.s : 0;
-        TfPGuRegs<IT> rg[M::D];
-#pragma unroll
-        for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
-        __syncthreads();  // the previous stage's LDS readers are done
-        __syncthreads();  // raw row and scale in LDS
-        if (tf_p_flag) return false;
-        tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
-        tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
-        __syncthreads();  // h of every compute wave in LDS
-        if (tf_p_flag) return false;
     }
     return true;
 }
