@@ -1010,6 +1010,12 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 // waves' tasks (with seven compute waves one SIMD had one and the other three
 // two).  Wave 0's poll waits for its own prefetch, which the warm-up has
 // mostly brought into the L2.
+// Gate/up tasks in flight per wave: 3 at SPR <= 8; 2 at SPR = 16 (7B widths,
+// where the rows are not warmed into the L2 and a deeper prefetch holds up
+// the x' poll: 2 / 3 / 4 / 5 gave 511 / 509 / 493 / 491 tok/s on config 4).
+#ifndef TF_P_GU_D16
+#define TF_P_GU_D16 2
+#endif
 #ifndef TF_P_GU_D
 #define TF_P_GU_D 3
 #endif
@@ -1025,7 +1031,7 @@ struct TfPGuMap {
     static constexpr int HMAX = SPR <= 8 ? 3 : 5;            // half-groups per workgroup
     // tasks per compute wave, and register sets in flight
     static constexpr int K = (16 * HMAX + TF_P_WAVES * JPW - 1) / (TF_P_WAVES * JPW);
-    static constexpr int D = SPR <= 8 ? TF_P_GU_D : 4;
+    static constexpr int D = SPR <= 8 ? TF_P_GU_D : TF_P_GU_D16;
     static_assert(JPW >= 1 && JPW <= 2, "gate/up lane map needs SPR >= 4");
 };
 
