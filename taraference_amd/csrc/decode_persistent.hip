@@ -577,6 +577,29 @@ __device__ __forceinline__ float tf_p_poll_rms(TfPA& a, float* dst, const unsign
 // The four partials of a lane advance together, four terms at a time with
 // their LDS reads issued first; a padded term adds fmaf(0, 0, p) = p
 // exactly (p >= +0), so the value is that of the plain per-partial loop.
+__device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps);
+
+// The RMSNorm input polled by every wave (K words per thread) into raw; wave 0
+// then forms the scale from LDS in the reference's order (tf_p_rms_scale:
+// the same sums as tf_p_poll_rms) into tf_p_rms.  Every thread calls it;
+// false (everywhere): aborted.  The caller's next barrier publishes tf_p_rms.
+#ifndef TF_P_AWP
+#define TF_P_AWP 1
+#endif
+template <int K>
+__device__ __forceinline__ bool tf_p_poll_rms_wg(TfPA& a, float* raw,
+                                                 const unsigned long long* src, int n,
+                                                 unsigned tag, float eps) {
+    if (!tf_p_poll<K, 1>([&](int i, uint32_t b) { raw[i] = __uint_as_float(b); }, src, n, tag,
+                         tf_p_tid(), TF_P_THREADS, a))
+        return false;
+    if ((tf_p_tid() >> 6) == 0) {
+        const float sc = tf_p_rms_scale(raw, n, eps);
+        if (tf_p_tid() == 0) tf_p_rms = sc;
+    }
+    return true;
+}
+
 __device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps) {
     const int lane = tf_p_tid() & 63;
     const int nj = n / 256;
@@ -2073,6 +2096,10 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
             const float sc = tf_p_rms_scale(raw, a.E, a.eps);
             if (tid == 0) tf_p_rms = sc;
         }
+    } else if constexpr (TF_P_AWP != 0) {
+        if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
+                                       tf_p_tag(tb, li - 1, TF_PK_XB), a.eps))
+            return false;
     } else if (wave == 0) {
         constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
         const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
@@ -2240,7 +2267,12 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    if (wave == 0) {
+    if constexpr (TF_P_AWP != 0) {
+        if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
+                                       tf_p_tag(tb, li, TF_PK_XA), a.eps))
+            return false;
+        if (wave == 0) tf_p_stamp(a, 5 * li + 3, 1);
+    } else if (wave == 0) {
         // E <= 256 SPR: 4 SPR words per lane, in passes of up to 32
         constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
         const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
