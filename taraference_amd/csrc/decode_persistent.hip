@@ -499,74 +499,8 @@ __device__ __forceinline__ void tf_p_stage8b(uint8_t* lds, int nb, const float* 
     __syncthreads();
 }
 
-// LDS word carrying the RMS scale from the polling wave to the others.
+// LDS word carrying the RMS scale from wave 0 to the others.
 __shared__ float tf_p_rms;
-
-// Wave-level poll of n flagged f32 words into LDS (dst[i]) that also forms
-// the reference's RMS partials on the way: lane l takes words l + 64 k, in
-// passes of PK words, and p[k mod 4] accumulates their squares in k order --
-// partial t = l + 64 c of the reference sums x[t], x[t + 256], ... in turn,
-// which is p[c] of lane l.  Padding past n adds nothing (fmaf(0, 0, p) = p).
-// Returns 1 / sqrt(mean + eps) on every lane; a time-out or abort sets
-// tf_p_flag (the caller reads it after its next barrier).
-template <int PK, int PP>
-__device__ __forceinline__ float tf_p_poll_rms(TfPA& a, float* dst, const unsigned long long* src,
-                                               int n, unsigned tag, float eps) {
-    const int lane = tf_p_tid() & 63;
-    float p[4] = {0.f, 0.f, 0.f, 0.f};
-    bool bad = n > 64 * PK * PP;
-#pragma unroll
-    for (int pp = 0; pp < PP; pp++) {
-        unsigned long long v[PK];
-        auto load = [&]() {
-#pragma unroll
-            for (int k = 0; k < PK; k++) {
-                const int i = lane + 64 * (pp * PK + k);
-                v[k] = tf_ldc64(src + (i < n ? i : 0));
-            }
-        };
-        load();
-        for (int spins = 0; !bad;) {
-            bool miss = false;
-#pragma unroll
-            for (int k = 0; k < PK; k++)
-                miss |= (unsigned)(v[k] >> 32) != tag && lane + 64 * (pp * PK + k) < n;
-            if (!__builtin_amdgcn_ballot_w64(miss)) break;
-            if (++spins > TF_SPIN_LIMIT || ((spins & 15) == 0 && tf_ldu(a.bar + TF_BAR_ABORT))) {
-                bad = true;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-            load();
-        }
-#pragma unroll
-        for (int k = 0; k < PK; k++) {
-            const int kk = pp * PK + k, i = lane + 64 * kk;
-            if (i < n) {
-                const float x = __uint_as_float((unsigned)v[k]);
-                dst[i] = x;
-                p[kk & 3] = fmaf(x, x, p[kk & 3]);
-            }
-        }
-    }
-    if (bad) {
-        tf_p_abort(a);
-        tf_p_flag = 1;
-    }
-    // red = (p0 + p2) + (p1 + p3), then the shift-down tree over offsets 32,
-    // 16, 8, 4, 2, 1 (lane 0 adds the value of lane k at each step): here as
-    // exchanges with lane ^ 32, ^ 16 and row rotations by 8 and 4 (the lanes
-    // they pair hold equal values after the earlier steps) and quad swaps, so
-    // every lane forms lane 0's sum
-    float v = (p[0] + p[2]) + (p[1] + p[3]);
-    v += __shfl_xor(v, 32, 64);
-    v += tf_swap16(v);
-    v += tf_dpp<TF_DPP_ROW_ROR8>(v);
-    v += tf_dpp<TF_DPP_ROW_ROR4>(v);
-    v += tf_dpp<TF_DPP_QUAD_2301>(v);
-    v += tf_dpp<TF_DPP_QUAD_1032>(v);
-    return 1.0f / sqrtf(v / (float)n + eps);
-}
 
 // 1 / sqrt(mean(x^2) + eps) of the n values x[0 .. n) in LDS, computed by
 // each wave on its own in the reference's order (kernels/ops.cu:4-34):
@@ -577,29 +511,6 @@ __device__ __forceinline__ float tf_p_poll_rms(TfPA& a, float* dst, const unsign
 // The four partials of a lane advance together, four terms at a time with
 // their LDS reads issued first; a padded term adds fmaf(0, 0, p) = p
 // exactly (p >= +0), so the value is that of the plain per-partial loop.
-__device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps);
-
-// The RMSNorm input polled by every wave (K words per thread) into raw; wave 0
-// then forms the scale from LDS in the reference's order (tf_p_rms_scale:
-// the same sums as tf_p_poll_rms) into tf_p_rms.  Every thread calls it;
-// false (everywhere): aborted.  The caller's next barrier publishes tf_p_rms.
-#ifndef TF_P_AWP
-#define TF_P_AWP 1
-#endif
-template <int K>
-__device__ __forceinline__ bool tf_p_poll_rms_wg(TfPA& a, float* raw,
-                                                 const unsigned long long* src, int n,
-                                                 unsigned tag, float eps) {
-    if (!tf_p_poll<K, 1>([&](int i, uint32_t b) { raw[i] = __uint_as_float(b); }, src, n, tag,
-                         tf_p_tid(), TF_P_THREADS, a))
-        return false;
-    if ((tf_p_tid() >> 6) == 0) {
-        const float sc = tf_p_rms_scale(raw, n, eps);
-        if (tf_p_tid() == 0) tf_p_rms = sc;
-    }
-    return true;
-}
-
 __device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps) {
     const int lane = tf_p_tid() & 63;
     const int nj = n / 256;
@@ -630,6 +541,26 @@ __device__ __forceinline__ float tf_p_rms_scale(const float* x, int n, float eps
     v = tf_readlane(v, 0);
     return 1.0f / sqrtf(v / (float)n + eps);
 }
+
+// The RMSNorm input polled by every wave (K words per thread) into raw; wave 0
+// then forms the scale from LDS in the reference's order (tf_p_rms_scale)
+// into tf_p_rms.  Every thread calls it; false (everywhere): aborted.  The
+// caller's next barrier publishes tf_p_rms.  (A poll by wave 0 alone, forming
+// the squares while it polls, saw the vector 0.35-0.45 us later.)
+template <int K>
+__device__ __forceinline__ bool tf_p_poll_rms_wg(TfPA& a, float* raw,
+                                                 const unsigned long long* src, int n,
+                                                 unsigned tag, float eps) {
+    if (!tf_p_poll<K, 1>([&](int i, uint32_t b) { raw[i] = __uint_as_float(b); }, src, n, tag,
+                         tf_p_tid(), TF_P_THREADS, a))
+        return false;
+    if ((tf_p_tid() >> 6) == 0) {
+        const float sc = tf_p_rms_scale(raw, n, eps);
+        if (tf_p_tid() == 0) tf_p_rms = sc;
+    }
+    return true;
+}
+
 
 // The 8 norm weights a lane applies in tf_p_stage8's single step (values
 // 512 wave + 8 lane .. +7), loaded with the stage's weight prefetch.
@@ -1021,18 +952,16 @@ __device__ __forceinline__ void tf_p_rows_run(const uint8_t* w, int cb, int nb, 
 // reads them.  Published group g: words 9 g .. 9 g + 7 hold the 32 Q8 bytes
 // (little-endian, 4 per word), word 9 g + 8 the scale d8.
 
-// Wave 0 of a workgroup polls the stage's input; the other waves (the
-// compute waves) own the GEMV tasks.  A wave's memory counter completes in
-// issue order, so a poll issued behind a weight prefetch would also wait for
-// all of that prefetch; with the roles split the input is staged as soon as
-// it arrives, and each compute wave then consumes its tasks one by one as
-// their weights land (QKV).
+// QKV: waves 1-7 (the compute waves) own the GEMV tasks; every wave polls
+// the stage's input, and wave 0, which has no weights in flight (a wave's
+// memory counter completes in issue order, so its poll would wait for them
+// too), forms the RMS scale.
 #define TF_P_CW (TF_P_WAVES - 1)
-// Gate/up, whose compute is VALU-bound, is the exception: wave 0 polls and
-// quantizes and also computes a share of the tasks, so each SIMD carries two
-// waves' tasks (with seven compute waves one SIMD had one and the other three
-// two).  Wave 0's poll waits for its own prefetch, which the warm-up has
-// mostly brought into the L2.
+// Gate/up, whose compute is VALU-bound: every wave prefetches, polls and
+// computes a share of the tasks, so each SIMD carries two waves' tasks (with
+// seven compute waves one SIMD had one and the other three two); wave 0 also
+// quantizes h.  The prefetch the polls wait for comes mostly from the L2 the
+// warm-up filled.
 // Gate/up tasks in flight per wave: 3 at SPR <= 8; 2 at SPR = 16 (7B widths,
 // where the rows are not warmed into the L2 and a deeper prefetch holds up
 // the x' poll: 2 / 3 / 4 / 5 gave 511 / 509 / 493 / 491 tok/s on config 4).
@@ -2069,7 +1998,7 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     const int nbE = a.E / 256, tid = tf_p_tid(), wave = tid >> 6;
     constexpr int NS = SPR <= 8 ? 1 : 2;
     const TfAct xE = tf_act_view(lds, nbE);
-    // compute waves 1 .. 7 of every workgroup share the tasks; wave 0 polls
+    // compute waves 1 .. 7 of every workgroup share the tasks
     const int cwid = (wave - 1) * (int)gridDim.x + (int)blockIdx.x, ncw = gridDim.x * TF_P_CW;
     float nw[NS][4];
     tf_p_norm_wload4<NS>(L.attn_norm, a.E, nw);
@@ -2096,15 +2025,9 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
             const float sc = tf_p_rms_scale(raw, a.E, a.eps);
             if (tid == 0) tf_p_rms = sc;
         }
-    } else if constexpr (TF_P_AWP != 0) {
-        if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
-                                       tf_p_tag(tb, li - 1, TF_PK_XB), a.eps))
-            return false;
-    } else if (wave == 0) {
-        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
-        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
-                                               tf_p_tag(tb, li - 1, TF_PK_XB), a.eps);
-        if (tid == 0) tf_p_rms = sc;
+    } else if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XB, li - 1), a.E,
+                                          tf_p_tag(tb, li - 1, TF_PK_XB), a.eps)) {
+        return false;
     }
     tf_p_stamp(a, 5 * li, 1);
     __syncthreads();  // raw row and scale in LDS
@@ -2267,19 +2190,11 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     for (int d = 0; d < M::D; d++) tf_p_gu_load<SPR, IT>(a, L, n_out, j0, d, rg[d]);
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    if constexpr (TF_P_AWP != 0) {
-        if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
-                                       tf_p_tag(tb, li, TF_PK_XA), a.eps))
-            return false;
-        if (wave == 0) tf_p_stamp(a, 5 * li + 3, 1);
-    } else if (wave == 0) {
-        // E <= 256 SPR: 4 SPR words per lane, in passes of up to 32
-        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
-        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
-                                               tf_p_tag(tb, li, TF_PK_XA), a.eps);
-        if (tf_p_tid() == 0) tf_p_rms = sc;
-        tf_p_stamp(a, 5 * li + 3, 1);
-    }
+    // E <= 256 SPR: SPR / 2 words per thread
+    if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XA, li), a.E,
+                                   tf_p_tag(tb, li, TF_PK_XA), a.eps))
+        return false;
+    if (wave == 0) tf_p_stamp(a, 5 * li + 3, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
     tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
@@ -2358,12 +2273,9 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     float* raw = tf_p_raw(lds, nbE);
     tf_p_stamp(a, 5 * L, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    if (wave == 0) {
-        constexpr int PK = 4 * SPR < 32 ? 4 * SPR : 32, PP = 4 * SPR / PK;
-        const float sc = tf_p_poll_rms<PK, PP>(a, raw, tf_p_vec(a, TF_PK_XB, L - 1), a.E,
-                                               tf_p_tag(tb, L - 1, TF_PK_XB), a.eps);
-        if (tid == 0) tf_p_rms = sc;
-    }
+    if (!tf_p_poll_rms_wg<SPR / 2>(a, raw, tf_p_vec(a, TF_PK_XB, L - 1), a.E,
+                                   tf_p_tag(tb, L - 1, TF_PK_XB), a.eps))
+        return false;
     tf_p_stamp(a, 5 * L, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
