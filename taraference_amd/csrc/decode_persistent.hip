@@ -141,6 +141,15 @@ __device__ __forceinline__ int tf_p_wid() {
 // Tags grow with the launch generation; the runtime zeroes the buffers
 // (tag 0, never expected) whenever it resets the generation.
 
+// lm_head tasks in flight per wave (3 / 4 / 5: 1019 / 1020 / 1013 tok/s) and the
+// all-wave polls' s_sleep between rounds (2 / 4 / 8: no measurable change)
+#ifndef TF_P_HEAD_D
+#define TF_P_HEAD_D 4
+#endif
+#ifndef TF_P_SLEEP
+#define TF_P_SLEEP 4
+#endif
+
 enum TfPKind {
     TF_PK_XA = 0, TF_PK_XB = 1, TF_PK_Q = 2, TF_PK_KV = 3, TF_PK_O = 4, TF_PK_H = 5, TF_PK_PART = 6,
     TF_PK_HX = 7
@@ -231,7 +240,7 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, Src src, int n, unsigned tag,
                 bad = 1;
                 break;
             }
-            __builtin_amdgcn_s_sleep(4);
+            __builtin_amdgcn_s_sleep(TF_P_SLEEP);
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const int i = i0 + k * R;
@@ -2261,7 +2270,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     TfPA& a = *pa;
     const int nbE = a.E / 256, tid = tf_p_tid(), L = a.n_layer;
     const TfAct xE = tf_act_view(lds, nbE);
-    constexpr int D = 4, NS = SPR <= 8 ? 1 : 2;
+    constexpr int D = TF_P_HEAD_D, NS = SPR <= 8 ? 1 : 2;
     const int wave = tid >> 6, nwv = gridDim.x * TF_P_WAVES, w0 = tf_p_wid();
     const int n_tasks = (a.n_vocab + 16 / SPR - 1) / (16 / SPR);
     float nw[NS][4];
