@@ -2007,8 +2007,12 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     const int nbE = a.E / 256, tid = tf_p_tid(), wave = tid >> 6;
     constexpr int NS = SPR <= 8 ? 1 : 2;
     const TfAct xE = tf_act_view(lds, nbE);
-    // compute waves 1 .. 7 of every workgroup share the tasks
-    const int cwid = (wave - 1) * (int)gridDim.x + (int)blockIdx.x, ncw = gridDim.x * TF_P_CW;
+    // compute waves 1 .. 7 of every workgroup share the tasks, dealt in the
+    // wave order 1, 5, 2, 3, 4, 6, 7: waves w and w + 4 share a SIMD, so with
+    // five tasks per workgroup (the 3B widths) the two on one SIMD are the
+    // first ones, and the last (the heavier Q6_K x f32 V rows) runs alone
+    const int wrank = wave == 5 ? 1 : (wave >= 2 && wave <= 4 ? wave : wave - 1);
+    const int cwid = wrank * (int)gridDim.x + (int)blockIdx.x, ncw = gridDim.x * TF_P_CW;
     float nw[NS][4];
     tf_p_norm_wload4<NS>(L.attn_norm, a.E, nw);
     // the first two tasks of the wave are loaded before the poll (a wave has
