@@ -2073,8 +2073,9 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
 // and the gate/up stage's weight loads, and the drain of its prefetch ahead of
 // the x' poll, then run from L2.  The copies start TF_P_WARM_DELAY x 10 ns
 // after the stage starts, once the attention workgroups' q poll is done (its
-// round trip slows under the extra traffic; 0.5 / 1.0 / 1.5 / 2.0 us gave
-// 1019 / 1023 / 1007 / 980 tok/s), and each wave keeps at most
+// round trip slows under the extra traffic; 0.5 / 0.8 / 1.0 / 1.2 / 1.5 /
+// 2.0 us gave 1019 / 1028 / 1025 / 1022 / 1007 / 980 tok/s), and each wave
+// keeps at most
 // 2 TF_P_WARM copies in flight.  Only when the XCD's share fits the L2 with
 // room to spare (gate + up at most 28 MB).  Their own wo poll, about 5 us
 // later, finds the copies drained.
@@ -2082,7 +2083,7 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
 #define TF_P_WARM 4
 #endif
 #ifndef TF_P_WARM_DELAY
-#define TF_P_WARM_DELAY 100
+#define TF_P_WARM_DELAY 80
 #endif
 // scratch above every activation image; it overlaps the short-split attention
 // area, which the warming workgroups (those without attention work) do not use
