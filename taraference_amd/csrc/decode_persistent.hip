@@ -2076,9 +2076,8 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
 // round trip slows under the extra traffic; 0.5 / 0.8 / 1.0 / 1.2 / 1.5 /
 // 2.0 us gave 1019 / 1028 / 1025 / 1022 / 1007 / 980 tok/s), and each wave
 // keeps at most 2 TF_P_WARM copies in flight.  Only when the XCD's share fits
-// the L2 with
-// room to spare (gate + up at most 28 MB).  Their own wo poll, about 5 us
-// later, finds the copies drained.
+// the L2 with room to spare (gate + up at most 28 MB).  Their own wo poll,
+// about 5 us later, finds the copies drained.
 #ifndef TF_P_WARM
 #define TF_P_WARM 4
 #endif
