@@ -37,7 +37,7 @@ DECODE_KERNEL = "tf_decode_persistent_kernel<8,1,16,3> (whole decode step, one l
 # scaled by the same counters' reading on a 256 MiB device copy (FETCH_SIZE
 # counts half of what a read moves here: factor 2.000; WRITE_SIZE factor
 # 1.000); the counter runs are kept in profiles/.
-DECODE_TRAFFIC = int((1050087.0 * 2.0 + 24010.5 * 1.0) * 1024)
+DECODE_TRAFFIC = int((1051398.3 * 2.0 + 24014.9 * 1.0) * 1024)
 # The standalone config-1a GEMV (the tf_gemv_q4k_ffn entry point), reported
 # beside it for the metric's "Q4_K GEMV % of HBM peak" part.
 ROOFLINE_KERNEL = "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU, 2048 -> 2x11008)"
