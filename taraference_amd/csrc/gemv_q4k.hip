@@ -75,8 +75,15 @@ __global__ __launch_bounds__(tf_bt_rows(SPR, SK)) void tf_q4k_rows_kernel(
     int task = wave;
     TfRowSel cs = tf_sel3(m, task * UNITS + unit, n_total, col_bytes);
     TfQ4kRow<ITERS> cur, nxt;
+    // A wide activation (16 super-blocks or more) is staged before the first
+    // weight loads: issued after them, its loads would complete only behind
+    // them (in issue order), and the staging would then lengthen the critical
+    // path (Q6_K 11008 -> 2048: 7.6 -> 7.1 us back to back); a narrow one costs
+    // less than the delay it would add to the weight stream.
+    const bool act_first = nb >= 16;
+    if (act_first) tf_stage_act<false, SK>(src, nb, lds);
     if (ITERS > 0 && task < n_tasks) tf_q4k_row_load<SPR, ITERS>(cs.col, cs.valid, 0, nb, sir, t, cur);
-    tf_stage_act<false, SK>(src, nb, lds);
+    if (!act_first) tf_stage_act<false, SK>(src, nb, lds);
     const TfAct x = tf_act_view(lds, nb);
     for (; task < n_tasks; task += nwaves) {
         const int nt = task + nwaves;
