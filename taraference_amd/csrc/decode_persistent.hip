@@ -587,9 +587,6 @@ __device__ __forceinline__ void tf_p_norm_wload(const float* w, int n, float (&r
     r[7] = __uint_as_float(b.w);
 }
 
-// Weights argument of the stages without a norm (unused).
-__device__ constexpr float tf_p_now[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-
 // Raw (unnormalized) row of a norm stage: an LDS area after the image.
 __device__ __forceinline__ float* tf_p_raw(uint8_t* lds, int nbE) {
     return reinterpret_cast<float*>(lds + tf_act_lds_bytes(nbE, true));
@@ -2275,7 +2272,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     const int nbE = a.E / 256, tid = tf_p_tid(), L = a.n_layer;
     const TfAct xE = tf_act_view(lds, nbE);
     constexpr int D = TF_P_HEAD_D, NS = SPR <= 8 ? 1 : 2;
-    const int wave = tid >> 6, nwv = gridDim.x * TF_P_WAVES, w0 = tf_p_wid();
+    const int nwv = gridDim.x * TF_P_WAVES, w0 = tf_p_wid();
     const int n_tasks = (a.n_vocab + 16 / SPR - 1) / (16 / SPR);
     float nw[NS][4];
     tf_p_norm_wload4<NS>(a.out_norm, a.E, nw);
