@@ -13,6 +13,11 @@ same position (K = 256 by default).  Each step is one full decode forward
 feeds back on the device and the K generated tokens are copied to the host
 once at the end.  value = K / elapsed.
 
+Beside it the same JSON line carries, each as its own guarded leg: the
+prefill rate, the per-kernel table (configs 0-2, a4, lm_head, prefill
+kernels), config 4 (a Qwen2.5-7B-shape model at a 32768-token context,
+128 timed greedy tokens, with its roofline) and the CPU-oracle baseline.
+
 Prints one JSON line on stdout.
 """
 from __future__ import annotations
@@ -117,12 +122,22 @@ def config4(ctx=32768, n_gen=128):
     e1.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    ms_ev = e0.elapsed_time(e1) / n_gen
+    wbytes = synth.weight_bytes(cfg)
+    # attention reads pos + 1 K/V rows at positions ctx .. ctx + n_gen - 1
+    kv = int(2 * cfg["n_layer"] * (ctx + (n_gen + 1) / 2.0) * cfg["n_kv"] * cfg["head_dim"] * 2)
+    gbs = (wbytes + kv) / (ms_ev * 1e-3) / 1e9
     out = {"config": "4: Qwen2.5-7B-shape Q4_K_M, 32768-token context, 128 greedy tokens",
            "path": m.path(), "prefill_tokens": ctx, "prefill_s": round(t_pf, 3),
            "prefill_tok_s": round(ctx / t_pf, 1), "decode_tokens": n_gen,
            "decode_tok_s": round(n_gen / dt, 2), "ms_per_token": round(dt * 1e3 / n_gen, 3),
-           "ms_per_token_events": round(e0.elapsed_time(e1) / n_gen, 3),
-           "weight_bytes_per_token": synth.weight_bytes(cfg),
+           "ms_per_token_events": round(ms_ev, 3),
+           "weight_bytes_per_token": wbytes,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "kernel": "tf_decode_persistent_kernel<16,1,16,5,true> long-context "
+                                  "instantiation (one launch per token)",
+                        "bytes_per_launch": wbytes + kv, "us_per_launch": round(ms_ev * 1e3, 2)},
            "greedy_tokens_head": [int(t) for t in toks[:8]]}
     m.close()
     return out
@@ -203,6 +218,8 @@ def kernel_table(iters, only=None):
         ("cfg0_q4k_896x4864", lambda: B.case_q4k_gemv(896, 4864, 0, iters)),
         ("cfg1a_q4k_gate_up_2048x2x11008", lambda: B.case_q4k_ffn(2048, 11008, 1, iters, False)),
         ("cfg1b_q6k_down_11008x2048", lambda: B.case_q6k(11008, 2048, 2, iters)),
+        # the reference's Q4_K ffn_down (18 of 36 layers): split-K + reduce
+        ("a4_q4k_down_splitk4_11008x2048", lambda: B.case_q4k_splitk(11008, 2048, 14, iters)),
         ("cfg1c_q4k_qkv_2048x2560", lambda: B.case_q4k_qkv(2048, 2048, 256, 3, iters)),
         ("lm_head_q6k_2048x151936", lambda: B.case_q6k(2048, 151936, 6, max(10, iters // 4),
                                                        "tf_gemv_q6k_compact_q8", 0)),
@@ -433,6 +450,8 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-config4", action="store_true",
+                    help="skip the config-4 leg (7B shape, 32768-token context)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--path", type=int, default=None,
                     help="decode kernel sequence (tf_model_set_path); default: the library's")
@@ -571,6 +590,10 @@ def main():
         out["prefill"] = pf
         out["kernels"] = {} if args.no_kernels else _leg("kernels",
                                                          lambda: kernel_table(args.kernel_iters))
+        if not args.no_config4:
+            log("[bench] config 4 ...")
+            out["config4"] = _leg("config4", config4)
+            log(f"[bench] config 4: {out['config4']}")
     out["cpu_baseline"] = (None if args.no_cpu or args.only_decode
                            else _leg("cpu_baseline", lambda: cpu_baseline(cfg, args.cpu_budget)))
     out["greedy_tokens_head"] = [int(t) for t in toks[:8]]

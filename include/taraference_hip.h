@@ -303,9 +303,8 @@ int tf_flash_decode_reduce(const float *partial, float *out, int n_head,
  * split-KV partials, then the log-sum-exp merge (a second kernel); when
  * q8/d8 are non-NULL the merged output is also quantized to Q8 (quantize_q8
  * of the wo GEMV input, matmul.rs:191).  pos0_dev non-NULL reads the position
- * from device memory (graph capture).  counters: n_kv unsigned ints, zero
- * before the first call; every call leaves them zero.  partial as for
- * tf_flash_decode_partial. */
+ * from device memory (graph capture).  counters: reserved, not used (may be
+ * NULL).  partial as for tf_flash_decode_partial. */
 int tf_flash_decode(const float *q, const uint16_t *k_cache,
                     const uint16_t *v_cache, float *partial, unsigned *counters,
                     float *out, int8_t *q8, float *d8, int n_head, int n_kv,
@@ -325,16 +324,24 @@ int tf_gemv_q4k_flash_out(const uint8_t *w, const float *partial, int n_head,
                           int8_t *attn_q8, float *attn_d8, tf_stream_t stream);
 /* No counterpart in the reference: tf_flash_decode for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  The split partials and merge
- * counters live in a static device array of this library (one per GPU,
- * held until the process ends): n_head * n_split * (2 + head_dim) <= 2^20
- * floats and n_kv <= 256, else hipErrorInvalidValue.  Allocates nothing.
+ * loops, harnesses that forbid hipMalloc).  The split partials live in a
+ * static device array of this library (one per GPU, held until the process
+ * ends): n_head * n_split * (2 + head_dim) <= 2^20 floats, else
+ * hipErrorInvalidValue.  Allocates nothing and enqueues nothing but the
+ * flash kernels, so it may be captured into a HIP graph from its first call.
  * Calls that overlap on one GPU share that array and race. */
 int tf_flash_decode_noalloc(const float *q, const uint16_t *k_cache,
                             const uint16_t *v_cache, float *out, int8_t *q8,
                             float *d8, int n_head, int n_kv, int head_dim,
                             int pos0, const int *pos0_dev, int n_split,
                             float scale, tf_stream_t stream);
+/* No counterpart in the reference (a parity check): the persistent decode
+ * step's in-kernel quantizers applied to x[n] (n % 32 == 0), writing the Q8
+ * of quantize_q8_global (kernels/gemv.cu:43-65): variant 0 = the eight-lane
+ * staging of its RMSNorm outputs, 1 = the sixteen-lane quantization of the
+ * attention output and of silu(gate)*up. */
+int tf_decode_step_quantize_q8(const float *x, int n, int variant, int8_t *q,
+                               float *d, tf_stream_t stream);
 /* Partition count this library recommends for a context of max_seq tokens
  * (a multiple of 8; 8 for short contexts).  The reference fixes 8
  * (cuda/decode.rs:38-41); on MI355X long contexts need more partitions to
@@ -551,6 +558,14 @@ const float *tf_model_logits(const tf_model *m);
 int tf_model_keep_stage_vectors(tf_model *m, int on);
 const unsigned long long *tf_model_stage_vector(const tf_model *m, int kind,
                                                 int li);
+/* No counterpart in the reference (a parity check of the persistent step):
+ * with the stage vectors kept, the step also records, for every quantizer
+ * it runs, the f32 values quantized and the Q8 produced.  site 0 = the
+ * normalized input of the QKV GEMVs (li = n_layer: of the lm_head), 1 = the
+ * merged attention output, 2 = the normalized input of gate/up, 3 =
+ * silu(gate)*up; part 0 = f32 values, 1 = int8 q, 2 = f32 d per 32 values.
+ * Device pointer; NULL when not kept or out of range. */
+const void *tf_model_q8_record(const tf_model *m, int site, int li, int part);
 uint16_t *tf_model_k_cache(const tf_model *m, int li);
 uint16_t *tf_model_v_cache(const tf_model *m, int li);
 

@@ -100,6 +100,29 @@ def case_q4k_gemv(n_rows, n_cols, seed, iters):
     return dict(per_us=per, b2b_us=b2b, bytes=alg)
 
 
+def case_q4k_splitk(n_rows, n_cols, seed, iters, n_split=4):
+    """The reference's tall Q4_K path (kernels/gemv.cu:1877 split-K partials
+    + :2243 reduce, in-place residual): two launches per GEMV."""
+    rng = np.random.default_rng(seed)
+    w, cb = synth.q4k_matrix(rng, n_rows, n_cols)
+    ws = _copies(w, w.nbytes)
+    x = _dev(synth.activation(rng, n_rows))
+    xq, xd = _q8(x)
+    part = torch.empty(n_split * n_cols, device="cuda")
+    out = torch.zeros(n_cols, device="cuda")
+    lib = capi.load()
+
+    def launch(i, s):
+        lib.tf_gemv_q4k_q8_splitk(ws[i].data_ptr(), xq.data_ptr(), xd.data_ptr(),
+                                  part.data_ptr(), n_rows, n_cols, cb, n_split, s)
+        lib.tf_gemv_splitk_reduce(part.data_ptr(), out.data_ptr(), n_cols, n_split, 0, None, 2,
+                                  None, s)
+
+    per, b2b = time_launches(launch, len(ws), iters)
+    alg = n_cols * (n_rows // 256) * 144 + n_rows + n_rows // 8 + 8 * n_cols
+    return dict(per_us=per, b2b_us=b2b, bytes=alg)
+
+
 def case_q4k_ffn(n_rows, n_cols, seed, iters, f32_x=True):
     rng = np.random.default_rng(seed)
     g, cb = synth.q4k_matrix(rng, n_rows, n_cols)

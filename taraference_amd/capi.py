@@ -8,7 +8,6 @@ library is missing, loading raises.
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load: shared HIP runtime)
@@ -74,6 +73,7 @@ SIGNATURES: dict[str, list] = {
     "tf_copy_kv_f16": [_P, _P, _I, _P, _I, _P],
     "tf_argmax": [_P, _I, _P, _P],
     "tf_q4k_block_dots": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "tf_decode_step_quantize_q8": [_P, _I, _I, _P, _P, _P],
     "tf_q6k_block_dots": [_P, _I, _P, _P, _I, _I, _I, _P],
     "tf_version": [],
     "tf_exported_symbol_count": [],
@@ -88,12 +88,12 @@ _lib = None
 
 
 def load(path: Path | str | None = None) -> C.CDLL:
-    """Load the HIP library (raises if it has not been built).  TF_HIP_LIB
-    names another build of the same library (A/B measurements)."""
+    """Load the in-tree HIP library (raises if it has not been built).  `path`
+    names another build of the same library; only the first load counts."""
     global _lib
     if _lib is not None:
         return _lib
-    p = Path(path or os.environ.get("TF_HIP_LIB") or LIB_PATH)
+    p = Path(path or LIB_PATH)
     if not p.exists():
         raise FileNotFoundError(
             f"{p} is missing: build it with `python -m taraference_amd.build` "
@@ -131,7 +131,7 @@ def stream_ptr(stream=None) -> int | None:
 BOUND_ELSEWHERE = {"tf_model_create", "tf_model_destroy", "tf_model_forward",
                    "tf_model_generate", "tf_model_set_path", "tf_model_get_path",
                    "tf_model_logits", "tf_model_prefill", "tf_model_keep_stage_vectors",
-                   "tf_model_stage_vector",
+                   "tf_model_stage_vector", "tf_model_q8_record",
                    "tf_model_k_cache", "tf_model_v_cache", "tf_exported_symbol",
                    # taraference_amd/gguf.py
                    "tf_gguf_open", "tf_gguf_close", "tf_gguf_version", "tf_gguf_data_offset",

@@ -275,120 +275,27 @@ __device__ __forceinline__ bool tf_p_poll(Dst dst, Src src, int n, unsigned tag,
 // ((x0+x1)+(x2+x3))+((x4+x5)+(x6+x7)) + ... of the reference staging; and
 // the RMS scale keeps the reference's summation order (below).
 //
-// Lane map: four lanes per 32-value group, lane j of the quad holding values
-// 8j .. 8j+7, so a wave stages 16 groups per step and every group reduction
-// is two quad DPP steps.
+// Lane map: eight lanes per 32-value group, lane j of the group holding
+// values 4j .. 4j+3, so every thread of the workgroup stages four values per
+// step and every group reduction is three DPP steps.
 
-// Q8 of eight values held by one lane of a group quad.
-struct TfQ8Oct {
-    int q[8];
-    float d;
-    int s_half, s_other;  // int sums of q over this lane's 16-value half / the other
-    float f_half;         // f32 sum of x over the half (pairwise tree)
+// Where a quantizer records its input and output when the launch keeps a Q8
+// record (TfPArgs::q8x); all nullptr otherwise.
+struct TfPQ8Rec {
+    float* x;
+    int8_t* q;
+    float* d;
 };
 
-template <bool F32>
-__device__ __forceinline__ TfQ8Oct tf_q8_oct(const float (&x)[8]) {
-    TfQ8Oct r;
-    float am = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
-    uint32_t u = __builtin_bit_cast(uint32_t, am);  // magnitudes order as unsigned ints
-    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)u));
-    u = max(u, (uint32_t)tf_dppi<TF_DPP_QUAD_2301>((int)u));
-    const float amax = __builtin_bit_cast(float, u);
-    r.d = amax * (1.0f / 127.0f);
-    const float rcp = __builtin_amdgcn_rcpf(r.d);
-    // y = x * rcp is within 2^-15 of RN(x / d); far from a .5 tie both round
-    // alike, otherwise (rare) the IEEE quotient decides (as tf_q8_value_r)
-    float y[8];
-    bool rk[8], any = false;
-    const bool tiny = !(r.d >= 1.17549435e-38f);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        y[i] = x[i] * rcp;
-        const float fr = fabsf(y[i] - __builtin_truncf(y[i]));
-        rk[i] = tiny || fabsf(fr - 0.5f) < 6.103515625e-05f;
-        any |= rk[i];
-    }
-    if (any) {
-        const float dd = amax == 0.f ? 1.f : r.d;
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (rk[i]) y[i] = x[i] / dd;
-    }
-    int s = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        r.q[i] = amax == 0.f ? 0 : (int)__builtin_rintf(y[i]);
-        s += r.q[i];
-    }
-    r.s_half = s + tf_dppi<TF_DPP_QUAD_1032>(s);
-    r.s_other = tf_dppi<TF_DPP_QUAD_2301>(r.s_half);
-    r.f_half = 0.f;
-    if (F32) {
-        const float t = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
-        r.f_half = t + tf_dpp<TF_DPP_QUAD_1032>(t);
-    }
-    return r;
-}
-
-// Builds the image from the n = 256 nb values src[0 .. n) in LDS.  NORM
-// multiplies each value by `scale` and by its norm weight first (w holds the
-// lane's 8 weights; rows up to 128 groups, one step) and, with F32, keeps
-// the normalized row and its 16-value sums for the Q6_K x f32 path.  Ends
-// with a workgroup barrier.
-template <bool F32, bool NORM>
-__device__ __forceinline__ void tf_p_stage8(uint8_t* lds, int nb, const float* src, float scale,
-                                            const float (&w)[8]) {
-    int8_t* q8s = reinterpret_cast<int8_t*>(lds);
-    float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
-    float* dss = d8s + nb * 8;
-    int32_t* s16 = reinterpret_cast<int32_t*>(dss + nb * 8);
-    float* xf = reinterpret_cast<float*>(s16 + nb * 16);
-    float* xs16 = xf + nb * 256;
-    const int Gq = nb * 8;
-    const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6, j = lane & 3;
-    constexpr int STEP = 16 * TF_P_WAVES;  // groups per step
-    for (int s0 = 0; s0 < Gq; s0 += STEP) {
-        const int g = s0 + wave * 16 + (lane >> 2);
-        const int e = 32 * (g < Gq ? g : Gq - 1) + 8 * j;
-        const float4 a = *reinterpret_cast<const float4*>(src + e);
-        const float4 b = *reinterpret_cast<const float4*>(src + e + 4);
-        float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        if (NORM) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) x[i] = x[i] * scale * w[i];
-        }
-        const TfQ8Oct r = tf_q8_oct<F32>(x);
-        if (g < Gq) {
-            uint32_t lo = 0, hi = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                lo |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
-                hi |= (uint32_t)(r.q[4 + i] & 0xff) << (8 * i);
-            }
-            *reinterpret_cast<uint2*>(q8s + tf_q8_pad(e)) = make_uint2(lo, hi);
-            if ((j & 1) == 0) {
-                s16[2 * g + (j >> 1)] = r.s_half;
-                if (F32) xs16[2 * g + (j >> 1)] = r.f_half;
-            }
-            if (j == 0) {
-                d8s[g] = r.d;
-                dss[g] = r.d * (float)(r.s_half + r.s_other);
-            }
-            if (F32 && NORM) {
-                *reinterpret_cast<float4*>(xf + e) = make_float4(x[0], x[1], x[2], x[3]);
-                *reinterpret_cast<float4*>(xf + e + 4) = make_float4(x[4], x[5], x[6], x[7]);
-            }
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ TfPQ8Rec tf_p_q8rec(TfPA& a, int li, int site, bool on = true) {
+    if (!a.q8x || !on) return TfPQ8Rec{nullptr, nullptr, nullptr};
+    const size_t off = ((size_t)li * 4 + site) * (size_t)a.q8n;
+    return TfPQ8Rec{a.q8x + off, a.q8q + off, a.q8d + off / 32};
 }
 
 // Q8 of four values held by one lane of an 8-lane group (lane j = lane & 7
-// holds values 4 j .. 4 j + 3 of the 32): the quantization of tf_q8_oct
-// spread over twice the lanes.  s_half: int sum over the lane's 16-value
+// holds values 4 j .. 4 j + 3 of the 32): per value the rule of
+// tf_q8_value_r, with the IEEE quotients of a lane taken in one branch.  s_half: int sum over the lane's 16-value
 // half (lanes 0-3 or 4-7), s_other: the other half's; f_half the f32 sum of
 // the half in the pairwise tree ((x0 + x1) + (x2 + x3)) + ... .
 struct TfQ8Quad {
@@ -411,7 +318,7 @@ __device__ __forceinline__ TfQ8Quad tf_q8_g8(const float (&x)[4]) {
     const float amax = __builtin_bit_cast(float, u);
     r.d = amax * (1.0f / 127.0f);
     const float rcp = __builtin_amdgcn_rcpf(r.d);
-    // as tf_q8_oct: the product is exact enough away from a .5 tie; near one
+    // as tf_q8_value_r: the product is exact enough away from a .5 tie; near one
     // (rare) the IEEE quotient decides
     float y[4];
     bool rk[4], any = false;
@@ -462,12 +369,14 @@ __device__ __forceinline__ void tf_p_norm_wload4(const float* w, int n, float (&
     }
 }
 
-// tf_p_stage8 with eight lanes per group: every thread of the workgroup
-// takes four values per step (NS steps cover 4 TF_P_THREADS NS values).
+// The activation image of the n = 256 nb values src[0 .. n) in LDS, eight
+// lanes per group (tf_q8_g8): every thread of the workgroup takes four
+// values per step (NS steps cover 4 TF_P_THREADS NS values).
 // Ends with a workgroup barrier.
 template <bool F32, bool NORM, int NS>
 __device__ __forceinline__ void tf_p_stage8b(uint8_t* lds, int nb, const float* src, float scale,
-                                             const float (&w)[NS][4]) {
+                                             const float (&w)[NS][4],
+                                             TfPQ8Rec rec = TfPQ8Rec{nullptr, nullptr, nullptr}) {
     int8_t* q8s = reinterpret_cast<int8_t*>(lds);
     float* d8s = reinterpret_cast<float*>(lds + TF_Q8_LDS_BYTES(nb));
     float* dss = d8s + nb * 8;
@@ -503,6 +412,11 @@ __device__ __forceinline__ void tf_p_stage8b(uint8_t* lds, int nb, const float* 
                 dss[g] = r.d * (float)(r.s_half + r.s_other);
             }
             if (F32 && NORM) *reinterpret_cast<float4*>(xf + e) = make_float4(x[0], x[1], x[2], x[3]);
+            if (rec.x) {  // workgroup-uniform (the Q8 record)
+                *reinterpret_cast<float4*>(rec.x + e) = make_float4(x[0], x[1], x[2], x[3]);
+                *reinterpret_cast<uint32_t*>(rec.q + e) = b;
+                if (j == 0) rec.d[g] = r.d;
+            }
         }
     }
     __syncthreads();
@@ -570,22 +484,6 @@ __device__ __forceinline__ bool tf_p_poll_rms_wg(TfPA& a, float* raw,
     return true;
 }
 
-
-// The 8 norm weights a lane applies in tf_p_stage8's single step (values
-// 512 wave + 8 lane .. +7), loaded with the stage's weight prefetch.
-__device__ __forceinline__ void tf_p_norm_wload(const float* w, int n, float (&r)[8]) {
-    const int e0 = 8 * tf_p_tid();
-    const int e = e0 < n ? e0 : 0;
-    const tf_u32x4 a = tf_ld16(w + e), b = tf_ld16(w + e + 4);
-    r[0] = __uint_as_float(a.x);
-    r[1] = __uint_as_float(a.y);
-    r[2] = __uint_as_float(a.z);
-    r[3] = __uint_as_float(a.w);
-    r[4] = __uint_as_float(b.x);
-    r[5] = __uint_as_float(b.y);
-    r[6] = __uint_as_float(b.z);
-    r[7] = __uint_as_float(b.w);
-}
 
 // Raw (unnormalized) row of a norm stage: an LDS area after the image.
 __device__ __forceinline__ float* tf_p_raw(uint8_t* lds, int nbE) {
@@ -1035,33 +933,24 @@ __device__ __forceinline__ void tf_p_gu_load(TfPA& a, TfPL& L, int n_out, int j0
 
 // Publishes the Q8 of one 32-value group held as two values per lane of a
 // 16-lane row (tf_q8_pair layout, the quantization of tf_quantize_q8) in the
-// tf_p_put_oct word layout: group G_ at words 9 G_ ... ; m = lane & 15.
+// 9-word group layout: group G_ at words 9 G_ ... ; m = lane & 15.
 __device__ __forceinline__ void tf_p_put_pair16_if(unsigned long long* dst, int G_, int m,
-                                                   float v0, float v1, unsigned tag, bool put) {
+                                                   float v0, float v1, unsigned tag, bool put,
+                                                   const TfPQ8Rec& rec) {
     const TfQ8Pair r = tf_q8_pair<false>(v0, v1);
     const uint32_t h16 = (uint32_t)(r.q0 & 0xff) | ((uint32_t)(r.q1 & 0xff) << 8);
     const uint32_t other = (uint32_t)tf_dppi<TF_DPP_QUAD_1032>((int)h16);  // lane m ^ 1
     if (put && (m & 1) == 0) tf_p_put(dst + 9 * G_ + (m >> 1), h16 | (other << 16), tag);
     if (put && m == 0) tf_p_put(dst + 9 * G_ + 8, __float_as_uint(r.d), tag);
+    if (rec.x && put) {  // the Q8 record
+        *reinterpret_cast<float2*>(rec.x + 32 * G_ + 2 * m) = make_float2(v0, v1);
+        *reinterpret_cast<uint16_t*>(rec.q + 32 * G_ + 2 * m) = (uint16_t)h16;
+        if (m == 0) rec.d[G_] = r.d;
+    }
 }
 __device__ __forceinline__ void tf_p_put_pair16(unsigned long long* dst, int G_, int m, float v0,
-                                                float v1, unsigned tag) {
-    tf_p_put_pair16_if(dst, G_, m, v0, v1, tag, true);
-}
-
-// Publishes the Q8 of one 32-value group held as 8 values per lane of a
-// quad (tf_q8_oct layout): words 9 g + 2 j, + 1 and (lane j = 0) the scale.
-__device__ __forceinline__ void tf_p_put_oct(unsigned long long* dst, int g, int j,
-                                             const TfQ8Oct& r, unsigned tag) {
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        lo |= (uint32_t)(r.q[i] & 0xff) << (8 * i);
-        hi |= (uint32_t)(r.q[4 + i] & 0xff) << (8 * i);
-    }
-    tf_p_put(dst + 9 * g + 2 * j, lo, tag);
-    tf_p_put(dst + 9 * g + 2 * j + 1, hi, tag);
-    if (j == 0) tf_p_put(dst + 9 * g + 8, __float_as_uint(r.d), tag);
+                                                float v1, unsigned tag, const TfPQ8Rec& rec) {
+    tf_p_put_pair16_if(dst, G_, m, v0, v1, tag, true, rec);
 }
 
 // Gate/up tasks of this wave: h = silu(gate) * up of the wave's outputs
@@ -1135,16 +1024,16 @@ __device__ __forceinline__ void tf_p_gu_exchange(TfPA& a, const TfPGuSpan& sp,
 // wave takes group g0 + k, two values per lane (tf_q8_pair: the same Q8 as
 // tf_quantize_q8), so the quantization is a few dozen instructions.
 __device__ __forceinline__ void tf_p_gu_quantize(const TfPGuSpan& sp, unsigned long long* fh,
-                                                 unsigned tag) {
+                                                 unsigned tag, const TfPQ8Rec& rec) {
     const int lane = tf_p_tid() & 63;
     const int g0 = (sp.s + 1) >> 1, ng = ((sp.e + 1) >> 1) - g0;
     const int k = lane >> 4, m = lane & 15;  // row k: group g0 + k, values 2 m, 2 m + 1
     const int o = k < ng ? 16 * (2 * (g0 + k) - sp.s) + 2 * m : 0;
     const float2 v = *reinterpret_cast<const float2*>(tf_p_hbuf + o);
-    tf_p_put_pair16_if(fh, g0 + k, m, v.x, v.y, tag, k < ng);
+    tf_p_put_pair16_if(fh, g0 + k, m, v.x, v.y, tag, k < ng, rec);
 }
 
-// Polls a Q8 vector published as 9-word groups (tf_p_put_oct layout) into the
+// Polls a Q8 vector published as 9-word groups (tf_p_put_pair16 layout) into the
 // LDS image of nb super-blocks, then forms the per-16 sums (s16) and
 // d8 * sum32 (ds) exactly as tf_stage_act does for a Q8 source.
 template <int K>
@@ -1583,7 +1472,7 @@ __device__ __forceinline__ void tf_p_attn_dma_run(TfPA& a, TfPL& L, const TfPAtt
 // added in wave order through LDS.
 __device__ __forceinline__ bool tf_p_attn_merge_wg(TfPA& a, const TfPAttnGeo& g,
                                                    unsigned long long* fo, unsigned to,
-                                                   unsigned tp) {
+                                                   unsigned tp, const TfPQ8Rec& rec) {
     constexpr int HD = TF_P_HD;
     constexpr size_t PS = 2 + HD;
     constexpr int KM = TF_P_MAX_SPLIT / TF_P_WAVES;  // splits per wave at most
@@ -1646,7 +1535,7 @@ __device__ __forceinline__ bool tf_p_attn_merge_wg(TfPA& a, const TfPAttnGeo& g,
             }
             const float den = fmaxf(Lt, 1e-20f);
             const int og = ((g.kh * G + h) * HD + 2 * lane) / 32;
-            tf_p_put_pair16(fo, og, lane & 15, B0 / den, B1 / den, to);
+            tf_p_put_pair16(fo, og, lane & 15, B0 / den, B1 / den, to, rec);
         }
         __syncthreads();  // red is reused by the next head
     }
@@ -1664,6 +1553,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     constexpr int HD = TF_P_HD;
     const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KV, stride = a.KV * HD;
+    const TfPQ8Rec rec = tf_p_q8rec(a, (sk - 1) / 5, 1);
     // matrix-core tiles copied HBM -> LDS per wave, for a single head group
     // with one wave per head (long contexts)
     const bool mm = MM && g.n_hg == 1 && g.wph == 1;
@@ -1885,7 +1775,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     if (g.n_ws == 1) {
         if (own) {
             const float den = fmaxf(l, 1e-20f);
-            tf_p_put_pair16(fo, og, lane & 15, o0 / den, o1 / den, to);
+            tf_p_put_pair16(fo, og, lane & 15, o0 / den, o1 / den, to, rec);
         }
         return true;
     }
@@ -1901,7 +1791,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         tf_p_putf(pp + 2 + 2 * lane, o0, tp);
         tf_p_putf(pp + 3 + 2 * lane, o1, tp);
     }
-    if (mm) return tf_p_attn_merge_wg(a, g, fo, to, tp);
+    if (mm) return tf_p_attn_merge_wg(a, g, fo, to, tp, rec);
     if (!own || hd % g.n_ws != g.ws) return true;
     // lane s holds split s's (m, l); lane = dims 2 lane, 2 lane + 1 for O.
     // M = max_s m_s; w_s = e^(m_s - M); L = sum_s w_s l_s; O = sum_s w_s O_s
@@ -1958,7 +1848,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
         }
     }
     const float den = fmaxf(Lt, 1e-20f);
-    tf_p_put_pair16(fo, og, lane & 15, A0 / den, A1 / den, to);
+    tf_p_put_pair16(fo, og, lane & 15, A0 / den, A1 / den, to, rec);
     return true;
 }
 
@@ -2042,7 +1932,7 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     tf_p_stamp(a, 5 * li, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<true, true, NS>(lds, nbE, raw, tf_p_rms, nw);
+    tf_p_stage8b<true, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, li, 0, blockIdx.x == 0));
     tf_p_stamp(a, 5 * li, 2);
     if (wave == 0) return true;
     const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
@@ -2210,7 +2100,7 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, li, 2, blockIdx.x == 0));
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 2);
     tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
     // wave 0 takes the second half of a group whose first half ends the span
@@ -2218,7 +2108,7 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     __syncthreads();  // h of every wave in LDS
     if (tf_p_flag) return false;
     if (wave == 0) {
-        tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H));
+        tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H), tf_p_q8rec(a, li, 3));
         tf_p_stamp(a, 5 * li + 3, 3);
     }
     return true;
@@ -2292,7 +2182,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     tf_p_stamp(a, 5 * L, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw);
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, L, 0, blockIdx.x == 0));
     tf_p_stamp(a, 5 * L, 2);
     tf_p_rows_ring<SPR, IT, true, D, 1>(a.head, a.head_cb, nbE, a.n_vocab, xE, rh, w0, nwv,
                                         [](int) { return 0.f; }, nullptr, 0u, a.logits, a.amax,
@@ -2488,4 +2378,51 @@ int tf_decode_persistent_launch(const TfPArgs& a, const TfPArgs* dev, int host_m
                         : tf_p_call<decltype(v)::value, false>(a, &l, stream, nullptr, nullptr);
     });
     return rc < 0 ? (int)hipErrorInvalidValue : rc;
+}
+
+// ------------------------------------------------ quantizer check entry
+//
+// The step's two in-kernel quantizers applied to a plain f32 vector, so that
+// their bytes can be compared with tf_quantize_q8 (kernels/gemv.cu:43-65) on
+// chosen inputs (near-ties, subnormal scales, zero groups): variant 0 is the
+// eight-lane staging of the norm inputs (tf_q8_g8, four values per lane),
+// variant 1 the sixteen-lane form of the attention output and of h
+// (tf_q8_pair, two values per lane).
+__global__ __launch_bounds__(256) void tf_p_q8_check_kernel(const float* __restrict__ x,
+                                                             int8_t* __restrict__ q,
+                                                             float* __restrict__ d, int n,
+                                                             int variant) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (variant == 0) {
+        const int e = 4 * t;  // groups never straddle a workgroup (256 x 4 = 32 x 32)
+        const bool live = e < n;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = live ? x[e + i] : 0.f;
+        const TfQ8Quad r = tf_q8_g8<false>(v);
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[e + i] = (int8_t)r.q[i];
+            if ((t & 7) == 0) d[e / 32] = r.d;
+        }
+    } else {
+        const int e = 2 * t;
+        const bool live = e < n;
+        const TfQ8Pair r = tf_q8_pair<false>(live ? x[e] : 0.f, live ? x[e + 1] : 0.f);
+        if (live) {
+            q[e] = (int8_t)r.q0;
+            q[e + 1] = (int8_t)r.q1;
+            if ((t & 15) == 0) d[e / 32] = r.d;
+        }
+    }
+}
+
+extern "C" int tf_decode_step_quantize_q8(const float* x, int n, int variant, int8_t* q,
+                                          float* d, tf_stream_t stream) {
+    TF_CHECK_ARG(x && q && d && n > 0 && n % 32 == 0 && (variant == 0 || variant == 1));
+    const int per = variant == 0 ? 4 : 2;  // values per thread
+    const int threads = n / per;
+    hipLaunchKernelGGL(tf_p_q8_check_kernel, dim3((threads + 255) / 256), dim3(256), 0,
+                       tf_stream(stream), x, q, d, n, variant);
+    return TF_LAUNCH_RESULT();
 }

@@ -75,6 +75,17 @@ struct TfPArgs {
     int *pos, *step, *token;
     const int *forced, *nforced;
     int* log;
+    // optional Q8 record (nullptr = off): for layer slot li (0 .. n_layer;
+    // slot n_layer is the lm_head input) and site s (0 QKV input, 1 attention
+    // output, 2 gate/up input, 3 silu(gate) * up), the f32 values one of the
+    // kernel's quantizers consumed and the Q8 it produced, at offset
+    // (4 li + s) q8n (q8x, q8q) and (4 li + s) q8n / 32 (q8d).  Each value
+    // is written by the workgroup that quantized it (workgroup 0 for the
+    // inputs every workgroup quantizes alike).
+    float* q8x;
+    int8_t* q8q;
+    float* q8d;
+    int q8n;
 };
 
 // True when the kernel has an instantiation for this shape.

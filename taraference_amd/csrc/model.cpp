@@ -22,6 +22,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <algorithm>
 #include <cstdlib>
 #include <memory>
 #include <new>
@@ -121,6 +122,11 @@ struct tf_model {
     unsigned long long* p_flags = nullptr;  // the flagged stage vectors
     bool p_keep = false;  // one copy of them per layer (tf_model_keep_stage_vectors)
     size_t p_flag_words = 0;
+    // the Q8 record of the step's quantizers (TfPArgs::q8x), kept with the
+    // stage vectors
+    float *p_q8x = nullptr, *p_q8d = nullptr;
+    int8_t* p_q8q = nullptr;
+    int p_q8n = 0;
     // diagnostic stage timeline of the persistent step: when the environment
     // names a file in TF_P_TRACE, the last step of each run() is written there
     unsigned long long* d_trace = nullptr;
@@ -448,6 +454,13 @@ struct tf_model {
                              (size_t)c.n_ff);
         p_flags = alloc<unsigned long long>(p_flag_words);
         p_part_words = (size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim);
+        if (p_keep) {
+            p_q8n = std::max({c.n_embd, c.n_ff, c.n_head * c.head_dim});
+            const size_t n = ((size_t)c.n_layer + 1) * 4 * (size_t)p_q8n;
+            p_q8x = alloc<float>(n);
+            p_q8q = alloc<int8_t>(n);
+            p_q8d = alloc<float>(n / 32);
+        }
         p_part = alloc<unsigned long long>(p_part_words);
         if (std::getenv("TF_P_TRACE")) {
             trace_words = (size_t)(5 * c.n_layer + 2) * TF_P_MAX_WG * 4;
@@ -521,6 +534,10 @@ struct tf_model {
         a.bar = d_bar;
         a.err = d_perr;
         a.trace = d_trace;
+        a.q8x = p_q8x;
+        a.q8q = p_q8q;
+        a.q8d = p_q8d;
+        a.q8n = p_q8n;
         a.argmax = d_argmax;
         a.pos = d_pos;
         a.step = d_step;
@@ -904,6 +921,16 @@ extern "C" const unsigned long long* tf_model_stage_vector(const tf_model* m, in
     case 5: return a.fh + (size_t)li * a.F;                 // silu(gate)*up, Q8 groups
     default: return nullptr;
     }
+}
+
+extern "C" const void* tf_model_q8_record(const tf_model* m, int site, int li, int part) {
+    if (!m || !m->p_keep || !m->p_q8x || site < 0 || site > 3 || li < 0 ||
+        li > m->cfg.n_layer || part < 0 || part > 2)
+        return nullptr;
+    const size_t off = ((size_t)li * 4 + (size_t)site) * (size_t)m->p_q8n;
+    if (part == 0) return m->p_q8x + off;
+    if (part == 1) return m->p_q8q + off;
+    return m->p_q8d + off / 32;
 }
 
 extern "C" const float* tf_model_logits(const tf_model* m) { return m ? m->logits : nullptr; }

@@ -164,6 +164,8 @@ static const char* const k_symbols[] = {
     "tf_model_logits",
     "tf_model_keep_stage_vectors",
     "tf_model_stage_vector",
+    "tf_model_q8_record",
+    "tf_decode_step_quantize_q8",
     "tf_model_k_cache",
     "tf_model_v_cache",
     "tf_q4k_block_dots",

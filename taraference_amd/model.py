@@ -62,6 +62,8 @@ def _bind(lib):
     lib.tf_model_keep_stage_vectors.restype = C.c_int
     lib.tf_model_stage_vector.argtypes = [C.c_void_p, C.c_int, C.c_int]
     lib.tf_model_stage_vector.restype = C.c_void_p
+    lib.tf_model_q8_record.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int]
+    lib.tf_model_q8_record.restype = C.c_void_p
     lib.tf_model_logits.argtypes = [C.c_void_p]
     lib.tf_model_logits.restype = C.c_void_p
     for n in ("tf_model_k_cache", "tf_model_v_cache"):
@@ -273,6 +275,24 @@ class DecodeModel:
             raise capi.HipError(f"tf_model_keep_stage_vectors returned {rc}")
 
     STAGE_XA, STAGE_XB, STAGE_Q, STAGE_O, STAGE_H = 0, 1, 2, 4, 5
+    Q8_QKV_IN, Q8_ATTN, Q8_GU_IN, Q8_H = 0, 1, 2, 3
+
+    def q8_record(self, site: int, layer: int):
+        """What the last persistent step's quantizer at `site` consumed and
+        produced in layer `layer` (layer n_layer, site Q8_QKV_IN: the lm_head
+        input): (f32 x[n], int8 q[n], f32 d[n/32]).  Needs keep_stage_vectors."""
+        c = self.cfg
+        n = {0: c["n_embd"], 1: c["n_head"] * c["head_dim"], 2: c["n_embd"], 3: c["n_ff"]}[site]
+        ptrs = [self.lib.tf_model_q8_record(self.h, site, layer, part) for part in range(3)]
+        if not all(ptrs):
+            raise capi.HipError("no Q8 record (keep_stage_vectors before the step)")
+        x = np.empty(n, np.float32)
+        q = np.empty(n, np.int8)
+        d = np.empty(n // 32, np.float32)
+        torch.cuda.synchronize()
+        for arr, p in zip((x, q, d), ptrs):
+            capi.memcpy_d2h(arr, p)
+        return x, q, d
 
     def stage_vector(self, kind: int, layer: int):
         """Layer `layer`'s stage vector from the last persistent step: f32

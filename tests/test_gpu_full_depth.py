@@ -17,19 +17,26 @@ be held to the fp32 tolerance at this depth; each stage, given its actual
 input, can.
 
 So the runtime keeps every layer's stage vectors (tf_model_keep_stage_vectors)
-and each stage is fed the GPU's own input (teacher forcing):
-  - QKV: RMSNorm + Q8 of the layer input (bit-exact on both sides), then the
-    roped query and the new f16 K/V rows against fp64 GEMVs rotated by the
-    reference's fp32 RoPE angles; 1e-5 of the GEMV terms plus the angle's
-    fp32 rounding at that position, one f16 ulp for the cache rows;
-  - attention over the GPU's K/V cache, as Q8: each int8 a correct rounding
-    of a value within 1e-4 of the fp64 softmax attention, the scale amax/127;
+and a record of every quantizer's f32 input and Q8 output, and each stage is
+fed the GPU's own input (teacher forcing):
+  - every Q8 the step forms in-kernel (the QKV, gate/up and lm_head inputs
+    after RMSNorm, the merged attention output, h) is checked byte for byte
+    against quantize_q8_global (gemv.cu:43-65, the oracle) of the f32 values
+    the kernel quantized, and the published Q8 against the recorded one;
+  - the RMSNorm outputs within two f32 ulps of the oracle's;
+  - QKV: the roped query and the new f16 K/V rows against fp64 GEMVs of the
+    oracle's Q8 rotated by the reference's fp32 RoPE angles; 1e-5 of the
+    GEMV terms plus the angle's fp32 rounding at that position, one f16 ulp
+    for the cache rows;
+  - attention over the GPU's K/V cache: the merged f32 output within 1e-4 of
+    the fp64 softmax attention;
   - wo on the GPU's attention Q8, plus the residual: GEMV tolerance;
-  - gate/up with SiLU: the Q8 of h as for attention, within the GEMV
-    tolerance propagated through SiLU;
+  - gate/up with SiLU: h within the GEMV tolerance propagated through SiLU;
   - down on the GPU's h Q8, plus the residual: GEMV tolerance;
   - the lm_head on the last residual: GEMV tolerance, and the token is the
     reference argmax of the GPU's logits (and the fp64 argmax when clear).
+Then the production layout (two alternating stage buffers, no record) runs
+the same step from the same prompt and must give bit-identical logits.
 
 Two weight distributions: the benchmark's (scores of order
 1e5, a near one-hot softmax) and a well-conditioned one (synth.q4k_blocks_wc
@@ -94,22 +101,39 @@ def _check_close(got, ref, tol, what):
     return float((err / np.maximum(tol, 1e-30)).max())
 
 
-def _check_q8(q, d, ref, tol, what):
-    """GPU Q8 (int8 q, f32 d per 32) of a vector whose fp64 value is ref
-    within tol: d = amax/127 of a value in tolerance, and every q a correct
-    rounding of ref/d within tol/d."""
-    r = ref.reshape(-1, 32)
-    t = tol.reshape(-1, 32)
-    d = d.astype(np.float64)
-    amax = np.abs(r).max(axis=1)
-    tamax = t.max(axis=1)
-    assert np.all(np.abs(d * 127 - amax) <= tamax + 1e-6 * amax), f"{what}: Q8 scale"
-    z = r / np.where(d == 0, 1, d)[:, None]
-    qq = q.reshape(-1, 32).astype(np.float64)
-    slack = 0.5 + t / np.where(d == 0, 1, d)[:, None] + 1e-5 * np.abs(z) + 1e-6
-    bad = np.abs(qq - z) > slack
-    assert not bad.any(), f"{what}: {int(bad.sum())} Q8 values not a rounding of the reference"
-    return int((qq != np.rint(z)).sum())
+def _check_q8_exact(gm, site, li, what, published=None):
+    """The Q8 the step's in-kernel quantizer produced at `site` of layer li
+    equals, byte for byte, quantize_q8_global (kernels/gemv.cu:43-65, the
+    oracle) of the f32 values that quantizer consumed; and, for the
+    published vectors, what the next stage read is that Q8.  Returns the
+    recorded f32 values."""
+    x, q, d = gm.q8_record(site, li)
+    q_ref, d_ref = oracle.quantize_q8(x)
+    nq = int((q != q_ref).sum())
+    assert nq == 0, f"{what}: {nq} Q8 values differ from quantize_q8 of the GPU's f32 input"
+    assert np.array_equal(d.view(np.uint32), d_ref.view(np.uint32)), f"{what}: Q8 scales differ"
+    if published is not None:
+        pq, pd = published
+        assert np.array_equal(pq, q) and np.array_equal(pd.view(np.uint32), d.view(np.uint32)), \
+            f"{what}: the published Q8 is not the recorded one"
+    return x
+
+
+def _check_norm(x_gpu, ref, what):
+    """RMSNorm output (x * scale * w in f32) against the oracle's: within two
+    f32 ulps; returns the count of values that are not bit-identical."""
+    x_gpu = np.asarray(x_gpu, np.float32)
+    ref = np.asarray(ref, np.float32)
+    err = np.abs(x_gpu.astype(np.float64) - ref)
+    tol = 2 * _ulp32(ref) + 1e-38
+    assert np.all(err <= tol), f"{what}: worst {err.max():.3e}"
+    return int((x_gpu.view(np.uint32) != ref.view(np.uint32)).sum())
+
+
+def _layers(cfg, wc, seed):
+    """The model's layers, generated one at a time (seeded)."""
+    rng = np.random.default_rng(seed)
+    return (synth.qwen_layer(rng, cfg, li, wc) for li in range(cfg["n_layer"]))
 
 
 def _run(cfg, context, wc, seed):
@@ -119,9 +143,8 @@ def _run(cfg, context, wc, seed):
     E, F, hd = c["n_embd"], c["n_ff"], c["head_dim"]
     H, KV = c["n_head"], c["n_kv"]
     nq, nk = H * hd, KV * hd
-    rng = np.random.default_rng(seed)
-    layers = [synth.qwen_layer(rng, cfg, li, wc) for li in range(c["n_layer"])]
-    emb = synth.qwen_embedding(rng, cfg, wc)
+    layers = list(_layers(cfg, wc, seed))
+    emb = synth.qwen_embedding(np.random.default_rng(seed + 2), cfg, wc)
     gm = DecodeModel(dict(cfg, max_seq=context + 2), layers, emb)
     assert gm.path() == 4
     gm.keep_stage_vectors(True)
@@ -133,12 +156,14 @@ def _run(cfg, context, wc, seed):
     logits = gm.logits()
     scale = float(np.float32(1.0 / np.sqrt(hd)))
     cs, dang = _rope_cs(nq, hd, pos, c["rope_theta"])
-    flips = 0
+    norm_diff = 0
     worst = {}
     x_in = oracle.embed_row(emb[0], 210, tok, E, emb[1])
     for li, L in enumerate(layers):
         # ---- QKV from the GPU's layer input
         xb = oracle.rms_norm(x_in, L["attn_norm"], c["rms_eps"])
+        xb_gpu = _check_q8_exact(gm, gm.Q8_QKV_IN, li, f"layer {li} QKV input Q8")
+        norm_diff += _check_norm(xb_gpu, xb, f"layer {li} attention RMSNorm")
         q8, d8 = oracle.quantize_q8(xb)
         cb = L["wq"][1]
         yq, aq = oracle.gemv_q4k_q8_f64(L["wq"][0], q8, d8, E, nq, cb)
@@ -161,7 +186,10 @@ def _run(cfg, context, wc, seed):
         # ---- attention over the GPU's cache with the GPU's query
         att = oracle.attn_f64(q_gpu, Kc, Vc, H, KV, hd, pos + 1, scale)
         (oq, od), _ = gm.stage_vector(gm.STAGE_O, li)
-        flips += _check_q8(oq, od, att, np.full(att.size, ATT_TOL), f"layer {li} attention Q8")
+        att_gpu = _check_q8_exact(gm, gm.Q8_ATTN, li, f"layer {li} attention Q8", (oq, od))
+        worst["att"] = max(worst.get("att", 0),
+                           _check_close(att_gpu, att, np.full(att.size, ATT_TOL),
+                                        f"layer {li} attention output"))
         # ---- wo + residual on the GPU's attention Q8
         yo, ao = oracle.gemv_q4k_q8_f64(L["wo"][0], oq, od, nq, E, L["wo"][1])
         xa_ref = x_in.astype(np.float64) + yo
@@ -171,17 +199,20 @@ def _run(cfg, context, wc, seed):
                                        f"layer {li} residual after wo"))
         # ---- gate/up + SiLU from the GPU's residual
         xb2 = oracle.rms_norm(xa, L["ffn_norm"], c["rms_eps"])
+        xb2_gpu = _check_q8_exact(gm, gm.Q8_GU_IN, li, f"layer {li} gate/up input Q8")
+        norm_diff += _check_norm(xb2_gpu, xb2, f"layer {li} FFN RMSNorm")
         q8, d8 = oracle.quantize_q8(xb2)
         g64, ga = oracle.gemv_q4k_q8_f64(L["gate"][0], q8, d8, E, F, L["gate"][1])
         u64, ua = oracle.gemv_q4k_q8_f64(L["up"][0], q8, d8, E, F, L["up"][1])
-        sig = 1.0 / (1.0 + np.exp(-g64))
+        sig = np.exp(-np.logaddexp(0.0, -g64))  # 1 / (1 + e^-g) without overflow
         h_ref = g64 * sig * u64
         dsilu = sig * (1.0 + g64 * (1.0 - sig))
         h_tol = GEMV_RTOL * (np.abs(dsilu * u64) * np.maximum(np.abs(g64), CANCEL_FLOOR * ga)
                              + np.abs(g64 * sig) * np.maximum(np.abs(u64), CANCEL_FLOOR * ua)
                              + np.abs(h_ref)) + 1e-30
         (hq, hdq), _ = gm.stage_vector(gm.STAGE_H, li)
-        flips += _check_q8(hq, hdq, h_ref, h_tol, f"layer {li} h Q8")
+        h_gpu = _check_q8_exact(gm, gm.Q8_H, li, f"layer {li} h Q8", (hq, hdq))
+        worst["h"] = max(worst.get("h", 0), _check_close(h_gpu, h_ref, h_tol, f"layer {li} h"))
         # ---- down + residual on the GPU's h Q8
         if L["down_q6k"]:
             comp, ccb = synth.q6k_compact(L["down"][0], F)
@@ -196,6 +227,8 @@ def _run(cfg, context, wc, seed):
         x_in = xo
     # ---- lm_head on the GPU's last residual
     xb = oracle.rms_norm(x_in, np.ones(E, np.float32), c["rms_eps"])
+    xh_gpu = _check_q8_exact(gm, gm.Q8_QKV_IN, c["n_layer"], "lm_head input Q8")
+    norm_diff += _check_norm(xh_gpu, xb, "output RMSNorm")
     q8, d8 = oracle.quantize_q8(xb)
     comp, ccb = synth.q6k_compact(emb[0], E)
     y64, ay = oracle.gemv_q6k_q8_f64(comp, 212, q8, d8, E, c["n_vocab"], ccb)
@@ -205,8 +238,18 @@ def _run(cfg, context, wc, seed):
     if srt[-1] - srt[-2] > 2 * gemv_tol(srt[-1:], ay.max(keepdims=True))[0]:
         assert nxt == int(np.argmax(y64))
     print(f"[full-depth] {c['n_layer']} layers: worst error/tolerance {worst}; "
-          f"{flips} Q8 values rounded the other way at a boundary", flush=True)
+          f"every Q8 bit-exact; {norm_diff} RMSNorm values not bit-identical to the oracle's",
+          flush=True)
     gm.close()
+    # The production layout (two alternating stage buffers, no record) runs
+    # the same arithmetic at other addresses: the same token and logits.
+    gm2 = DecodeModel(dict(cfg, max_seq=context + 2), _layers(cfg, wc, seed), emb)
+    assert gm2.path() == 4
+    assert gm2.prefill(prompt, 0) == tok
+    assert gm2.forward(tok, pos) == nxt
+    assert np.array_equal(gm2.logits().view(np.uint32), logits.view(np.uint32)), \
+        "two-buffer step logits differ from the kept-vector step's"
+    gm2.close()
 
 
 @pytest.mark.parametrize("wc", [True, False], ids=["well_conditioned", "baseline_dist"])

@@ -1,8 +1,13 @@
 """The allocation-free flash decode (tf_flash_decode_noalloc, workspace in
 the library's static device array) against tf_flash_decode with caller
-workspace: two calls in a row, the second smaller, then a split count whose
-merge runs as a second kernel; outputs and Q8 bit-identical (the same
-kernels on the same inputs), and oversize requests rejected."""
+workspace: two calls in a row, the second smaller, then a third at a long
+context; outputs and Q8 bit-identical (the same kernels on the same
+inputs), oversize requests rejected, and, in a fresh process, the first
+call captured into a HIP graph and replayed."""
+import subprocess
+import sys
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -40,7 +45,7 @@ def test_noalloc_matches_workspace_entry(gpu):
     _pair(rng, 28, 4, 4096, 64)
     print("[no-alloc] 16/2 heads, L 512, 8 splits (smaller)", flush=True)
     _pair(rng, 16, 2, 512, 8)
-    print("[no-alloc] 16/2 heads, L 32768, 256 splits (separate merge kernel)", flush=True)
+    print("[no-alloc] 16/2 heads, L 32768, 256 splits", flush=True)
     _pair(rng, 16, 2, 32768, 256)
 
 
@@ -53,3 +58,13 @@ def test_noalloc_rejects_oversize(gpu):
     rc = capi.load().tf_flash_decode_noalloc(P(z), P(z), P(z), P(out), None, None, 64, 8, 128, 10,
                                             None, 256, 0.1, S())
     assert rc == 1  # hipErrorInvalidValue
+
+
+def test_noalloc_first_call_under_graph_capture(gpu):
+    """A fresh process (an empty per-device address cache) whose first call
+    is captured: the set-up enqueues nothing into the graph."""
+    script = Path(__file__).resolve().parent / "_noalloc_graph.py"
+    print("[no-alloc] graph capture in a child process", flush=True)
+    r = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "noalloc-graph ok" in r.stdout
