@@ -220,6 +220,7 @@ def kernel_table(iters, only=None):
         ("cfg1b_q6k_down_11008x2048", lambda: B.case_q6k(11008, 2048, 2, iters)),
         # the reference's Q4_K ffn_down (18 of 36 layers): split-K + reduce
         ("a4_q4k_down_splitk4_11008x2048", lambda: B.case_q4k_splitk(11008, 2048, 14, iters)),
+        ("q4k_down_single_pass_11008x2048", lambda: B.case_q4k_gemv(11008, 2048, 14, iters)),
         ("cfg1c_q4k_qkv_2048x2560", lambda: B.case_q4k_qkv(2048, 2048, 256, 3, iters)),
         ("lm_head_q6k_2048x151936", lambda: B.case_q6k(2048, 151936, 6, max(10, iters // 4),
                                                        "tf_gemv_q6k_compact_q8", 0)),
@@ -239,6 +240,7 @@ def kernel_table(iters, only=None):
     for L in (512, 4096, 32768):
         rows.append((f"cfg2_flash_L{L}_split8", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters, 8)))
         rows.append((f"cfg2_flash_L{L}_auto", lambda L=L: B.case_flash(L, 16, 2, 128, 7, iters)))
+    rows.append(("flash_L512_split1", lambda: B.case_flash(512, 16, 2, 128, 7, iters, 1)))
     out = {}
     for name, fn in rows:
         if only and only not in name:
@@ -246,12 +248,40 @@ def kernel_table(iters, only=None):
         r = B.report(name, fn())
         out[name] = {"us": round(r["per_us"], 2), "us_b2b": round(r["b2b_us"], 2),
                      "MB": round(r["bytes"] / 1e6, 3), "GBs": round(r["gbs"], 1),
-                     "frac_hbm": round(r["frac"], 4)}
+                     "frac_hbm": round(r["frac"], 4),
+                     "frac_hbm_b2b": round(r["bytes"] / (r["b2b_us"] * 1e-6) / 8e12, 4)}
         if "n_split" in r:
             out[name]["n_split"] = r["n_split"]
         if "flops" in r:
             out[name]["TFLOPs"] = round(r["flops"] / (r["b2b_us"] * 1e-6) / 1e12, 1)
         log(f"[bench] {name}: {out[name]}")
+    return out
+
+
+FLOOR_SIZES = [("2.1MB", 2122416), ("3.0MB", 2972160), ("12.7MB", 12710592),
+               ("18.5MB", 18522240), ("25.4MB", 25408768), ("255.9MB", 255863296)]
+
+
+def floor_table(iters, sweep=False):
+    """The streaming-read floor (tf_stream_read_probe) at the GEMVs' byte
+    counts; sweep=True also tries the grid and load-depth variants."""
+    from taraference_amd import benchkit as B
+
+    configs = ([(2, 8, 1)] if not sweep else
+               [(1, 8, 0), (2, 8, 0), (4, 8, 0), (1, 4, 1), (1, 8, 1), (2, 4, 1), (2, 8, 1),
+                (4, 4, 1), (4, 8, 1)])
+    out = {}
+    for label, nb in FLOOR_SIZES:
+        nb = (nb + 15) // 16 * 16
+        for bpc, depth, contig in configs:
+            key = f"stream_{label}_wg{bpc}_d{depth}_{'contig' if contig else 'inter'}"
+            r = B.report(key, B.case_stream(nb, iters if nb < (64 << 20) else max(10, iters // 4),
+                                            bpc, depth, contig))
+            out[key] = {"us": round(r["per_us"], 2), "us_b2b": round(r["b2b_us"], 2),
+                        "MB": round(nb / 1e6, 3), "GBs": round(r["gbs"], 1),
+                        "frac_hbm": round(r["frac"], 4),
+                        "frac_hbm_b2b": round(nb / (r["b2b_us"] * 1e-6) / 8e12, 4)}
+            log(f"[bench] {key}: {out[key]}")
     return out
 
 
@@ -469,6 +499,8 @@ def main():
                     help="only the runtime's 512-token prefill of the 3B-shape model")
     ap.add_argument("--kernel-filter", default=None,
                     help="with --only-kernels: rows whose name contains this text")
+    ap.add_argument("--only-floor", action="store_true",
+                    help="only the streaming-read floor, swept over grid and load depth")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     ap.add_argument("--only-cpu", action="store_true",
@@ -504,6 +536,9 @@ def main():
         return
     if args.q05:
         print(json.dumps(q05_decode(CONTEXT, max(2, args.steps))), flush=True)
+        return
+    if args.only_floor:
+        print(json.dumps({"floor": floor_table(args.kernel_iters, sweep=True)}), flush=True)
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters, args.kernel_filter)}),
@@ -590,6 +625,8 @@ def main():
         out["prefill"] = pf
         out["kernels"] = {} if args.no_kernels else _leg("kernels",
                                                          lambda: kernel_table(args.kernel_iters))
+        out["streaming_floor"] = {} if args.no_kernels else _leg(
+            "streaming_floor", lambda: floor_table(args.kernel_iters))
         if not args.no_config4:
             log("[bench] config 4 ...")
             out["config4"] = _leg("config4", config4)

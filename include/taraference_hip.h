@@ -342,6 +342,16 @@ int tf_flash_decode_noalloc(const float *q, const uint16_t *k_cache,
  * attention output and of silu(gate)*up. */
 int tf_decode_step_quantize_q8(const float *x, int n, int variant, int8_t *q,
                                float *d, tf_stream_t stream);
+/* No counterpart in the reference (a measurement aid for bench.py): reads
+ * n_bytes (a multiple of 16) at src with 16-byte loads, `depth` (4, 8 or 16)
+ * in flight per thread, on blocks_per_cu (1..8) x CUs workgroups of 512
+ * threads (contiguous != 0: each workgroup reads its own contiguous run,
+ * else the threads interleave over the whole buffer), and writes one word
+ * per workgroup to sink (blocks_per_cu x CUs words).  The plain
+ * streaming-read rate the GEMVs are priced against. */
+int tf_stream_read_probe(const void *src, long long n_bytes, uint32_t *sink,
+                         int blocks_per_cu, int depth, int contiguous,
+                         tf_stream_t stream);
 /* Partition count this library recommends for a context of max_seq tokens
  * (a multiple of 8; 8 for short contexts).  The reference fixes 8
  * (cuda/decode.rs:38-41); on MI355X long contexts need more partitions to

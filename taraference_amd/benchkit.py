@@ -100,6 +100,21 @@ def case_q4k_gemv(n_rows, n_cols, seed, iters):
     return dict(per_us=per, b2b_us=b2b, bytes=alg)
 
 
+def case_stream(n_bytes, iters, blocks_per_cu=2, depth=8, contiguous=1):
+    """The streaming-read floor: tf_stream_read_probe over n_bytes per launch,
+    rotating through >= 1 GiB of distinct buffers like the GEMV cases."""
+    ws = _copies(np.zeros(n_bytes, np.uint8), n_bytes)
+    sink = torch.empty(8 * 1024, dtype=torch.int32, device="cuda")
+    lib = capi.load()
+
+    def launch(i, s):
+        lib.tf_stream_read_probe(ws[i].data_ptr(), n_bytes, sink.data_ptr(), blocks_per_cu,
+                                 depth, contiguous, s)
+
+    per, b2b = time_launches(launch, len(ws), iters)
+    return dict(per_us=per, b2b_us=b2b, bytes=n_bytes)
+
+
 def case_q4k_splitk(n_rows, n_cols, seed, iters, n_split=4):
     """The reference's tall Q4_K path (kernels/gemv.cu:1877 split-K partials
     + :2243 reduce, in-place residual): two launches per GEMV."""
@@ -309,11 +324,10 @@ def case_flash(L, n_head, n_kv, hd, seed, iters, n_split=None):
     out = torch.empty(n_head * hd, device="cuda")
     scale = float(np.float32(1 / np.sqrt(hd)))
 
-    def launch(i, s):
-        lib.tf_flash_decode_partial(q.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
-                                    part.data_ptr(), n_head, n_kv, hd, L - 1, 1, n_split,
-                                    scale, s)
-        lib.tf_flash_decode_reduce(part.data_ptr(), out.data_ptr(), n_head, hd, n_split, 1, s)
+    def launch(i, s):  # the tf_flash_decode entry: partials and their merge
+        lib.tf_flash_decode(q.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(), part.data_ptr(),
+                            None, out.data_ptr(), None, None, n_head, n_kv, hd, L - 1, None,
+                            n_split, scale, s)
 
     per, b2b = time_launches(launch, len(ks), iters)
     alg = kvb + 4 * n_head * hd * 2

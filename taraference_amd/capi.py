@@ -74,6 +74,7 @@ SIGNATURES: dict[str, list] = {
     "tf_argmax": [_P, _I, _P, _P],
     "tf_q4k_block_dots": [_P, _P, _P, _P, _I, _I, _I, _P],
     "tf_decode_step_quantize_q8": [_P, _I, _I, _P, _P, _P],
+    "tf_stream_read_probe": [_P, C.c_longlong, _P, _I, _I, _I, _P],
     "tf_q6k_block_dots": [_P, _I, _P, _P, _I, _I, _I, _P],
     "tf_version": [],
     "tf_exported_symbol_count": [],

@@ -281,10 +281,15 @@ extern "C" int tf_flash_debug_fd_stamps(unsigned long long* host) {
     } while (0)
 #endif
 
+// With out != nullptr (n_split == 1 only) the workgroup's (m, l, O) is the
+// whole context's: it writes out = O / max(l, 1e-20) (the merge of a single
+// partition, bit-identical to tf_flash_reduce_kernel's) and, with q8, its
+// Q8 instead of the partial, so the decode needs no second launch.
 __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, float* __restrict__ partial, int n_head, int n_kv,
-    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale) {
+    int pos0, const int* __restrict__ pos0_dev, int n_split, float scale,
+    float* __restrict__ out, int8_t* __restrict__ q8, float* __restrict__ d8) {
     constexpr int HD = 128;
     extern __shared__ __align__(16) uint8_t lds_raw[];
 #ifdef TF_FLASH_STAMPS
@@ -528,6 +533,18 @@ __global__ __launch_bounds__(512) void tf_flash_partial_dma_kernel(
             O += a * cmb[(w * 16 + h) * TF_FD_CR + 4 + d];
             L += a * cmb[(w * 16 + h) * TF_FD_CR + 1];
         }
+        if (out) {  // workgroup-uniform; G * HD is a multiple of 64
+            const float v = O / fmaxf(L, 1e-20f);
+            const size_t oi = (size_t)kv_h * G * HD + i;
+            out[oi] = v;
+            if (q8) {  // this 32-lane half holds one 32-value group
+                const float amax = tf_group32_max(fabsf(v));
+                const float dq = amax * (1.0f / 127.0f);
+                q8[oi] = (int8_t)tf_q8_value(v, amax, dq);
+                if ((lane & 31) == 0) d8[oi >> 5] = dq;
+            }
+            continue;
+        }
         float* base = partial + ((size_t)(kv_h * G + h) * n_split + s) * po;
         if (d == 0) {
             base[0] = M;
@@ -673,7 +690,8 @@ template <int HD>
 static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t* v,
                               float* partial, int n_head, int n_kv, int pos0,
                               const int* pos0_dev, int n_split, float scale,
-                              tf_stream_t stream) {
+                              tf_stream_t stream, float* out = nullptr, int8_t* q8 = nullptr,
+                              float* d8 = nullptr) {
     const int G = n_head / n_kv;
     const dim3 grid(n_kv, n_split);
     if (HD == 128 && G <= 16) {  // the DMA-fed matrix-core partial
@@ -681,7 +699,7 @@ static int tf_flash_launch_hd(const float* q, const uint16_t* k, const uint16_t*
         if (rc) return rc;
         hipLaunchKernelGGL(tf_flash_partial_dma_kernel, grid, dim3(64 * TF_FD_WAVES), TF_FD_LDS,
                            tf_stream(stream), q, k, v, partial, n_head, n_kv, pos0, pos0_dev,
-                           n_split, scale);
+                           n_split, scale, out, q8, d8);
         return TF_LAUNCH_RESULT();
     }
     if (G <= 4)
@@ -769,11 +787,20 @@ extern "C" int tf_flash_decode(const float* q, const uint16_t* k_cache, const ui
     TF_CHECK_ARG(out && ((q8 == nullptr) == (d8 == nullptr)));
     (void)counters;  // reserved (may be NULL)
     TF_CHECK_ARG(n_kv > 0 && n_head > 0 && n_head % n_kv == 0);
-    // The merge runs as its own kernel (`counters` is not used).  Merging inside the partial launch measured slower:
-    // with a release fence per workgroup (the last one of a kv head merges)
-    // 14.2 vs 9.7 us at L = 512, 43.9 vs 10.8 us at 4096; with 4 G merge
-    // workgroups per kv head polling a device-coherent count of finished
-    // splits, 10.0 vs 8.3 us at 512 and 17.2 vs 15.1 us at 32768.
+    // One partition on the DMA-fed kernel: it writes the output itself.
+    // Otherwise the merge runs as its own kernel.  Merging inside the partial
+    // launch measured slower: with a release fence per workgroup (the last
+    // one of a kv head merges) 14.2 vs 9.7 us at L = 512, 43.9 vs 10.8 us at
+    // 4096; with 4 G merge workgroups per kv head polling a device-coherent
+    // count of finished splits, 10.0 vs 8.3 us at 512 and 17.2 vs 15.1 us at
+    // 32768.
+    if (n_split == 1 && head_dim == 128 && n_head / n_kv <= 16) {
+        TF_CHECK_ARG(q && k_cache && v_cache && (pos0_dev || pos0 >= 0));
+        TF_CHECK_ARG(((uintptr_t)q & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 &&
+                     ((uintptr_t)v_cache & 15) == 0);
+        return tf_flash_launch_hd<128>(q, k_cache, v_cache, partial, n_head, n_kv, pos0,
+                                       pos0_dev, 1, scale, stream, out, q8, d8);
+    }
     const int rc = tf_flash_partial_any(q, k_cache, v_cache, partial, n_head, n_kv, head_dim,
                                         pos0, pos0_dev, 1, n_split, scale, stream);
     if (rc) return rc;

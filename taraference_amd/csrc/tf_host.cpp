@@ -166,6 +166,7 @@ static const char* const k_symbols[] = {
     "tf_model_stage_vector",
     "tf_model_q8_record",
     "tf_decode_step_quantize_q8",
+    "tf_stream_read_probe",
     "tf_model_k_cache",
     "tf_model_v_cache",
     "tf_q4k_block_dots",

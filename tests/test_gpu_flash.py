@@ -80,7 +80,9 @@ def test_flash_prefix_of_longer_cache(gpu):
 @pytest.mark.parametrize("n_head,n_kv,hd,L,n_split", [
     (16, 2, 128, 1, 8), (16, 2, 128, 5, 8), (16, 2, 128, 777, 8), (16, 2, 128, 4096, 32),
     (16, 2, 128, 5000, 64), (16, 2, 128, 32768, 256),
-    (28, 4, 128, 3000, 16), (8, 8, 64, 100, 8), (32, 2, 128, 600, 8), (16, 4, 256, 700, 24)])
+    (28, 4, 128, 3000, 16), (8, 8, 64, 100, 8), (32, 2, 128, 600, 8), (16, 4, 256, 700, 24),
+    (16, 2, 128, 1, 1), (16, 2, 128, 512, 1), (16, 2, 128, 2048, 1), (28, 4, 128, 3000, 1),
+    (8, 8, 64, 100, 1)])
 def test_flash_decode_one_call(gpu, n_head, n_kv, hd, L, n_split):
     """tf_flash_decode: split partials then the log-sum-exp merge (+ Q8 of
     the merged output) in one call.  Attention within 2e-3 of fp64 softmax
@@ -108,3 +110,28 @@ def test_flash_decode_one_call(gpu, n_head, n_kv, hd, L, n_split):
     ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)
     assert np.abs(outs[0] - ref).max() < ATOL
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("n_head,n_kv,L", [(16, 2, 512), (16, 2, 1500), (28, 4, 777)])
+def test_flash_single_partition_direct_output(gpu, n_head, n_kv, L):
+    """With one partition tf_flash_decode writes the output (and its Q8) from
+    the partial kernel itself: bit-identical to the partial + merge pair of
+    launches (tf_flash_decode_partial, tf_flash_decode_reduce_q8)."""
+    hd = 128
+    q, K, V = case(L, n_head, n_kv, hd, L + 1)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    qd, kd, vd = dev(q), dev(K), dev(V)
+    n = n_head * hd
+    part = empty(n_head * (2 + hd))
+    o1, q1, d1 = empty(n), empty(n, torch.int8), empty(n // 32)
+    call("tf_flash_decode", P(qd), P(kd), P(vd), P(part), None, P(o1), P(q1), P(d1),
+         n_head, n_kv, hd, L - 1, None, 1, scale, S())
+    o2, q2, d2 = empty(n), empty(n, torch.int8), empty(n // 32)
+    call("tf_flash_decode_partial", P(qd), P(kd), P(vd), P(part), n_head, n_kv, hd, L - 1, 1, 1,
+         scale, S())
+    call("tf_flash_decode_reduce_q8", P(part), P(o2), P(q2), P(d2), n_head, hd, 1, S())
+    assert np.array_equal(host(o1).view(np.uint32), host(o2).view(np.uint32))
+    assert np.array_equal(host(q1), host(q2))
+    assert np.array_equal(host(d1).view(np.uint32), host(d2).view(np.uint32))
+    ref = oracle.attn_f64(q, K, V, n_head, n_kv, hd, L, scale)
+    assert np.abs(host(o1) - ref).max() < ATOL
