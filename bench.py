@@ -262,16 +262,18 @@ FLOOR_SIZES = [("2.1MB", 2122416), ("3.0MB", 2972160), ("12.7MB", 12710592),
                ("18.5MB", 18522240), ("25.4MB", 25408768), ("255.9MB", 255863296)]
 
 
-def floor_table(iters, sweep=False):
+def floor_table(iters, sweep=False, only_bytes=None):
     """The streaming-read floor (tf_stream_read_probe) at the GEMVs' byte
-    counts; sweep=True also tries the grid and load-depth variants."""
+    counts (or at only_bytes alone); sweep=True also tries the grid,
+    load-depth and access-pattern variants."""
     from taraference_amd import benchkit as B
 
     configs = ([(2, 8, 1)] if not sweep else
                [(1, 8, 0), (2, 8, 0), (4, 8, 0), (1, 4, 1), (1, 8, 1), (2, 4, 1), (2, 8, 1),
                 (4, 4, 1), (4, 8, 1)])
     out = {}
-    for label, nb in FLOOR_SIZES:
+    sizes = FLOOR_SIZES if not only_bytes else [(f"{only_bytes / 1e6:.1f}MB", only_bytes)]
+    for label, nb in sizes:
         nb = (nb + 15) // 16 * 16
         for bpc, depth, contig in configs:
             key = f"stream_{label}_wg{bpc}_d{depth}_{'contig' if contig else 'inter'}"
@@ -500,7 +502,11 @@ def main():
     ap.add_argument("--kernel-filter", default=None,
                     help="with --only-kernels: rows whose name contains this text")
     ap.add_argument("--only-floor", action="store_true",
-                    help="only the streaming-read floor, swept over grid and load depth")
+                    help="only the streaming-read floor (tf_stream_read_probe)")
+    ap.add_argument("--floor-sweep", action="store_true",
+                    help="with --only-floor: also the grid, depth and pattern variants")
+    ap.add_argument("--floor-bytes", type=int, default=None,
+                    help="with --only-floor: this one size only (for counter runs)")
     ap.add_argument("--only-kernels", action="store_true",
                     help="run only the per-kernel table (for kernel traces)")
     ap.add_argument("--only-cpu", action="store_true",
@@ -538,7 +544,8 @@ def main():
         print(json.dumps(q05_decode(CONTEXT, max(2, args.steps))), flush=True)
         return
     if args.only_floor:
-        print(json.dumps({"floor": floor_table(args.kernel_iters, sweep=True)}), flush=True)
+        print(json.dumps({"floor": floor_table(args.kernel_iters, args.floor_sweep,
+                                               args.floor_bytes)}), flush=True)
         return
     if args.only_kernels:
         print(json.dumps({"kernels": kernel_table(args.kernel_iters, args.kernel_filter)}),
