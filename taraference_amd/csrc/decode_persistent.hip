@@ -1111,6 +1111,7 @@ struct TfPAttnGeo {
     bool active;
 };
 
+template <bool MM>
 __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     TfPAttnGeo g;
     const int seq = pos + 1;
@@ -1119,7 +1120,8 @@ __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     const int grid = (int)gridDim.x;
     // the most head groups (4, 2, 1) that still give every tile its own split
     g.n_hg = 1;
-    if (G >= 4 && a.KV * n_tiles * 4 <= grid) g.n_hg = 4;
+    if (MM && G > 4) {
+    } else if (G >= 4 && a.KV * n_tiles * 4 <= grid) g.n_hg = 4;
     else if (G >= 2 && a.KV * n_tiles * 2 <= grid) g.n_hg = 2;
     g.hpw = (G + g.n_hg - 1) / g.n_hg;
     g.hpw = g.hpw <= 2 ? 2 : (g.hpw <= 4 ? 4 : 8);  // a power of two dividing 8
@@ -1127,17 +1129,24 @@ __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     g.wph = TF_P_WAVES / g.hpw;
     int per_kv = grid / (a.KV * g.n_hg);
     per_kv = per_kv < 1 ? 1 : (per_kv > TF_P_MAX_SPLIT ? TF_P_MAX_SPLIT : per_kv);
-    const int n0 = n_tiles < per_kv ? n_tiles : per_kv;
-    g.tpw = (n_tiles + n0 - 1) / n0;
-    g.n_ws = (n_tiles + g.tpw - 1) / g.tpw;  // every split holds at least one tile
+    // split length in tokens: whole 64-token tiles, except on the matrix-core
+    // path (one head group with one wave per head), whose waves copy 16-token
+    // tiles: there 16-token units spread the context over up to per_kv
+    // workgroups of a kv head
+    const int unit = MM && g.n_hg == 1 && g.wph == 1 ? 16 : TF_P_TILE;
+    const int n_units = (seq + unit - 1) / unit;
+    const int n0 = n_units < per_kv ? n_units : per_kv;
+    const int upw = (n_units + n0 - 1) / n0;
+    g.n_ws = (n_units + upw - 1) / upw;  // every split holds at least one unit
+    g.tpw = (upw * unit + TF_P_TILE - 1) / TF_P_TILE;
     const int b = blockIdx.x;
     g.active = b < a.KV * g.n_hg * g.n_ws;
     const int kg = g.active ? b / g.n_ws : 0;
     g.kh = kg / g.n_hg;
     g.hg = kg % g.n_hg;
     g.ws = g.active ? b % g.n_ws : 0;
-    g.t_begin = g.ws * g.tpw * TF_P_TILE;
-    const int te = (g.ws + 1) * g.tpw * TF_P_TILE;
+    g.t_begin = g.ws * upw * unit;
+    const int te = (g.ws + 1) * upw * unit;
     g.t_end = te < seq ? te : seq;
     return g;
 }
@@ -1207,7 +1216,7 @@ typedef float tf_p_f32x4 __attribute__((ext_vector_type(4)));
 
 // 16-token tile j of the split -> slot b of this wave's ring: four copies of
 // 4 K rows, then four of 4 V rows; rows past the split repeat its last token
-// (their scores are masked).
+// (their scores are masked and their V values zeroed when the tile is used).
 __device__ __forceinline__ void tf_p_attn_dma_tile(TfPL& L, const TfPAttnGeo& g, int stride,
                                                    uint8_t* lds, int j, int b) {
     const int lane = tf_p_tid() & 63, wave = tf_p_tid() >> 6;
@@ -1390,15 +1399,20 @@ __device__ __forceinline__ void tf_p_attn_dma_run(TfPA& a, TfPL& L, const TfPAtt
             pb[4 + r] = (_Float16)(p - (float)h0);
         }
         l = l * alpha + ps;
-        // ---- O^T += V^T P^T (hi and lo parts of p in one k = 32 step)
+        // ---- O^T += V^T P^T (hi and lo parts of p in one k = 32 step).  The
+        // V values of rows past the split are zeroed, not only their p: those
+        // slot rows repeat the row `pos`, whose cache line this launch is
+        // still writing (its old bits may be a NaN, and 0 x NaN is NaN).
         {
             _Float16 vv[8][4];
             const uint8_t* vp = slot + voff;
 #pragma unroll
             for (int db = 0; db < 8; db++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    vv[db][i] = *reinterpret_cast<const _Float16*>(vp + 256 * i + 32 * db);
+                for (int i = 0; i < 4; i++) {
+                    const _Float16 v = *reinterpret_cast<const _Float16*>(vp + 256 * i + 32 * db);
+                    vv[db][i] = t0 + 4 * gg + i < g.t_end ? v : (_Float16)0.f;
+                }
 #pragma unroll
             for (int db = 0; db < 8; db++) {
                 tf_h16x8 va;
@@ -2009,9 +2023,9 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
     TfPL& L = tf_p_layer(a, li);
-    const TfPAttnGeo g = tf_p_attn_geo(a, pos);
+    const TfPAttnGeo g = tf_p_attn_geo<MM>(a, pos);
     if (!g.active) {
-        if constexpr (!MM) tf_p_gu_warm(a, L, a.KV * g.n_hg * g.n_ws);
+        tf_p_gu_warm(a, L, a.KV * g.n_hg * g.n_ws);
         return true;
     }
     TfPAttnRegs ra;
@@ -2353,8 +2367,11 @@ bool tf_decode_persistent_supported(int n_layer, int E, int F, int H, int KV, in
 }
 
 bool tf_decode_persistent_long_ctx(const TfPArgs& a, int grid, int pos) {
-    // tf_p_attn_geo: one head group with one wave per head
     const int G = a.H / a.KV;
+#ifdef TF_P_MM_ALWAYS
+    return G > 4;
+#endif
+    // tf_p_attn_geo: one head group with one wave per head
     const int n_tiles = (pos + 1 + TF_P_TILE - 1) / TF_P_TILE;
     if (G >= 4 && a.KV * n_tiles * 4 <= grid) return false;
     if (G >= 2 && a.KV * n_tiles * 2 <= grid) return false;
