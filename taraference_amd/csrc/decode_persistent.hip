@@ -1120,8 +1120,7 @@ __device__ __forceinline__ TfPAttnGeo tf_p_attn_geo(TfPA& a, int pos) {
     const int grid = (int)gridDim.x;
     // the most head groups (4, 2, 1) that still give every tile its own split
     g.n_hg = 1;
-    if (MM && G > 4) {
-    } else if (G >= 4 && a.KV * n_tiles * 4 <= grid) g.n_hg = 4;
+    if (G >= 4 && a.KV * n_tiles * 4 <= grid) g.n_hg = 4;
     else if (G >= 2 && a.KV * n_tiles * 2 <= grid) g.n_hg = 2;
     g.hpw = (G + g.n_hg - 1) / g.n_hg;
     g.hpw = g.hpw <= 2 ? 2 : (g.hpw <= 4 ? 4 : 8);  // a power of two dividing 8
@@ -2025,7 +2024,7 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
     TfPL& L = tf_p_layer(a, li);
     const TfPAttnGeo g = tf_p_attn_geo<MM>(a, pos);
     if (!g.active) {
-        tf_p_gu_warm(a, L, a.KV * g.n_hg * g.n_ws);
+        if constexpr (!MM) tf_p_gu_warm(a, L, a.KV * g.n_hg * g.n_ws);
         return true;
     }
     TfPAttnRegs ra;
@@ -2368,9 +2367,6 @@ bool tf_decode_persistent_supported(int n_layer, int E, int F, int H, int KV, in
 
 bool tf_decode_persistent_long_ctx(const TfPArgs& a, int grid, int pos) {
     const int G = a.H / a.KV;
-#ifdef TF_P_MM_ALWAYS
-    return G > 4;
-#endif
     // tf_p_attn_geo: one head group with one wave per head
     const int n_tiles = (pos + 1 + TF_P_TILE - 1) / TF_P_TILE;
     if (G >= 4 && a.KV * n_tiles * 4 <= grid) return false;
