@@ -27,16 +27,19 @@ __global__ __launch_bounds__(512) void tf_stream_read_kernel(const tf_u32x4* __r
         c = threadIdx.x;
     }
     uint32_t acc = 0;
-    for (; c + (U - 1) * T < n_chunks; c += U * T) {
+    // U loads in flight per pass, every one issued (a chunk past the end
+    // reloads chunk c, already on its way, and is not folded in): a tail
+    // loop of single loads would pay one memory round trip per chunk
+    for (; c < n_chunks; c += U * T) {
         tf_u32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = tf_ld16(src + c + u * T);
+        for (int u = 0; u < U; u++) {
+            const long long cu = c + u * T;
+            v[u] = tf_ld16(src + (cu < n_chunks ? cu : c));
+        }
 #pragma unroll
-        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; c < n_chunks; c += T) {
-        const tf_u32x4 v = tf_ld16(src + c);
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        for (int u = 0; u < U; u++)
+            if (c + u * T < n_chunks) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     // thread 0's fold stands for the workgroup (every lane's loads are issued
     // regardless: the store is conditional at run time only)
