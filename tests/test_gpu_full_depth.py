@@ -1,6 +1,7 @@
 """Full-depth decode parity: the real config-3 model (Qwen2.5-3B shape, 36
 layers, vocab 151936) at a 512-token context and the config-4 model
-(Qwen2.5-7B shape, 28 layers, vocab 152064) at a 4096-token context, the
+(Qwen2.5-7B shape, 28 layers, vocab 152064) at a 4096-token context and at
+its full 32768-token context, the
 default persistent step (path 4) checked stage by stage, in every layer,
 against the oracle's fp64 truths (the reference's op order: forward.rs:
 360-407, layer.rs attn_block / ffn_block_dense).
@@ -260,3 +261,10 @@ def test_config3_full_depth(gpu, wc):
 @pytest.mark.parametrize("wc", [True, False], ids=["well_conditioned", "baseline_dist"])
 def test_config4_full_depth(gpu, wc):
     _run(dict(synth.QWEN25_7B), 4096, wc, 0x7A7A0004)
+
+
+def test_config4_full_depth_full_context(gpu):
+    """Config 4 jointly at full depth (28 layers) and full context (32768
+    tokens written by the runtime's prefill), every stage of every layer
+    checked as above."""
+    _run(dict(synth.QWEN25_7B), 32768, True, 0x7A7A0014)
