@@ -287,8 +287,11 @@ struct TfPQ8Rec {
     float* d;
 };
 
+// REC: the kernel instantiation that keeps the record (production launches
+// compile it out).
+template <bool REC>
 __device__ __forceinline__ TfPQ8Rec tf_p_q8rec(TfPA& a, int li, int site, bool on = true) {
-    if (!a.q8x || !on) return TfPQ8Rec{nullptr, nullptr, nullptr};
+    if (!REC || !a.q8x || !on) return TfPQ8Rec{nullptr, nullptr, nullptr};
     const size_t off = ((size_t)li * 4 + site) * (size_t)a.q8n;
     return TfPQ8Rec{a.q8x + off, a.q8q + off, a.q8d + off / 32};
 }
@@ -1555,7 +1558,7 @@ __device__ __forceinline__ bool tf_p_attn_merge_wg(TfPA& a, const TfPAttnGeo& g,
     return true;
 }
 
-template <bool MM>
+template <bool MM, bool REC>
 __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo& g, int pos,
                                               TfPAttnRegs& r, uint8_t* lds,
                                               const unsigned long long* fq,
@@ -1566,7 +1569,7 @@ __device__ __forceinline__ bool tf_p_attn_run(TfPA& a, TfPL& L, const TfPAttnGeo
     constexpr int HD = TF_P_HD;
     const int tid = tf_p_tid(), lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KV, stride = a.KV * HD;
-    const TfPQ8Rec rec = tf_p_q8rec(a, (sk - 1) / 5, 1);
+    const TfPQ8Rec rec = tf_p_q8rec<REC>(a, (sk - 1) / 5, 1);
     // matrix-core tiles copied HBM -> LDS per wave, for a single head group
     // with one wave per head (long contexts)
     const bool mm = MM && g.n_hg == 1 && g.wph == 1;
@@ -1899,7 +1902,7 @@ __device__ __forceinline__ bool tf_p_poll_xf(TfPA& a, float* xf, const unsigned 
 }
 
 // Layer li's norm + QKV + RoPE + K/V append.
-template <int SPR, int IT>
+template <int SPR, int IT, bool REC>
 __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, int pos, int token) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
@@ -1945,7 +1948,7 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
     tf_p_stamp(a, 5 * li, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<true, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, li, 0, blockIdx.x == 0));
+    tf_p_stage8b<true, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec<REC>(a, li, 0, blockIdx.x == 0));
     tf_p_stamp(a, 5 * li, 2);
     if (wave == 0) return true;
     const TfPQkvGeo g = tf_p_qkv_geo<SPR>(a);
@@ -2017,7 +2020,7 @@ __device__ __forceinline__ void tf_p_gu_warm(TfPA& a, TfPL& L, int n_active) {
     }
 }
 
-template <bool MM>
+template <bool MM, bool REC>
 __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, int pos) {
     uint8_t* lds = tf_p_lds;
     TfPA& a = *pa;
@@ -2035,7 +2038,7 @@ __device__ __forceinline__ bool tf_p_stage_attn(TfPA* pa, int li, unsigned tb, i
         tf_p_attn_load(L, a.KV * TF_P_HD, g.kh, g.t_begin, g.t_end, pos, ra);
     tf_p_stamp(a, 5 * li + 1, 0);
     __syncthreads();  // the previous stage's LDS readers are done
-    const bool ok = tf_p_attn_run<MM>(
+    const bool ok = tf_p_attn_run<MM, REC>(
         a, L, g, pos, ra, lds, tf_p_vec(a, TF_PK_Q, li), tf_p_vec(a, TF_PK_KV, li),
         tf_p_tag(tb, li, TF_PK_Q), tf_p_tag(tb, li, TF_PK_KV), tf_p_vec(a, TF_PK_O, li),
         tf_p_tag(tb, li, TF_PK_O), tf_p_tag(tb, li, TF_PK_PART), 5 * li + 1);
@@ -2081,7 +2084,7 @@ __device__ __forceinline__ bool tf_p_stage_wo(TfPA* pa, int li, unsigned tb, int
     return true;
 }
 
-template <int SPR, int IT>
+template <int SPR, int IT, bool REC>
 __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     using M = TfPGuMap<SPR>;
     constexpr int NS = SPR <= 8 ? 1 : 2;  // staging steps (E <= 2048 NS)
@@ -2113,7 +2116,7 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, li, 2, blockIdx.x == 0));
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec<REC>(a, li, 2, blockIdx.x == 0));
     if (wave == 0) tf_p_stamp(a, 5 * li + 3, 2);
     tf_p_gu_compute<SPR, IT>(a, L, xE, rg, sp, fx, tag_x);
     // wave 0 takes the second half of a group whose first half ends the span
@@ -2121,7 +2124,7 @@ __device__ __forceinline__ bool tf_p_stage_gu(TfPA* pa, int li, unsigned tb) {
     __syncthreads();  // h of every wave in LDS
     if (tf_p_flag) return false;
     if (wave == 0) {
-        tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H), tf_p_q8rec(a, li, 3));
+        tf_p_gu_quantize(sp, fh, tf_p_tag(tb, li, TF_PK_H), tf_p_q8rec<REC>(a, li, 3));
         tf_p_stamp(a, 5 * li + 3, 3);
     }
     return true;
@@ -2167,7 +2170,7 @@ __device__ __forceinline__ bool tf_p_stage_down(TfPA* pa, int li, unsigned tb) {
 // argmax and advances the decode state.
 __shared__ unsigned long long tf_p_key[TF_P_WAVES];
 
-template <int SPR, int IT>
+template <int SPR, int IT, bool REC>
 __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_mode, int pos,
                                              unsigned gen) {
     uint8_t* lds = tf_p_lds;
@@ -2195,7 +2198,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
     tf_p_stamp(a, 5 * L, 1);
     __syncthreads();  // raw row and scale in LDS
     if (tf_p_flag) return false;
-    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec(a, L, 0, blockIdx.x == 0));
+    tf_p_stage8b<false, true, NS>(lds, nbE, raw, tf_p_rms, nw, tf_p_q8rec<REC>(a, L, 0, blockIdx.x == 0));
     tf_p_stamp(a, 5 * L, 2);
     tf_p_rows_ring<SPR, IT, true, D, 1>(a.head, a.head_cb, nbE, a.n_vocab, xE, rh, w0, nwv,
                                         [](int) { return 0.f; }, nullptr, 0u, a.logits, a.amax,
@@ -2242,7 +2245,7 @@ __device__ __forceinline__ bool tf_p_stage_head(TfPA* pa, unsigned tb, int host_
 
 // ------------------------------------------------------------ the kernel
 
-template <int SPR_E, int IT_E, int SPR_F, int IT_F, bool MM>
+template <int SPR_E, int IT_E, int SPR_F, int IT_F, bool MM, bool REC>
 __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     const TfPArgs* args, int host_mode, int token_host, int pos_host) {
     {
@@ -2267,13 +2270,13 @@ __global__ __launch_bounds__(TF_P_THREADS) void tf_decode_persistent_kernel(
     const unsigned tb = gen * (unsigned)(8 * a.n_layer + 8);
     __syncthreads();
     for (int li = 0; li < a.n_layer; li++) {
-        if (!tf_p_stage_qkv<SPR_E, IT_E>(&a, li, tb, pos, token)) return;
-        if (!tf_p_stage_attn<MM>(&a, li, tb, pos)) return;
+        if (!tf_p_stage_qkv<SPR_E, IT_E, REC>(&a, li, tb, pos, token)) return;
+        if (!tf_p_stage_attn<MM, REC>(&a, li, tb, pos)) return;
         if (!tf_p_stage_wo<SPR_E, IT_E>(&a, li, tb, token)) return;
-        if (!tf_p_stage_gu<SPR_E, IT_E>(&a, li, tb)) return;
+        if (!tf_p_stage_gu<SPR_E, IT_E, REC>(&a, li, tb)) return;
         if (!tf_p_stage_down<SPR_F, IT_F>(&a, li, tb)) return;
     }
-    tf_p_stage_head<SPR_E, IT_E>(&a, tb, host_mode, pos, gen);
+    tf_p_stage_head<SPR_E, IT_E, REC>(&a, tb, host_mode, pos, gen);
     tf_p_trace_flush(a);
 }
 
@@ -2298,10 +2301,10 @@ struct TfPLaunch {
     int host_mode, token, pos;
 };
 
-template <int SE, int IE, int SF, int IF, bool MM>
+template <int SE, int IE, int SF, int IF, bool MM, bool REC>
 int tf_p_launch_t(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid_out,
                   int* lds_out) {
-    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, MM>;
+    auto kern = tf_decode_persistent_kernel<SE, IE, SF, IF, MM, REC>;
     const int lds = MM && tf_p_lds(a) < TfPDmaLayout::BYTES ? TfPDmaLayout::BYTES : tf_p_lds(a);
     // the dynamic LDS limit of this instantiation, raised per device to the
     // largest size a model has needed so far
@@ -2350,11 +2353,17 @@ int tf_p_dispatch(int E, int F_, int H, int KV, int HD, F&& f) {
 
 // MM: the instantiation whose attention runs long contexts on the matrix
 // cores (its extra registers would cost the short-context step ~2%).
+// REC: the instantiation that keeps the Q8 record (TfPArgs::q8x set).
+template <int V, bool MM, bool REC>
+int tf_p_call_r(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid, int* lds) {
+    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1, MM, REC>(a, l, s, grid, lds);
+    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3, MM, REC>(a, l, s, grid, lds);
+    else return tf_p_launch_t<16, 1, 16, 5, MM, REC>(a, l, s, grid, lds);
+}
 template <int V, bool MM>
 int tf_p_call(const TfPArgs& a, const TfPLaunch* l, hipStream_t s, int* grid, int* lds) {
-    if constexpr (V == 0) return tf_p_launch_t<4, 1, 4, 1, MM>(a, l, s, grid, lds);
-    else if constexpr (V == 1) return tf_p_launch_t<8, 1, 16, 3, MM>(a, l, s, grid, lds);
-    else return tf_p_launch_t<16, 1, 16, 5, MM>(a, l, s, grid, lds);
+    return a.q8x ? tf_p_call_r<V, MM, true>(a, l, s, grid, lds)
+                 : tf_p_call_r<V, MM, false>(a, l, s, grid, lds);
 }
 
 }  // namespace
