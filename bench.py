@@ -36,13 +36,29 @@ sys.path.insert(0, str(ROOT))
 
 # The dominant kernel of the timed workload: the persistent decode step (one
 # launch per token, 99% of the GPU time in the kernel trace).
-DECODE_KERNEL = "tf_decode_persistent_kernel<8,1,16,3> (whole decode step, one launch per token)"
+DECODE_KERNEL = ("tf_decode_persistent_kernel<8,1,16,3,false,false> (whole decode step, one "
+                 "launch per token)")
 # Its HBM bytes per launch: rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per
 # dispatch, timed dispatches of `bench.py --only-decode --steps 64 --warmup 4`)
 # scaled by the same counters' reading on a 256 MiB device copy (FETCH_SIZE
 # counts half of what a read moves here: factor 2.000; WRITE_SIZE factor
-# 1.000); the counter runs are kept in profiles/.
-DECODE_TRAFFIC = int((1051398.3 * 2.0 + 24014.9 * 1.0) * 1024)
+# 1.000); the counter runs are kept in profiles/.  The figure belongs to the
+# kernel source it was measured on (DECODE_TRAFFIC_SRC, the first 16 hex
+# digits of the SHA-256 of decode_persistent.hip + .hpp); a run on other
+# source reports traffic null rather than a stale number.
+DECODE_TRAFFIC = int((1051380.4 * 2.0 + 24012.2 * 1.0) * 1024)
+DECODE_TRAFFIC_SRC = "899142eca4a72949"
+
+
+def _decode_src_hash() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in ("decode_persistent.hip", "decode_persistent.hpp"):
+        h.update((ROOT / "taraference_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 # The standalone config-1a GEMV (the tf_gemv_q4k_ffn entry point), reported
 # beside it for the metric's "Q4_K GEMV % of HBM peak" part.
 ROOFLINE_KERNEL = "tf_q4k_pair_rows_kernel<8,1,0> (fused Q4_K gate+up+SiLU, 2048 -> 2x11008)"
@@ -592,7 +608,8 @@ def main():
     step_gbs = step_bytes / (us_step * 1e-6) / 1e9
     roof = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-            "traffic": DECODE_TRAFFIC if path == 4 else None,
+            "traffic": (DECODE_TRAFFIC if path == 4 and _decode_src_hash() == DECODE_TRAFFIC_SRC
+                        else None),
             "kernel": DECODE_KERNEL if path == 4 else f"decode step, path {path} (several kernels)",
             "bytes_per_launch": step_bytes, "us_per_launch": round(us_step, 2)}
     out = {
