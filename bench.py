@@ -74,13 +74,17 @@ def log(*a):
 
 
 def build_model(cfg, seed, max_seq):
+    """Random-init weights of the config's shape, drawn from the
+    well-conditioned block distribution (synth.q4k_blocks_wc /
+    q6k_blocks_wc), so the greedy tokens vary from step to step; the bytes
+    per token are those of any Q4_K_M model of the shape."""
     from taraference_amd import synth
     from taraference_amd.model import DecodeModel
 
     rng = np.random.default_rng(seed)
     t0 = time.time()
-    layers = (synth.qwen_layer(rng, cfg, li) for li in range(cfg["n_layer"]))
-    emb = synth.qwen_embedding(rng, cfg)
+    layers = (synth.qwen_layer(rng, cfg, li, wc=True) for li in range(cfg["n_layer"]))
+    emb = synth.qwen_embedding(rng, cfg, wc=True)
     m = DecodeModel(dict(cfg, max_seq=max_seq), layers, emb)
     log(f"[bench] model built in {time.time() - t0:.1f}s")
     return m

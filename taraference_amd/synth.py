@@ -196,7 +196,7 @@ def qwen_layer(rng, cfg: dict, layer: int, wc: bool = False) -> dict:
     Q4_K for q/k/o/gate/up, Q6_K for v, Q6_K or Q4_K for down; norms = 1,
     q/k/v biases ~ N(0, 0.02).  wc: well-conditioned blocks (activations,
     attention scores and logits of order 1, so the softmax is not one-hot)
-    instead of the benchmark's block distribution."""
+    instead of the plain random block distribution (the bench draws wc)."""
     e, f = cfg["n_embd"], cfg["n_ff"]
     nq = cfg["n_head"] * cfg["head_dim"]
     nkv = cfg["n_kv"] * cfg["head_dim"]
