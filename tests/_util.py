@@ -167,14 +167,14 @@ def assert_gemv_close(y, y_ref, rowabs, what=""):
 
 
 def silu64(g):
-    return g / (1.0 + np.exp(-g))
+    return g * np.exp(-np.logaddexp(0.0, -g))  # g / (1 + e^-g) without overflow
 
 
 def assert_ffn_close(h, g64, ga, u64, ua, what="ffn"):
     """h = silu(g) * u with g, u carrying the GEMV tolerance; first-order
     propagation of 1e-5 relative errors in g, u, plus 1e-5 relative for the
     SiLU evaluation itself."""
-    sig = 1.0 / (1.0 + np.exp(-g64))
+    sig = np.exp(-np.logaddexp(0.0, -g64))  # 1 / (1 + e^-g) without overflow
     dsilu = sig * (1.0 + g64 * (1.0 - sig))
     ref = silu64(g64) * u64
     sg = np.maximum(np.abs(g64), CANCEL_FLOOR * ga)
