@@ -455,7 +455,8 @@ struct tf_model {
         p_flags = alloc<unsigned long long>(p_flag_words);
         p_part_words = (size_t)c.n_head * TF_P_MAX_SPLIT * (2 + c.head_dim);
         if (p_keep) {
-            p_q8n = std::max({c.n_embd, c.n_ff, c.n_head * c.head_dim});
+            // a whole number of 32-value groups per record (the scales index off / 32)
+            p_q8n = (std::max({c.n_embd, c.n_ff, c.n_head * c.head_dim}) + 31) & ~31;
             const size_t n = ((size_t)c.n_layer + 1) * 4 * (size_t)p_q8n;
             p_q8x = alloc<float>(n);
             p_q8q = alloc<int8_t>(n);
