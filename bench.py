@@ -46,8 +46,8 @@ DECODE_KERNEL = ("tf_decode_persistent_kernel<8,1,16,3,false,false> (whole decod
 # kernel source it was measured on (DECODE_TRAFFIC_SRC, the first 16 hex
 # digits of the SHA-256 of decode_persistent.hip + .hpp); a run on other
 # source reports traffic null rather than a stale number.
-DECODE_TRAFFIC = int((1051380.4 * 2.0 + 24012.2 * 1.0) * 1024)
-DECODE_TRAFFIC_SRC = "899142eca4a72949"
+DECODE_TRAFFIC = int((1013669.6 * 2.0 + 24008.8 * 1.0) * 1024)
+DECODE_TRAFFIC_SRC = "b52ba0cdb9b34fd8"
 
 
 def _decode_src_hash() -> str:

@@ -1980,12 +1980,21 @@ __device__ __forceinline__ bool tf_p_stage_qkv(TfPA* pa, int li, unsigned tb, in
 // 2.0 us gave 1019 / 1028 / 1025 / 1022 / 1007 / 980 tok/s), and each wave
 // keeps at most 2 TF_P_WARM copies in flight.  Only when the XCD's share fits
 // the L2 with room to spare (gate + up at most 28 MB).  Their own wo poll,
-// about 5 us later, finds the copies drained.
+// about 5 us later, finds the copies drained.  Only the first TF_P_WARM_PCT %
+// of each workgroup's gate and up runs are warmed: with all of them the L2
+// evicted about 2.3 MB per layer before the gate/up stage read it (read twice
+// from HBM); 100 / 85 / 70 / 60 / 50 / 40 % gave 1027 / 1031 / 1031 / 1029 /
+// 1028 / 1017 tok/s and FETCH_SIZE 1,050,687 / 1,021,159 / 1,013,650 /
+// 1,012,876 / 1,012,766 / 1,012,892 KiB per launch (warming the last 85 %
+// instead of the first: 1016 tok/s).
 #ifndef TF_P_WARM
 #define TF_P_WARM 4
 #endif
 #ifndef TF_P_WARM_DELAY
 #define TF_P_WARM_DELAY 80
+#endif
+#ifndef TF_P_WARM_PCT
+#define TF_P_WARM_PCT 70
 #endif
 // scratch above every activation image; it overlaps the short-split attention
 // area, which the warming workgroups (those without attention work) do not use
@@ -2010,7 +2019,9 @@ __device__ __forceinline__ void tf_p_gu_warm(TfPA& a, TfPL& L, int n_active) {
         // the gate/up span of workgroup x + 8 jj (tf_p_gu_span)
         const int bb = x + 8 * jj;
         const int s0 = (int)((long long)nh * bb / G), e0 = (int)((long long)nh * (bb + 1) / G);
-        const size_t pieces = ((size_t)16 * (e0 - s0) * cb + 1023) / 1024;
+        // the first TF_P_WARM_PCT % of each of its gate and up runs
+        const size_t pieces =
+            ((size_t)16 * (e0 - s0) * cb + 1023) / 1024 * TF_P_WARM_PCT / 100;
         for (size_t pc = wave; pc < 2 * pieces; pc += TF_P_WAVES) {
             const int m = pc >= pieces ? 1 : 0;
             const size_t off = (size_t)16 * s0 * cb + (pc - m * pieces) * 1024 + 16 * lane;
