@@ -349,14 +349,10 @@ static bool tf_q6c_weights_ok(const uint8_t* w, int nb, int col_bytes) {
 }
 
 // The LDS-fed kernel serves wide matrices with K = 1024 or 2048, 16-byte
-// aligned rows of exactly nb compact blocks, a Q8 activation and a plain output (TF_Q6K_DMA=0 turns it off for comparisons).
+// aligned rows of exactly nb compact blocks, a Q8 activation and a plain output.
 static bool tf_q6k_dma_ok(const uint8_t* w, int nb, int n_cols, int col_bytes, int use_bias,
                           int use_res) {
-    static const bool on = [] {
-        const char* e = getenv("TF_Q6K_DMA");
-        return !(e && e[0] == '0');
-    }();
-    return on && (nb == 8 || nb == 4) && col_bytes == nb * 212 && ((uintptr_t)w & 15) == 0 &&
+    return (nb == 8 || nb == 4) && col_bytes == nb * 212 && ((uintptr_t)w & 15) == 0 &&
            n_cols >= 65536 && !use_bias && use_res == 0;
 }
 

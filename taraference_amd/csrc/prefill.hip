@@ -1178,15 +1178,6 @@ __global__ __launch_bounds__(256) void tf_gemm_split_reduce_kernel(const float* 
 
 // ---------------------------------------------------------------- C ABI
 
-// TF_GEMM_BF16=1 selects the three-part bf16 Q4_K kernel (A/B measurements).
-static bool tf_gemm_bf16_q4k() {
-    static const bool on = [] {
-        const char* e = getenv("TF_GEMM_BF16");
-        return e && e[0] == '1';
-    }();
-    return on;
-}
-
 int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows, int n_cols,
                int col_bytes, int n_tok, int accumulate, tf_stream_t stream, float* ws,
                size_t ws_floats) {
@@ -1207,16 +1198,12 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
     // them XCD by XCD; the padding exits at once)
     dim3 grid((unsigned)(8 * ((tiles + 7) / 8)), 1);
     // Split-K when the tile grid leaves the chip short of workgroups: about
-    // 512 workgroups in all (TF_GEMM_SPLIT_TARGET overrides; measured on the
-    // 3B prefill against 384, 768, 1024 and 1536), partial slices into ws,
-    // then a fixed-order sum.
+    // 512 workgroups in all (measured on the 3B prefill against 384, 768, 1024
+    // and 1536), partial slices into ws, then a fixed-order sum.
     const size_t slice = (size_t)n_tok * n_cols;
     int n_split = 1;
     if (ws && tiles < 384 && (n_cols & 3) == 0 && ((uintptr_t)ws & 15) == 0) {
-        static const int target = [] {
-            const char* e = getenv("TF_GEMM_SPLIT_TARGET");
-            return e && atoi(e) > 0 ? atoi(e) : 512;
-        }();
+        constexpr int target = 512;
         n_split = (int)((target + tiles - 1) / tiles);
         if (n_split > nb) n_split = nb;
         while (n_split > 1 && (size_t)n_split * slice > ws_floats) n_split--;
@@ -1226,9 +1213,6 @@ int tf_gemm_kq(bool q6, const uint8_t* w, const float* x, float* out, int n_rows
     const int acc = n_split > 1 ? 0 : accumulate;
     if (q6)
         hipLaunchKernelGGL(tf_gemm_kq_kernel<true>, grid, dim3(256), 0, tf_stream(stream), w, x,
-                           dst, n_rows, n_cols, col_bytes, n_tok, acc, n_split, (long long)slice);
-    else if (tf_gemm_bf16_q4k())
-        hipLaunchKernelGGL(tf_gemm_kq_kernel<false>, grid, dim3(256), 0, tf_stream(stream), w, x,
                            dst, n_rows, n_cols, col_bytes, n_tok, acc, n_split, (long long)slice);
     else
         hipLaunchKernelGGL(tf_gemm_q4k_h_kernel, grid, dim3(256), 0, tf_stream(stream), w, x,
@@ -1251,15 +1235,6 @@ extern "C" int tf_gemm_q6k_f32(const uint8_t* w, const float* x, float* out, int
     return tf_gemm_kq(true, w, x, out, n_rows, n_cols, col_bytes, n_tok, 0, stream, nullptr, 0);
 }
 
-// TF_ATTN_PREFILL_VALU=1 selects the vector-ALU attention for head_dim 128.
-static bool tf_attn_prefill_valu() {
-    static const bool on = [] {
-        const char* e = getenv("TF_ATTN_PREFILL_VALU");
-        return e && e[0] == '1';
-    }();
-    return on;
-}
-
 int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                float* out, int n_head, int n_kv, int head_dim, int pos0,
                                const int* pos0_dev, int n_q, float scale, tf_stream_t stream) {
@@ -1274,12 +1249,11 @@ int tf_attn_prefill_any(const float* q, const uint16_t* k_cache, const uint16_t*
                            n_head, n_kv, pos0, pos0_dev, n_q, scale);
     };
     if (head_dim == 64) go(tf_attn_prefill_kernel<64>);
-    else if (head_dim == 128 && !tf_attn_prefill_valu()) {
+    else if (head_dim == 128) {
         const dim3 g16((n_q + 15) / 16, n_head);
         hipLaunchKernelGGL(tf_attn_prefill_mfma_kernel, g16, dim3(256), 0, tf_stream(stream), q,
                            k_cache, v_cache, out, n_head, n_kv, pos0, pos0_dev, n_q, scale);
-    } else if (head_dim == 128) go(tf_attn_prefill_kernel<128>);
-    else go(tf_attn_prefill_kernel<256>);
+    } else go(tf_attn_prefill_kernel<256>);
     return TF_LAUNCH_RESULT();
 }
 
