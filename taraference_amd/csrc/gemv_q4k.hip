@@ -109,6 +109,44 @@ __global__ __launch_bounds__(tf_bt_rows(SPR, SK)) void tf_q4k_rows_kernel(
     }
 }
 
+// Narrow rows (at most eight super-blocks) with a Q8 activation: the lanes
+// read the activation bytes from global memory right behind their weight
+// loads instead of staging an LDS image first (no staging round trip, no
+// barrier); arithmetic as tf_q4k_rows_kernel.
+template <int SPR, int ITERS>
+__global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q4k_rows_gq8_kernel(
+    TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
+    int col_bytes, int use_bias, int use_res, const float* __restrict__ residual) {
+    constexpr int UNITS = 16 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int t = lane & 3, slot = lane >> 2, unit = slot / SPR, sir = slot % SPR;
+    const int wave = tf_wave_id();
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int n_total = m.n0 + m.n1 + m.n2;
+    const int n_tasks = (n_total + UNITS - 1) / UNITS;
+    int task = wave;
+    TfRowSel cs = tf_sel3(m, task * UNITS + unit, n_total, col_bytes);
+    TfQ4kRow<ITERS> cur, nxt;
+    if (task < n_tasks) tf_q4k_row_load_u<SPR, ITERS>(cs.col, nb, sir, t, cur);
+    for (; task < n_tasks; task += nwaves) {
+        const int nt = task + nwaves;
+        const TfRowSel ns = tf_sel3(m, nt * UNITS + unit, n_total, col_bytes);
+        if (nt < n_tasks) tf_q4k_row_load_u<SPR, ITERS>(ns.col, nb, sir, t, nxt);
+        float acc = tf_q4k_row_partial_g<SPR, ITERS>(cur, cs.valid, nb, sir, t, xq, xd);
+        acc = tf_group_sum<4 * SPR>(acc);
+        if (cs.valid && (lane & (4 * SPR - 1)) == 0) {
+            const int j = cs.j, mi = cs.mi;
+            float* out = mi == 0 ? m.o0 : (mi == 1 ? m.o1 : m.o2);
+            if (use_res == 1) acc += residual[j];
+            else if (use_res == 2) acc += out[j];
+            if (use_bias) acc += (mi == 0 ? m.b0 : (mi == 1 ? m.b1 : m.b2))[j];
+            out[j] = acc;
+        }
+        cur = nxt;
+        cs = ns;
+    }
+}
+
 template <int MODE>
 __device__ __forceinline__ void tf_pair_write(float g, float u, float* out_a, float* out_b,
                                               int j) {
@@ -325,6 +363,21 @@ static int tf_q4k_rows(const TfQ4kMats& m, const TfActSrc& src, int n_rows, int 
     const int n_total = m.n0 + m.n1 + m.n2;
     const int lds = tf_act_lds_bytes(nb, false);
     int rc = 0;
+    if (src.kind == TF_SRC_Q8 && nb <= 8 && ((uintptr_t)src.xq & 15) == 0 &&
+        ((uintptr_t)src.xd & 7) == 0) {
+        // the lane map of tf_q4k_dispatch for nb <= 8: one part per lane
+        auto go = [&](auto spr) {
+            constexpr int SPR = decltype(spr)::value;
+            auto fn = tf_q4k_rows_gq8_kernel<SPR, 1>;
+            const int tasks = (n_total + 16 / SPR - 1) / (16 / SPR);
+            const int BT = tf_block_threads(tf_bt_rows(SPR), tasks);
+            const int blocks = tf_persistent_blocks((const void*)fn, BT, 0, tasks);
+            hipLaunchKernelGGL(fn, dim3(blocks), dim3(BT), 0, tf_stream(stream), m, src.xq,
+                               src.xd, nb, col_bytes, use_bias, use_res, residual);
+            return (int)TF_LAUNCH_RESULT();
+        };
+        return nb <= 4 ? go(tf_ic<4>{}) : go(tf_ic<8>{});
+    }
     tf_q4k_dispatch(nb, [&](auto spr, auto it) {
         constexpr int SPR = decltype(spr)::value, IT = decltype(it)::value;
         auto fn = tf_sk_pick(src.kind, tf_q4k_rows_kernel<SPR, IT, TF_SRC_Q8>,

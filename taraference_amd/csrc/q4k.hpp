@@ -87,21 +87,60 @@ __device__ __forceinline__ void tf_q4k_idots(const TfQ4kPart& p, const int8_t* q
     tf_q4k_idots_r(p, qv[0], qv[1], qv[2], qv[3], dlo, dhi);
 }
 
+// The fp32 contribution from the exact integer sums dlo, dhi, the two
+// groups' Q8 scales d8 and their d8 * sum(q8) ds.
+__device__ __forceinline__ float tf_q4k_part_fp(const TfQ4kPart& p, int t, int dlo, int dhi,
+                                                float2 d8, float2 ds) {
+    int sc0, sc1, m0, m1;
+    tf_q4k_scales(p.h, t, sc0, sc1, m0, m1);
+    const float d = tf_h2f(p.h.x);
+    const float dmin = tf_h2f(p.h.x >> 16);
+    const float scale_term = d8.x * (float)(dlo * sc0) + d8.y * (float)(dhi * sc1);
+    const float min_term = (float)m0 * ds.x + (float)m1 * ds.y;
+    return d * scale_term - dmin * min_term;
+}
+
 // fp32 contribution of this lane's two sub-blocks of super-block sb.
 __device__ __forceinline__ float tf_q4k_part_dot(const TfQ4kPart& p, int t, int sb,
                                                  const TfQ8Lds& x) {
     int dlo, dhi;
     tf_q4k_idots(p, x.q8 + tf_q8_pad(sb * 256 + 64 * t), dlo, dhi);
-    int sc0, sc1, m0, m1;
-    tf_q4k_scales(p.h, t, sc0, sc1, m0, m1);
-    const float d = tf_h2f(p.h.x);
-    const float dmin = tf_h2f(p.h.x >> 16);
     const int g = sb * 8 + 2 * t;
-    const float2 d8 = *reinterpret_cast<const float2*>(x.d8 + g);
-    const float2 ds = *reinterpret_cast<const float2*>(x.ds + g);
-    const float scale_term = d8.x * (float)(dlo * sc0) + d8.y * (float)(dhi * sc1);
-    const float min_term = (float)m0 * ds.x + (float)m1 * ds.y;
-    return d * scale_term - dmin * min_term;
+    return tf_q4k_part_fp(p, t, dlo, dhi, *reinterpret_cast<const float2*>(x.d8 + g),
+                          *reinterpret_cast<const float2*>(x.ds + g));
+}
+
+// The same reading the Q8 activation from global memory (xq 16-byte
+// aligned): the 64 bytes of groups 2t, 2t+1, their scales, and the group
+// sums formed here as the staging forms them (ds = d8 * (float)sum).
+__device__ __forceinline__ float tf_q4k_part_dot_g(const TfQ4kPart& p, int t, int sb,
+                                                   const int8_t* __restrict__ xq,
+                                                   const float* __restrict__ xd) {
+    const int8_t* q = xq + sb * 256 + 64 * t;
+    const tf_u32x4 u0 = tf_ld16(q), u1 = tf_ld16(q + 16), w0 = tf_ld16(q + 32),
+                   w1 = tf_ld16(q + 48);
+    const int g = sb * 8 + 2 * t;
+    const float2 d8 = *reinterpret_cast<const float2*>(xd + g);
+    int dlo, dhi;
+    tf_q4k_idots_r(p, u0, u1, w0, w1, dlo, dhi);
+    const int one = 0x01010101;
+    int s0 = tf_dot4(one, (int)u0.x, 0);
+    s0 = tf_dot4(one, (int)u0.y, s0);
+    s0 = tf_dot4(one, (int)u0.z, s0);
+    s0 = tf_dot4(one, (int)u0.w, s0);
+    s0 = tf_dot4(one, (int)u1.x, s0);
+    s0 = tf_dot4(one, (int)u1.y, s0);
+    s0 = tf_dot4(one, (int)u1.z, s0);
+    s0 = tf_dot4(one, (int)u1.w, s0);
+    int s1 = tf_dot4(one, (int)w0.x, 0);
+    s1 = tf_dot4(one, (int)w0.y, s1);
+    s1 = tf_dot4(one, (int)w0.z, s1);
+    s1 = tf_dot4(one, (int)w0.w, s1);
+    s1 = tf_dot4(one, (int)w1.x, s1);
+    s1 = tf_dot4(one, (int)w1.y, s1);
+    s1 = tf_dot4(one, (int)w1.z, s1);
+    s1 = tf_dot4(one, (int)w1.w, s1);
+    return tf_q4k_part_fp(p, t, dlo, dhi, d8, make_float2(d8.x * (float)s0, d8.y * (float)s1));
 }
 
 // Row dot split into a load phase and a compute phase so that kernels can
@@ -148,6 +187,20 @@ __device__ __forceinline__ float tf_q4k_row_partial(const TfQ4kRow<ITERS>& r, bo
     for (int i = 0; i < ITERS; i++) {
         const int sb = sb0 + sir + i * SPR;
         if (valid && sb < sb1) acc += tf_q4k_part_dot(r.p[i], t, sb, x);
+    }
+    return acc;
+}
+
+template <int SPR, int ITERS>
+__device__ __forceinline__ float tf_q4k_row_partial_g(const TfQ4kRow<ITERS>& r, bool valid,
+                                                      int nb, int sir, int t,
+                                                      const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ xd) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int sb = sir + i * SPR;
+        if (valid && sb < nb) acc += tf_q4k_part_dot_g(r.p[i], t, sb, xq, xd);
     }
     return acc;
 }
