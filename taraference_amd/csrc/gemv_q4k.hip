@@ -112,7 +112,11 @@ __global__ __launch_bounds__(tf_bt_rows(SPR, SK)) void tf_q4k_rows_kernel(
 // Narrow rows (at most eight super-blocks) with a Q8 activation: the lanes
 // read the activation bytes from global memory right behind their weight
 // loads instead of staging an LDS image first (no staging round trip, no
-// barrier); arithmetic as tf_q4k_rows_kernel.
+// barrier); arithmetic as tf_q4k_rows_kernel.  It pays where a wave has one
+// or two tasks (config 0: 3.72 -> 3.25 us, config 1c: 4.05 -> 3.57 us back to
+// back); the fused gate+up at 2048 -> 2 x 11008, five or six tasks per wave,
+// went 7.23 -> 8.84 us with it (every task re-reads the activation through
+// the memory queue its weight prefetch is in), so the pair keeps the image.
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q4k_rows_gq8_kernel(
     TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
