@@ -116,7 +116,9 @@ __global__ __launch_bounds__(tf_bt_rows(SPR, SK)) void tf_q4k_rows_kernel(
 // or two tasks (config 0: 3.72 -> 3.25 us, config 1c: 4.05 -> 3.57 us back to
 // back); the fused gate+up at 2048 -> 2 x 11008, five or six tasks per wave,
 // went 7.23 -> 8.84 us with it (every task re-reads the activation through
-// the memory queue its weight prefetch is in), so the pair keeps the image.
+// the memory queue its weight prefetch is in), so the pair keeps the image;
+// so does the Q6_K down at K = 11008 (one task per wave, but as many
+// activation bytes per lane as weight bytes: 7.03 -> 7.67 us).
 template <int SPR, int ITERS>
 __global__ __launch_bounds__(tf_bt_rows(SPR)) void tf_q4k_rows_gq8_kernel(
     TfQ4kMats m, const int8_t* __restrict__ xq, const float* __restrict__ xd, int nb,
