@@ -70,6 +70,8 @@ def test_q4k_block_dots_exact(gpu, n_rows, n_cols):
     (3584, 3584, 0, True),    # 7B width
     (18944, 256, 2, True),
     (256, 5, 0, False),       # ragged: fewer rows than one wave pass
+    (1280, 1001, 2, True),    # five super-blocks (8 slots per row), odd row count
+    (512, 3000, 1, False),    # two super-blocks (4 slots per row)
 ])
 def test_q4k_gemv(gpu, n_rows, n_cols, use_res, bias):
     w, cb, x, q8, d8 = q4k_case(n_rows, n_cols, n_rows + n_cols)
@@ -88,6 +90,29 @@ def test_q4k_gemv(gpu, n_rows, n_cols, use_res, bias):
     yo = oracle.gemv_q4k_q8(w, q8, d8, n_rows, n_cols, cb, bias=b, use_res=use_res,
                             residual=r, out=r.copy())
     assert_gemv_close(y, yo.astype(np.float64), absn + extra_abs, "gpu vs oracle fp32")
+
+
+@pytest.mark.parametrize("n_rows,n_cols", [(896, 4864), (2048, 2048), (1280, 77)])
+def test_q4k_gemv_unaligned_activation(gpu, n_rows, n_cols):
+    """Narrow rows (K <= 2048) read a 16-byte aligned Q8 activation straight
+    from global memory; an activation one byte off that alignment is staged
+    through LDS instead.  Both within the GEMV bound of the fp64 truth, and
+    within a few fp32 roundings of each other."""
+    w, cb, x, q8, d8 = q4k_case(n_rows, n_cols, 3 * n_rows + n_cols)
+    wd = dev(w)
+    buf = empty(n_rows + 64, torch.int8)
+    buf[1:1 + n_rows].copy_(dev(q8))
+    xd = dev(d8)
+    outs = []
+    for q in (dev(q8), buf[1:1 + n_rows]):
+        o = empty(n_cols)
+        call("tf_gemv_q4k_q8", P(wd), P(q), P(xd), P(o), n_rows, n_cols, cb, 0, None, 0, None,
+             S())
+        outs.append(host(o))
+    y64, absn = oracle.gemv_q4k_q8_f64(w, q8, d8, n_rows, n_cols, cb)
+    for y in outs:
+        assert_gemv_close(y, y64, absn, "q4k gemv")
+    assert np.abs(outs[0] - outs[1]).max() <= 1e-5 * absn.max()
 
 
 def test_q4k_qkv_and_pair(gpu):
