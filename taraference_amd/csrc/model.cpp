@@ -233,7 +233,10 @@ struct tf_model {
     // The same step with fused kernels: each activation is normalized and
     // quantized once (tf_norm_quant, or the flash reduce for the attention
     // output), QKV + RoPE + KV append run in one GEMV launch, and the head
-    // carries the argmax: nine launches per layer.
+    // carries the argmax: nine launches per layer (path 1).  With `prologue`
+    // (paths 2 and 3) the RMSNorm + Q8 run in the staging of the QKV and
+    // gate/up kernels and the split merge + Q8 in the staging of wo: six
+    // launches per layer with the Q8 down (path 3), five with the f32 down.
     void step_fused(hipStream_t s, int token, int pos, bool device_state, bool prologue,
                     bool q8_down) {
         const tf_model_config& c = cfg;
